@@ -1,0 +1,162 @@
+#!/usr/bin/env python3
+"""Batch-1 int4 greedy decode benchmark on one MI355X.
+
+One "step" = one decoded token = ONE persistent cooperative kernel launch (fl_decode_step) over
+the 40-layer 3B-class synthetic int4 model: all layers, final norm, tied bf16 LM head, greedy
+argmax. Tokens chain on the device (step i reads the token step i-1 wrote), so the timed loop
+has no host synchronisation. Weights are seeded random (no checkpoint exists); the prompt is
+512 seeded-uniform token ids prefilled before timing.
+
+Prints ONE JSON line (the driver's contract) with `roofline` (HBM-bound: algorithmic bytes per
+step / measured step time vs 8 TB/s) and `cpu_baseline` (the reference int4 decode path on the
+host CPU, a bounded sample of the same workload).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def step_bytes(args, packed, T):
+    """Algorithmic HBM bytes of one decode step attending to T keys."""
+    D, NL, NKV, hd = args.dim, args.n_layer, args.n_local_heads, args.head_dim
+    int4 = packed.nbytes_int4()                      # packed weights + scale/zero words
+    lm = args.vocab_size * D * 2                     # tied bf16 LM head
+    norms = (2 * NL + 1) * D * 2
+    emb_row = D * 2
+    kv_read = T * NL * NKV * hd * 2 * 2              # K and V of T keys
+    kv_write = NL * NKV * hd * 2 * 2
+    return int4 + lm + norms + emb_row + kv_read + kv_write
+
+
+def cpu_baseline(args, sd, ctx, steps):
+    from oracle.cpu_int4 import CpuInt4Decoder
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    log(f"cpu baseline: packing int4 weights for the CPU kernel ({ncores} threads)")
+    dec = CpuInt4Decoder(args, sd)
+    dec.setup_caches(ctx + steps + 8, fill_upto=ctx, seed=5)
+    tok = 1
+    for i in range(2):  # warmup
+        tok = dec.step(tok, ctx + i)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        tok = dec.step(tok, ctx + 2 + i)
+    dt = time.perf_counter() - t0
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": ncores, "kind": "port",
+            "sample": f"{steps} greedy int4 decode steps at ctx {ctx} (random KV) of the same "
+                      f"40-layer model via aten::_weight_int4pack_mm_for_cpu; {model}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--ctx", type=int, default=512)
+    ap.add_argument("--config", default="flint-3b")
+    ap.add_argument("--cpu-steps", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {a.gpus} is not supported (batch-1 decode "
+              f"runs on a single MI355X; multi-GPU sharding is design-only).", file=sys.stderr)
+        sys.exit(2)
+
+    from flint_amd.model import Transformer
+    from flint_amd.synth import ModelArgs, synth_weights
+
+    dev = torch.device("cuda:0")
+    args = ModelArgs.from_name(a.config)
+    log(f"synthesising {a.config} weights on the GPU")
+    sd = synth_weights(args, seed=0, device=dev)
+    model = Transformer.from_weights(args, sd, dev)
+    torch.cuda.synchronize()
+    total = a.ctx + a.warmup + a.steps + 8
+    model.setup_caches(1, total)
+    g = torch.Generator().manual_seed(1234)
+    prompt = torch.randint(0, args.vocab_size, (a.ctx,), generator=g, dtype=torch.int32).to(dev)
+    seq = torch.empty(a.ctx + a.warmup + a.steps, dtype=torch.int32, device=dev)
+    seq[:a.ctx] = prompt
+    log(f"prefill {a.ctx} tokens")
+    scratch = torch.empty(1, dtype=torch.int32, device=dev)
+    for i in range(a.ctx - 1):
+        model.decode_step(seq[i:i + 1], i, token_out=scratch)
+    torch.cuda.synchronize()
+    model.check()
+    p0 = a.ctx - 1
+    log(f"warmup {a.warmup} steps")
+    for i in range(a.warmup):
+        model.decode_step(seq[p0 + i:p0 + i + 1], p0 + i, token_out=seq[p0 + i + 1:p0 + i + 2])
+    torch.cuda.synchronize()
+    p1 = p0 + a.warmup
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log(f"timing {a.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(a.steps):
+        model.decode_step(seq[p1 + i:p1 + i + 1], p1 + i, token_out=seq[p1 + i + 1:p1 + i + 2])
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    model.check()
+    ms = ev0.elapsed_time(ev1) / a.steps
+    tok_s = 1000.0 / ms
+    mean_bytes = sum(step_bytes(args, model.packed, p1 + i + 1) for i in range(a.steps)) / a.steps
+    achieved = mean_bytes / (ms * 1e-3) / 1e9
+    log(f"{tok_s:.1f} tok/s, {ms * 1e3:.1f} us/step, {achieved:.0f} GB/s algorithmic "
+        f"(wall {a.steps / wall:.1f} tok/s)")
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(args, sd, a.ctx, a.cpu_steps)
+            log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
+        except Exception as e:  # the GPU figure stands on its own
+            log(f"cpu baseline failed: {e!r}")
+    out = {
+        "metric": "batch-1 decode tok/s + achieved HBM GB/s (MBU) at ctx 512, 1xMI355X",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4w/bf16",
+        "data": "synthetic (seeded random int4 weights, seeded uniform prompt ids)",
+        "config": {"workload": f"{a.config}: 40-layer int4 g128 greedy decode, prompt {a.ctx}, "
+                               f"{a.steps} timed tokens (BASELINE config 2)",
+                   "ctx": a.ctx, "global_batch": 1, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

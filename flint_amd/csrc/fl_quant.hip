@@ -1,0 +1,181 @@
+// int4 group quantisation, bit-exact dequantisation and the standalone M=1 int4 GEMV.
+//
+// Quantisation restates gpt-fast's asymmetric group scheme (reference engine/quantize.py:58-76,
+// :102-128, :131-135): every step is a bf16 tensor op in the reference, so every step here
+// computes in fp32 and rounds to bf16 (RNE) at the same points.
+#include "fl_common.h"
+
+namespace {
+
+constexpr uint32_t kBf16OneEMinus6 = 0x3586u;  // bf16(1e-6): clamp(min=1e-6) on a bf16 tensor
+
+// One thread per packed word (8 elements); 16 consecutive threads form one (row, 128-group).
+__global__ __launch_bounds__(256) void k_quantize(const uint16_t* __restrict__ w,
+                                                  uint32_t* __restrict__ q,
+                                                  uint32_t* __restrict__ sz, int64_t nwords) {
+  const int64_t word = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool valid = word < nwords;
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (valid) v = *reinterpret_cast<const uint4*>(w + word * 8);
+  const uint32_t pk[4] = {v.x, v.y, v.z, v.w};
+  float x[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[2 * j] = bflo(pk[j]);
+    x[2 * j + 1] = bfhi(pk[j]);
+  }
+  float mx = x[0], mn = x[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) {
+    mx = fmaxf(mx, x[e]);
+    mn = fminf(mn, x[e]);
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mn = fminf(mn, __shfl_xor(mn, o, 64));
+  }
+  // get_group_qparams (quantize.py:71-74)
+  float d = rbf(mx - mn);
+  d = fmaxf(d, bf2f(kBf16OneEMinus6));
+  const float scale = rbf(d / 15.0f);
+  const float s8 = rbf(scale * 8.0f);
+  const float zero = rbf(mn + s8);
+  // group_quantize_tensor_from_qparams (quantize.py:116-126)
+  const float minv = rbf(zero - s8);
+  uint32_t word_q = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float t = rbf(x[e] - minv);
+    t = rbf(t / scale);
+    float r = rbf(rintf(t));
+    r = fminf(fmaxf(r, 0.0f), 15.0f);
+    word_q |= ((uint32_t)r) << (4 * e);
+  }
+  if (valid) {
+    q[word] = word_q;
+    if ((word & 15) == 0) sz[word >> 4] = f2bf(scale) | (f2bf(zero) << 16);
+  }
+}
+
+// One thread per packed word: 8 bf16 outputs through the same dq8 the GEMVs use.
+__global__ __launch_bounds__(256) void k_dequant(const uint32_t* __restrict__ q,
+                                                 const uint32_t* __restrict__ sz,
+                                                 uint16_t* __restrict__ out, int64_t nwords) {
+  const int64_t word = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (word >= nwords) return;
+  const uint32_t szw = sz[word >> 4];
+  const float s = bf2f(szw & 0xFFFFu), z = bf2f(szw >> 16);
+  uint32_t d[4];
+  dq8(q[word], s, z, -8.0f * s, d);
+  *reinterpret_cast<uint4*>(out + word * 8) = make_uint4(d[0], d[1], d[2], d[3]);
+}
+
+// M=1 GEMV. A workgroup owns `rows_per_wg` consecutive rows, whose packed words form one
+// contiguous block; its 16-byte chunks (32 elements each) are dealt round-robin over the
+// threads so that every thread gets the same number of chunks and every load is coalesced.
+// Per-chunk partial sums go to LDS and each row is summed there in a fixed order.
+constexpr int kGemvThreads = 256;
+constexpr int kGemvMaxChunks = 8;  // per thread
+
+__global__ __launch_bounds__(kGemvThreads) void k_gemv(const uint32_t* __restrict__ q,
+                                                       const uint32_t* __restrict__ sz,
+                                                       const uint16_t* __restrict__ x,
+                                                       uint16_t* __restrict__ y, int n, int k,
+                                                       int rows_per_wg) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+  float* part = reinterpret_cast<float*>(smem + (size_t)k * 2);
+  const int tid = threadIdx.x;
+  const int r0 = blockIdx.x * rows_per_wg;
+  const int rows = min(rows_per_wg, n - r0);
+  const int cpr = k >> 5;  // chunks per row
+  const int total = rows * cpr;
+  const uint4* wblk = reinterpret_cast<const uint4*>(q + (size_t)r0 * (k >> 3));
+  const uint32_t* sblk = sz + (size_t)r0 * (k >> 7);
+
+  // issue the weight loads first: they do not depend on x
+  uint4 wr[kGemvMaxChunks];
+  uint32_t sr[kGemvMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kGemvMaxChunks; ++i) {
+    const int f = tid + i * kGemvThreads;
+    if (f < total) {
+      wr[i] = wblk[f];
+      sr[i] = sblk[f >> 2];
+    }
+  }
+  for (int i = tid; i < (k >> 3); i += kGemvThreads)
+    reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(x)[i];
+  __syncthreads();
+  int c = tid % cpr;
+  const int step = kGemvThreads % cpr;
+#pragma unroll
+  for (int i = 0; i < kGemvMaxChunks; ++i) {
+    const int f = tid + i * kGemvThreads;
+    if (f < total) {
+      const uint4* x4 = reinterpret_cast<const uint4*>(xs + c * 32);
+      part[f] = chunk_dot(wr[i], sr[i], x4, 0.0f);
+    }
+    c += step;
+    if (c >= cpr) c -= cpr;
+  }
+  __syncthreads();
+  // row reduction: L lanes per row, L = largest power of two <= threads/rows (<= 64)
+  int L = 64;
+  while (L * rows > kGemvThreads) L >>= 1;
+  const int row = tid / L, li = tid % L;
+  float acc = 0.0f;
+  if (row < rows)
+    for (int j = li; j < cpr; j += L) acc += part[row * cpr + j];
+  acc = group_sum(acc, L);
+  if (row < rows && li == 0) y[r0 + row] = (uint16_t)f2bf(acc);
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+int fl_version(void) { return 1; }
+
+int fl_quantize_int4(const uint16_t* w, uint32_t* q, uint32_t* sz, int32_t n, int32_t k,
+                     void* stream) {
+  if (!w || !q || !sz || n <= 0 || k <= 0 || (k % FL_GROUP) != 0) return FL_E_ARG;
+  const int64_t nwords = (int64_t)n * (k / 8);
+  const int64_t blocks = (nwords + 255) / 256;
+  if (blocks > 0x7FFFFFFF) return FL_E_ARG;
+  hipLaunchKernelGGL(k_quantize, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), w, q, sz,
+                     nwords);
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+}
+
+int fl_dequant_int4(const uint32_t* q, const uint32_t* sz, uint16_t* out, int32_t n, int32_t k,
+                    void* stream) {
+  if (!q || !sz || !out || n <= 0 || k <= 0 || (k % FL_GROUP) != 0) return FL_E_ARG;
+  const int64_t nwords = (int64_t)n * (k / 8);
+  const int64_t blocks = (nwords + 255) / 256;
+  if (blocks > 0x7FFFFFFF) return FL_E_ARG;
+  hipLaunchKernelGGL(k_dequant, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), q, sz,
+                     out, nwords);
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+}
+
+int fl_gemv_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint16_t* y, int32_t n,
+                 int32_t k, void* stream) {
+  if (!q || !sz || !x || !y || n <= 0 || k <= 0 || (k % FL_GROUP) != 0 || k > 16384)
+    return FL_E_ARG;
+  const int cpr = k / 32;
+  // rows per workgroup: as many as keep every thread at <= kGemvMaxChunks chunks, at most 16
+  int rows = (kGemvThreads * kGemvMaxChunks) / cpr;
+  if (rows > 8) rows = 8;
+  if (rows < 1) return FL_E_ARG;
+  const int blocks = (n + rows - 1) / rows;
+  const size_t shm = (size_t)k * 2 + (size_t)rows * cpr * 4;
+  hipLaunchKernelGGL(k_gemv, dim3(blocks), dim3(kGemvThreads), shm, as_stream(stream), q, sz, x, y,
+                     n, k, rows);
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+}
+
+}  // extern "C"

@@ -1,0 +1,59 @@
+"""Greedy generation loop over the HIP decode kernel.
+
+Mirrors reference engine/generate.py:57-81,137-206 (prefill / decode_one_token / decode_n_tokens /
+generate) for greedy sampling and chat.py:71-96 (logits_at / pick / respond). Tokens stay on
+the device between steps: step i reads the token step i-1 wrote, so the loop issues launches
+back-to-back with no host synchronisation (gpt-fast's decode loop has none either).
+"""
+import torch
+
+
+def prefill(model, x, input_pos):
+    """Feed prompt tokens x (int32 device [T]) at positions input_pos[0]..; returns the greedy next
+    token (int32 device [1]). Prefill is one decode step per prompt token (reference chat.py:85-86)."""
+    x = x.reshape(-1).to(device=model.device, dtype=torch.int32)
+    p0 = int(input_pos.reshape(-1)[0]) if torch.is_tensor(input_pos) else int(input_pos)
+    out = torch.empty(1, dtype=torch.int32, device=model.device)
+    for i in range(x.numel()):
+        model.decode_step(x[i:i + 1], p0 + i, token_out=out)
+    return out
+
+
+def decode_one_token(model, x, input_pos, logits=None):
+    """(next_token int32 device [1], logits) for one token at input_pos (greedy)."""
+    pos = int(input_pos.reshape(-1)[0]) if torch.is_tensor(input_pos) else int(input_pos)
+    if logits is None:
+        logits = torch.empty(model.config.vocab_size, dtype=torch.float32, device=model.device)
+    out = torch.empty(1, dtype=torch.int32, device=model.device)
+    model.decode_step(x.reshape(-1)[:1].to(torch.int32), pos, token_out=out, logits=logits)
+    return out, logits
+
+
+def decode_n_tokens(model, cur_token, input_pos, num_new_tokens, out=None):
+    """Greedy-decode num_new_tokens tokens after cur_token (int32 device [1]) at input_pos.
+    Returns int32 device [num_new_tokens]; no host synchronisation inside the loop."""
+    pos = int(input_pos.reshape(-1)[0]) if torch.is_tensor(input_pos) else int(input_pos)
+    buf = torch.empty(num_new_tokens + 1, dtype=torch.int32, device=model.device)
+    buf[:1] = cur_token.reshape(-1)[:1]
+    for i in range(num_new_tokens):
+        model.decode_step(buf[i:i + 1], pos + i, token_out=buf[i + 1:i + 2])
+    if out is not None:
+        out.copy_(buf[1:])
+        return out
+    return buf[1:]
+
+
+@torch.no_grad()
+def generate(model, prompt, max_new_tokens):
+    """Greedy generate: returns int32 device [T + max_new_tokens] = prompt + new tokens."""
+    prompt = prompt.reshape(-1).to(device=model.device, dtype=torch.int32)
+    T = prompt.numel()
+    model.setup_caches(1, T + max_new_tokens)
+    seq = torch.empty(T + max_new_tokens, dtype=torch.int32, device=model.device)
+    seq[:T] = prompt
+    if T > 1:
+        prefill(model, prompt[:-1], 0)
+    # the last prompt token produces the first new token
+    for i in range(max_new_tokens):
+        model.decode_step(seq[T - 1 + i:T + i], T - 1 + i, token_out=seq[T + i:T + i + 1])
+    return seq

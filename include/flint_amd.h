@@ -1,0 +1,131 @@
+/*
+ * flint_amd.h — C ABI of the MI355X (gfx950) batch-1 int4 decode engine.
+ *
+ * Every entry point takes plain device pointers and sizes, is stream-ordered on the
+ * hipStream_t passed as `stream` (NULL = the legacy default stream), allocates nothing
+ * on the decode/verify hot path, and returns an int status: FL_OK (0) or a negative
+ * FL_E* code. Nothing here is thread-safe for a shared fl_state.
+ *
+ * Weight layout (owned by this library; produced by fl_quantize_int4):
+ *   q  : uint32 [N, K/8]    row-major; element k of a row sits in word k/8 at bits 4*(k%8)
+ *   sz : uint32 [N, K/128]  per (row, 128-group): bits 0..15 = scale (bf16),
+ *                           bits 16..31 = zero (bf16)
+ * Values follow gpt-fast's asymmetric group quantisation
+ *   (reference engine/quantize.py:58-76 get_group_qparams, :102-128 quantise),
+ * and dequantise to  bf16( bf16((q-8)*scale) + zero )  (reference engine/quantize.py:138-155).
+ *
+ * bf16 values are passed as uint16_t bit patterns.
+ */
+#ifndef FLINT_AMD_H
+#define FLINT_AMD_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FL_OK = 0,
+  FL_E_ARG = -1,        /* null pointer / bad size / unsupported shape                         */
+  FL_E_POS = -2,        /* pos (+ M) beyond the state's max_seq or the rope table              */
+  FL_E_M = -3,          /* verify width M outside 1..FL_MAX_VERIFY                             */
+  FL_E_LAUNCH = -4,     /* HIP launch failed (e.g. cooperative grid cannot be co-resident)     */
+  FL_E_HIP = -5,        /* other HIP runtime error (allocation, copy)                          */
+  FL_E_TIMEOUT = -6     /* a grid barrier spin limit was hit in an earlier launch (state is bad) */
+};
+
+#define FL_MAX_VERIFY 16
+#define FL_HEAD_DIM 64
+#define FL_GROUP 128
+
+/* Model shape and scalar multipliers. Mirrors reference engine/model.py:20-45 ModelArgs
+ * (head_dim fixed at 64, group size fixed at 128). */
+typedef struct fl_model_desc {
+  int32_t n_layer, dim, n_head, n_kv_head, inter, vocab;
+  float norm_eps, emb_mult, attn_scale, resid_mult, logits_scaling;
+} fl_model_desc;
+
+/* Device pointers to one model's packed weights (caller-owned). Layer-stacked.
+ * QKV rows are stored NEOX-pair-interleaved: packed row 2i / 2i+1 of head h holds
+ *   model row h*64 + i / h*64 + i + 32  (i < 32), heads ordered [q heads | k heads | v heads].
+ * Gate/up rows are interleaved: packed row 2i = w1 row i (gate), 2i+1 = w3 row i (up). */
+typedef struct fl_weights {
+  const uint32_t *wqkv_q, *wqkv_sz;   /* [NL, (NH+2*NKV)*64, D/8], [.., D/128]  */
+  const uint32_t *wo_q, *wo_sz;       /* [NL, D, D/8], [NL, D, D/128]           */
+  const uint32_t *wgu_q, *wgu_sz;     /* [NL, 2F, D/8], [NL, 2F, D/128]         */
+  const uint32_t *wd_q, *wd_sz;       /* [NL, D, F/8], [NL, D, F/128]           */
+  const uint16_t *attn_norm;          /* [NL, D] bf16                            */
+  const uint16_t *ffn_norm;           /* [NL, D] bf16                            */
+  const uint16_t *final_norm;         /* [D] bf16                                */
+  const uint16_t *embed;              /* [V, D] bf16, tied LM head               */
+  const uint16_t *rope;               /* [rope_len, 32, 2] bf16 (cos, sin)       */
+  int32_t rope_len;
+} fl_weights;
+
+typedef struct fl_state fl_state;
+
+/* Library/device information. */
+int fl_version(void);
+int fl_device_info(int32_t* num_cu, int32_t* decode_grid);
+
+/* ---- quantisation / dequantisation / standalone GEMV --------------------------------- */
+
+/* Group-wise int4 quantisation of a bf16 [N,K] matrix (K % 128 == 0).
+ * Replaces reference engine/quantize.py:131-135 group_quantize_tensor (+ :359-364 prepare_...). */
+int fl_quantize_int4(const uint16_t* w, uint32_t* q, uint32_t* sz,
+                     int32_t n, int32_t k, void* stream);
+
+/* Bit-exact dequantisation to bf16 [N,K], the same device routine the GEMVs use.
+ * Replaces reference engine/quantize.py:138-162 group_dequantize_tensor(_from_qparams). */
+int fl_dequant_int4(const uint32_t* q, const uint32_t* sz, uint16_t* out,
+                    int32_t n, int32_t k, void* stream);
+
+/* y[N] = bf16( sum_k x[k] * dq[n,k] ), fp32 accumulation. M=1 int4 GEMV.
+ * Replaces reference engine/quantize.py:517-525 WeightOnlyInt4Linear.forward ->
+ * aten::_weight_int4pack_mm (:370) at M=1, and kernels/int4_gemv.cu:383-424 int4_gemv_v. */
+int fl_gemv_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint16_t* y,
+                 int32_t n, int32_t k, void* stream);
+
+/* Y[M,N] = bf16( X[M,K] . dq[N,K]^T ), M <= FL_MAX_VERIFY, weight read once for all M rows.
+ * Replaces reference kernels/int4_gemv_mk.cu:11-57 gemv_mk<M> and kernels/int4_gemm_tc.cu:12-70. */
+int fl_gemm_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint16_t* y,
+                 int32_t m, int32_t n, int32_t k, void* stream);
+
+/* ---- decode state --------------------------------------------------------------------- */
+
+/* Binds a caller-owned bf16 KV cache (k_cache, v_cache: [NL, NKV, max_seq, 64] each, device)
+ * and allocates all decode/verify scratch once (hipMalloc here, never on the hot path).
+ * Replaces the per-call torch::empty scratch of reference kernels/megakernel_decode.cu:212-223;
+ * the caller-owned cache mirrors reference chat.py:68-69 / engine/model.py:82-98 KVCache. */
+int fl_state_create(const fl_model_desc* desc, int32_t max_seq, uint16_t* k_cache,
+                    uint16_t* v_cache, fl_state** out);
+int fl_state_destroy(fl_state* st);
+/* Zero all scratch counters (not the KV cache). */
+int fl_state_reset(fl_state* st, void* stream);
+/* Last error recorded by a kernel (FL_OK or FL_E_TIMEOUT); synchronises the stream. */
+int fl_state_check(fl_state* st, void* stream);
+
+/* One full decode step in ONE persistent cooperative launch: embedding of *token_in at
+ * position pos, all layers, final norm, LM head, greedy argmax (first index on ties over the
+ * bf16-rounded logits) written to *token_out. logits (fp32 [V], bf16-exact values) and
+ * feat (bf16 [D], post-final-norm hidden) are optional (NULL to skip).
+ * token_in / token_out / logits / feat are device pointers.
+ * Replaces reference kernels/megakernel_decode.cu:204-237 decode_mega_launch and
+ * engine/generate.py:62-66 decode_one_token (greedy). */
+int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, int32_t pos,
+                   int32_t* token_out, float* logits, uint16_t* feat, void* stream);
+
+/* Speculative verify of M tokens in one pass (weights read once for all M):
+ * token m sits at cache slot pos+m, RoPE position pos+depth[m]; it attends to the cache
+ * [0,pos) plus the slots pos+j with amask[m*M+j] != 0. Writes logits [M,V] (fp32, bf16-exact),
+ * argmax per token to tokens_out [M] and feat [M,D] (optional).
+ * tokens, depth, amask, tokens_out, logits, feat are device pointers.
+ * Replaces reference kernels/verify_mega.cu:246-283 verify_mega_launch. */
+int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t m,
+              const int32_t* depth, const uint8_t* amask, int32_t pos,
+              int32_t* tokens_out, float* logits, uint16_t* feat, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FLINT_AMD_H */

@@ -1,0 +1,76 @@
+"""The reference int4 decode path on the host CPU, used as bench.py's timed CPU baseline
+(test infrastructure only; never part of the product).
+
+gpt-fast runs every linear through aten::_weight_int4pack_mm on tinygemm-packed weights
+(reference engine/quantize.py:359-373, 517-525). That CUDA op has no CPU kernel here; its CPU
+counterparts aten::_convert_weight_to_int4pack_for_cpu / aten::_weight_int4pack_mm_for_cpu take
+the same int32 [N, K] values and [K/128, N, 2] bf16 scales_and_zeros. The rest of the step is
+oracle.model (norm, NEOX RoPE, fp32 attention, SwiGLU, tied bf16 LM head, greedy argmax).
+"""
+import torch
+import torch.nn.functional as F
+
+from . import quant
+from .model import attention, freqs_cis, rms_norm, rope_neox
+
+
+class CpuInt4Linear:
+    def __init__(self, w_bf16):
+        q, s, z = quant.group_quantize(w_bf16)
+        self.n = w_bf16.shape[0]
+        self.w = torch.ops.aten._convert_weight_to_int4pack_for_cpu(q.cpu().contiguous(), 8)
+        self.sz = quant.pack_scales_and_zeros(s, z).cpu()
+
+    def __call__(self, x):
+        return torch.ops.aten._weight_int4pack_mm_for_cpu(x, self.w, quant.GROUP, self.sz)
+
+
+class CpuInt4Decoder:
+    """Batch-1 greedy decode on the CPU with int4 linears. `sd` holds bf16 master weights (any
+    device; quantisation runs where they live, the packed weights live on the CPU)."""
+
+    def __init__(self, args, sd):
+        self.args = a = args
+        self.layers = []
+        for l in range(a.n_layer):
+            p = f"layers.{l}."
+            self.layers.append(dict(
+                wqkv=CpuInt4Linear(sd[p + "wqkv"]), wo=CpuInt4Linear(sd[p + "wo"]),
+                w1=CpuInt4Linear(sd[p + "w1"]), w3=CpuInt4Linear(sd[p + "w3"]),
+                w2=CpuInt4Linear(sd[p + "w2"]),
+                attn_norm=sd[p + "attn_norm"].cpu(), ffn_norm=sd[p + "ffn_norm"].cpu()))
+        self.norm = sd["norm"].cpu()
+        self.embed = sd["embed"].cpu()
+        self.table = freqs_cis(a.block_size, a.head_dim, a.rope_base)
+
+    def setup_caches(self, max_seq, fill_upto=0, seed=0):
+        a = self.args
+        shape = (a.n_layer, a.n_local_heads, max_seq, a.head_dim)
+        g = torch.Generator().manual_seed(seed)
+        self.k = torch.zeros(shape, dtype=torch.bfloat16)
+        self.v = torch.zeros(shape, dtype=torch.bfloat16)
+        if fill_upto:
+            self.k[:, :, :fill_upto] = torch.randn(*shape[:2], fill_upto, shape[3], generator=g).to(torch.bfloat16)
+            self.v[:, :, :fill_upto] = torch.randn(*shape[:2], fill_upto, shape[3], generator=g).to(torch.bfloat16)
+
+    def step(self, token, pos):
+        a = self.args
+        hd = a.head_dim
+        x = (self.embed[token] * a.embedding_multiplier).view(1, -1)
+        rows = self.table[pos:pos + 1]
+        valid = torch.ones(pos + 1, dtype=torch.bool)
+        for l, w in enumerate(self.layers):
+            xn = rms_norm(x, w["attn_norm"], a.norm_eps)
+            qkv = w["wqkv"](xn)
+            q, k, v = qkv.split([a.n_head * hd, a.n_local_heads * hd, a.n_local_heads * hd], dim=-1)
+            q = rope_neox(q.view(1, a.n_head, hd), rows)[0]
+            k = rope_neox(k.view(1, a.n_local_heads, hd), rows)[0]
+            self.k[l, :, pos] = k
+            self.v[l, :, pos] = v.view(a.n_local_heads, hd)
+            y = attention(q, self.k[l, :, :pos + 1], self.v[l, :, :pos + 1], valid, a.attn_scale)
+            h = x + w["wo"](y.view(1, -1)) * a.residual_multiplier
+            hn = rms_norm(h, w["ffn_norm"], a.norm_eps)
+            x = h + w["w2"](F.silu(w["w1"](hn)) * w["w3"](hn)) * a.residual_multiplier
+        xn = rms_norm(x, self.norm, a.norm_eps)
+        logits = F.linear(xn, self.embed) / a.logits_scaling
+        return int(torch.argmax(logits[0]))

@@ -1,0 +1,91 @@
+"""GPU parity of the int4 kernels (quantise, dequantise, M=1 GEMV) against the CPU oracle.
+
+Bar: quantised values / scales / zeros and dequantised weights bit-exact; GEMV within the
+fp32-accumulation bound of an fp64 brute force, rounded to bf16.
+"""
+import pytest
+import torch
+
+from tests.helpers import log
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(3584, 2560), (2560, 2560), (16384, 2560), (2560, 8192), (8, 128), (24, 384)]
+
+
+def _weights(n, k, seed, kind="normal"):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(n, k, generator=g) * 0.02)
+    if kind == "edge":
+        w = w.view(n, k // 128, 128)
+        w[0, :] = 0.25                       # constant group -> scale clamp 1e-6
+        w[1 % n, 0] = -1.0                   # outlier
+        w[-1, -1, :64] = 3.0                 # two-valued group
+        w = w.view(n, k)
+    return w.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+def test_quantize_bit_exact(dev, n, k):
+    from flint_amd.quantize import quantize_int4, unpack_q, unpack_sz
+    from oracle import quant
+    for kind in ("normal", "edge"):
+        log(f"quantize n={n} k={k} kind={kind}")
+        w = _weights(n, k, 1, kind)
+        q, sz = quantize_int4(w.to(dev))
+        torch.cuda.synchronize()
+        qo, so, zo = quant.group_quantize(w)
+        assert torch.equal(unpack_q(q).cpu(), qo)
+        s, z = unpack_sz(sz)
+        assert torch.equal(s.cpu().view(torch.int16), so.view(torch.int16))
+        assert torch.equal(z.cpu().view(torch.int16), zo.view(torch.int16))
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+def test_dequant_bit_exact(dev, n, k):
+    from flint_amd.quantize import quantize_int4, dequantize_int4
+    from oracle import quant
+    w = _weights(n, k, 2, "edge")
+    log(f"dequant n={n} k={k}")
+    q, sz = quantize_int4(w.to(dev))
+    dq = dequantize_int4(q, sz).cpu()
+    ref = quant.dq_linear_weight(w)
+    assert torch.equal(dq.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+def test_gemv_vs_fp64(dev, n, k):
+    from flint_amd.quantize import quantize_int4, gemv_int4
+    from oracle import quant
+    w = _weights(n, k, 3)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(k, generator=g).to(torch.bfloat16)
+    log(f"gemv n={n} k={k}")
+    q, sz = quantize_int4(w.to(dev))
+    y = gemv_int4(q, sz, x.to(dev)).cpu()
+    dq = quant.dq_linear_weight(w).double()
+    ref = dq @ x.double()
+    # fp32 accumulation of k products: |err| <= k * 2^-24 * sum|x*w|, plus bf16 output rounding
+    bound = k * 2.0 ** -24 * (dq.abs() @ x.double().abs()) + ref.abs() * 2.0 ** -8 + 1e-30
+    err = (y.double() - ref).abs()
+    assert bool((err <= bound).all()), float((err / bound).max())
+    # rounded results agree with the fp64 reference rounded once except at rare rounding ties
+    mism = (y != ref.float().to(torch.bfloat16)).float().mean().item()
+    log(f"  bf16 mismatch rate vs fp64-rounded: {mism:.2e}")
+    assert mism < 2e-3
+
+
+def test_gemv_matches_oracle_linear(dev):
+    """Same contract as the oracle's F.linear on dequantised weights (the reference linear)."""
+    from flint_amd.quantize import quantize_int4, gemv_int4
+    from oracle import quant
+    n, k = 16384, 2560
+    w = _weights(n, k, 5)
+    x = torch.randn(k, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    q, sz = quantize_int4(w.to(dev))
+    y = gemv_int4(q, sz, x.to(dev)).cpu()
+    ref = torch.nn.functional.linear(x.view(1, -1), quant.dq_linear_weight(w)).view(-1)
+    diff = (y.float() - ref.float()).abs().max().item()
+    mism = (y != ref).float().mean().item()
+    log(f"gemv vs oracle linear: max|diff|={diff:.3e} mismatch={mism:.2e}")
+    assert mism < 2e-3 and diff < 2e-2
