@@ -7,7 +7,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libflint_amd.so")
+LIB_PATH = os.environ.get("FLINT_AMD_LIB", os.path.join(HERE, "libflint_amd.so"))
 
 FL_OK = 0
 ERRORS = {
@@ -26,6 +26,7 @@ GROUP = 128
 EXPORTS = [
     "fl_version", "fl_device_info", "fl_quantize_int4", "fl_dequant_int4", "fl_gemv_int4",
     "fl_gemm_int4", "fl_state_create", "fl_state_destroy", "fl_state_reset", "fl_state_check",
+    "fl_state_profile", "fl_state_buffers",
     "fl_decode_step", "fl_verify",
 ]
 
@@ -80,6 +81,8 @@ def load(path=LIB_PATH):
         "fl_state_destroy": ([vp], i32),
         "fl_state_reset": ([vp, vp], i32),
         "fl_state_check": ([vp, vp], i32),
+        "fl_state_profile": ([vp, vp, i32, vp], i32),
+        "fl_state_buffers": ([vp, vp, vp, vp, vp], i32),
         "fl_decode_step": ([ctypes.POINTER(Weights), vp, vp, i32, vp, vp, vp, vp], i32),
         "fl_verify": ([ctypes.POINTER(Weights), vp, vp, i32, vp, vp, i32, vp, vp, vp, vp], i32),
     }
@@ -112,3 +115,15 @@ def stream_ptr(stream=None):
     import torch
     s = stream if stream is not None else torch.cuda.current_stream()
     return ctypes.c_void_p(s.cuda_stream)
+
+
+def device_view(ptr_value, n, dtype):
+    """torch tensor viewing n elements of device memory owned by the library (diagnostics)."""
+    import torch
+    typestr = {torch.bfloat16: "<u2", torch.int32: "<i4", torch.float32: "<f4"}[dtype]
+
+    class _Arr:
+        __cuda_array_interface__ = {"shape": (n,), "typestr": typestr,
+                                    "data": (int(ptr_value), False), "version": 3}
+    t = torch.as_tensor(_Arr(), device="cuda")
+    return t.view(torch.bfloat16) if dtype == torch.bfloat16 else t

@@ -29,41 +29,158 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 }
 
 // ---- int4 group dequantisation -------------------------------------------------------------
-// One packed word holds 8 consecutive elements, element e at bits 4e. Produces the four
-// packed bf16 pairs (e0,e1) (e2,e3) (e4,e5) (e6,e7) of
-//     dq = bf16( bf16((q - 8) * s) + z )
-// i.e. gpt-fast's group_dequantize_tensor_from_qparams (reference engine/quantize.py:152-154):
-// int32.sub(8).mul(bf16 scale) rounds to bf16, then .add(bf16 zero) rounds to bf16 again.
-// (q-8)*s has at most 12 significant bits, so fma(q, s, -8s) is exact in fp32.
-__device__ __forceinline__ void dq8(uint32_t w, float s, float z, float c8, uint32_t out[4]) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;
-  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const float q0 = (float)((lo >> (8 * b)) & 0xFFu);
-    const float q1 = (float)((hi >> (8 * b)) & 0xFFu);
-    const uint32_t p = pack_bf16x2(__builtin_fmaf(q0, s, c8), __builtin_fmaf(q1, s, c8));
-    out[b] = pack_bf16x2(bflo(p) + z, bfhi(p) + z);
+// Packed word layout (8 consecutive elements e0..e7 of one row): element 2k sits in nibble k and
+// element 2k+1 in nibble k+4 (k = 0..3), i.e. bits 4k and 16+4k. One AND-OR then yields the
+// bf16 pair (128 + q_2k, 128 + q_2k+1) (0x4300 = 128.0, the nibble lands in the mantissa).
+//
+// dq = bf16( bf16((q - 8) * s) + z ) is gpt-fast's group_dequantize_tensor_from_qparams
+// (reference engine/quantize.py:152-154): int32.sub(8).mul(bf16 scale) rounds to bf16, then
+// .add(bf16 zero) rounds to bf16 again. Both fp32 steps run on v_dot2_f32_bf16, whose bf16
+// products are exact in fp32:
+//   (128+q)*s + 0 + (-136*s) = (q-8)*s          exact ((q-8)*s has <= 12 significant bits)
+//   p_bf16*1 + 0 + z          = fp32(p_bf16 + z) one rounding, as torch's fp32 add
+// and v_cvt_pk_bf16_f32 rounds each result to bf16 (RNE). 35 VALU ops per 8 weights.
+struct DqConst {
+  uint32_t s_lo, s_hi;  // bf16 pairs (s, 0) and (0, s)
+  float c;              // -136 * s (exact)
+  float z;
+};
+__device__ __forceinline__ DqConst dq_const(uint32_t szw) {
+  const uint32_t sb = szw & 0xFFFFu;
+  DqConst k;
+  k.s_lo = sb;
+  k.s_hi = sb << 16;
+  k.c = -136.0f * bf2f(sb);
+  k.z = bf2f(szw >> 16);
+  return k;
+}
+
+// Step j (nibbles j and j+4) of four words w0..w3 of one 128-group: o[i] = packed bf16
+// dequantised pair (element 2j, 2j+1) of word i. One asm block so the instruction order is
+// fixed: the three-address (VOP3P) v_dot2_f32_bf16 needs no copy of its shared accumulator, and
+// every value is consumed at least three instructions after it is written (a VOP3P dot reading
+// a VGPR written just before it must be separated from the write; the compiler does not track
+// that across inline asm).
+template <int J>
+__device__ __forceinline__ void dq_step4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                         const DqConst& k, uint32_t magic, uint32_t one_lo,
+                                         uint32_t one_hi, uint32_t (&o)[4]) {
+  uint32_t m0, m1, m2, m3, p00, p01, p10, p11, p20, p21, p30, p31, p0, p1, p2, p3;
+  uint32_t d00, d01, d10, d11, d20, d21, d30, d31;
+  if (J > 0) {
+    asm("v_lshrrev_b32 %0, %4, %0\n\t"
+        "v_lshrrev_b32 %1, %4, %1\n\t"
+        "v_lshrrev_b32 %2, %4, %2\n\t"
+        "v_lshrrev_b32 %3, %4, %3"
+        : "+v"(w0), "+v"(w1), "+v"(w2), "+v"(w3) : "I"(4 * J));
   }
+  asm("s_nop 2\n\t"
+      "v_and_or_b32 %[m0], %[w0], %[mask], %[magic]\n\t"
+      "v_and_or_b32 %[m1], %[w1], %[mask], %[magic]\n\t"
+      "v_and_or_b32 %[m2], %[w2], %[mask], %[magic]\n\t"
+      "v_and_or_b32 %[m3], %[w3], %[mask], %[magic]\n\t"
+      "s_nop 2\n\t"
+      "v_dot2_f32_bf16 %[p00], %[m0], %[slo], %[c]\n\t"
+      "v_dot2_f32_bf16 %[p10], %[m1], %[slo], %[c]\n\t"
+      "v_dot2_f32_bf16 %[p20], %[m2], %[slo], %[c]\n\t"
+      "v_dot2_f32_bf16 %[p30], %[m3], %[slo], %[c]\n\t"
+      "v_dot2_f32_bf16 %[p01], %[m0], %[shi], %[c]\n\t"
+      "v_dot2_f32_bf16 %[p11], %[m1], %[shi], %[c]\n\t"
+      "v_dot2_f32_bf16 %[p21], %[m2], %[shi], %[c]\n\t"
+      "v_dot2_f32_bf16 %[p31], %[m3], %[shi], %[c]\n\t"
+      "v_cvt_pk_bf16_f32 %[p0], %[p00], %[p01]\n\t"
+      "v_cvt_pk_bf16_f32 %[p1], %[p10], %[p11]\n\t"
+      "v_cvt_pk_bf16_f32 %[p2], %[p20], %[p21]\n\t"
+      "v_cvt_pk_bf16_f32 %[p3], %[p30], %[p31]\n\t"
+      "v_dot2_f32_bf16 %[d00], %[p0], %[olo], %[z]\n\t"
+      "v_dot2_f32_bf16 %[d10], %[p1], %[olo], %[z]\n\t"
+      "v_dot2_f32_bf16 %[d20], %[p2], %[olo], %[z]\n\t"
+      "v_dot2_f32_bf16 %[d30], %[p3], %[olo], %[z]\n\t"
+      "v_dot2_f32_bf16 %[d01], %[p0], %[ohi], %[z]\n\t"
+      "v_dot2_f32_bf16 %[d11], %[p1], %[ohi], %[z]\n\t"
+      "v_dot2_f32_bf16 %[d21], %[p2], %[ohi], %[z]\n\t"
+      "v_dot2_f32_bf16 %[d31], %[p3], %[ohi], %[z]\n\t"
+      "v_cvt_pk_bf16_f32 %[o0], %[d00], %[d01]\n\t"
+      "v_cvt_pk_bf16_f32 %[o1], %[d10], %[d11]\n\t"
+      "v_cvt_pk_bf16_f32 %[o2], %[d20], %[d21]\n\t"
+      "v_cvt_pk_bf16_f32 %[o3], %[d30], %[d31]"
+      : [m0] "=&v"(m0), [m1] "=&v"(m1), [m2] "=&v"(m2), [m3] "=&v"(m3),
+        [p00] "=&v"(p00), [p01] "=&v"(p01), [p10] "=&v"(p10), [p11] "=&v"(p11),
+        [p20] "=&v"(p20), [p21] "=&v"(p21), [p30] "=&v"(p30), [p31] "=&v"(p31),
+        [p0] "=&v"(p0), [p1] "=&v"(p1), [p2] "=&v"(p2), [p3] "=&v"(p3),
+        [d00] "=&v"(d00), [d01] "=&v"(d01), [d10] "=&v"(d10), [d11] "=&v"(d11),
+        [d20] "=&v"(d20), [d21] "=&v"(d21), [d30] "=&v"(d30), [d31] "=&v"(d31),
+        [o0] "=&v"(o[0]), [o1] "=&v"(o[1]), [o2] "=&v"(o[2]), [o3] "=&v"(o[3])
+      : [w0] "v"(w0), [w1] "v"(w1), [w2] "v"(w2), [w3] "v"(w3), [mask] "s"(0x000F000Fu),
+        [magic] "v"(magic), [slo] "v"(k.s_lo), [shi] "v"(k.s_hi), [c] "v"(k.c),
+        [olo] "v"(one_lo), [ohi] "v"(one_hi), [z] "v"(k.z));
+}
+
+// Dequantise the four words of a 16-byte chunk (32 elements of one group):
+// d[j][i] = packed pair (element 2j, 2j+1) of word i.
+__device__ __forceinline__ void dq32(const uint4 w, const DqConst& k, uint32_t (&d)[4][4]) {
+  const uint32_t magic = 0x43004300u;  // bf16 pair (128, 128)
+  const uint32_t one_lo = 0x00003F80u, one_hi = 0x3F800000u;  // bf16 pairs (1, 0), (0, 1)
+  dq_step4<0>(w.x, w.y, w.z, w.w, k, magic, one_lo, one_hi, d[0]);
+  dq_step4<1>(w.x, w.y, w.z, w.w, k, magic, one_lo, one_hi, d[1]);
+  dq_step4<2>(w.x, w.y, w.z, w.w, k, magic, one_lo, one_hi, d[2]);
+  dq_step4<3>(w.x, w.y, w.z, w.w, k, magic, one_lo, one_hi, d[3]);
 }
 
 // dot of one 16-byte chunk (32 int4 elements of one 128-group) with 32 bf16 x values
 // (16 packed pairs), accumulated into acc.
 __device__ __forceinline__ float chunk_dot(const uint4 w, uint32_t szw, const uint4* x4, float acc) {
-  const float s = bf2f(szw & 0xFFFFu), z = bf2f(szw >> 16), c8 = -8.0f * s;
-  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  uint32_t d[4][4];
+  dq32(w, dq_const(szw), d);
+  const uint4 x[4] = {x4[0], x4[1], x4[2], x4[3]};
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t d[4];
-    dq8(ws[j], s, z, c8, d);
-    const uint4 xv = x4[j];
-    acc = dot2_bf16(d[0], xv.x, acc);
-    acc = dot2_bf16(d[1], xv.y, acc);
-    acc = dot2_bf16(d[2], xv.z, acc);
-    acc = dot2_bf16(d[3], xv.w, acc);
+  for (int i = 0; i < 4; ++i) {
+    acc = dot2_bf16(d[0][i], x[i].x, acc);
+    acc = dot2_bf16(d[1][i], x[i].y, acc);
+    acc = dot2_bf16(d[2][i], x[i].z, acc);
+    acc = dot2_bf16(d[3][i], x[i].w, acc);
   }
   return acc;
 }
+
+// nibble position of element e (0..7) within its packed word
+__device__ __forceinline__ int nib_pos(int e) { return (e >> 1) + 4 * (e & 1); }
+
+// ---- device-coherent accesses ----------------------------------------------------------------
+// Data exchanged between workgroups inside one launch goes through agent-scope relaxed atomic
+// loads/stores (global_load/store ... sc1: coherent across the 8 XCD L2s) instead of plain
+// accesses plus acquire/release fences, which on gfx950 write back / invalidate a whole L2.
+__device__ __forceinline__ void st_coh_u16(uint16_t* p, uint32_t v) {
+  __hip_atomic_store(p, (uint16_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh_f32(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_coh_u32(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh_f32(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint4 ld_coh_u128(const void* p) {
+  unsigned long long* q = reinterpret_cast<unsigned long long*>(const_cast<void*>(p));
+  const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+}
+__device__ __forceinline__ void st_coh_u64(unsigned long long* p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_coh_u64(const unsigned long long* p) {
+  return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+// wait until every memory operation this wave issued has completed (stores acknowledged at
+// device scope); required before signalling other workgroups.
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ---- wave reductions (wave64) ---------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {

@@ -9,16 +9,22 @@
 //    block of weight rows (one contiguous span of HBM) dealt as 16-byte chunks round-robin over
 //    all 512 threads, so every workgroup streams the same number of bytes with fully coalesced
 //    loads; per-chunk partials are summed per row in LDS in a fixed order (deterministic);
-//  * the next phase's weight chunks are loaded into registers BEFORE the grid barrier, so the
-//    HBM stream overlaps the barrier latency and the epilogue;
-//  * RMSNorm is recomputed by every workgroup from the residual (no barrier of its own);
-//    RoPE + KV append are fused into the QKV epilogue (NEOX pairs live in adjacent packed rows);
-//    SwiGLU is fused into the gate/up epilogue (gate/up rows interleaved); residual adds are fused
-//    into the O / down epilogues; greedy argmax is fused into the LM head;
-//  * attention is flash-decode over (kv-group, 64-key chunk) units, one wave each, all query heads
-//    of a GQA group sharing every K/V load; the last unit of a group to finish merges the group's
-//    partials (arrival counter), so attention costs a single grid barrier;
-//  * 5 grid barriers per layer, each a single agent-scope counter with a bounded spin.
+//  * NO grid barriers: every activation word carries a 16-bit phase tag next to its bf16 value
+//    and is exchanged through device-coherent (agent-scope) stores/loads; a consumer polls the
+//    words it needs until they carry the producing phase's tag, so one coherence round trip
+//    replaces store-completion wait + flag + poll + reload. Every exchange is all-to-all (each
+//    phase needs every producer of the previous one), so no workgroup runs more than one phase
+//    ahead and buffers need no double-buffering;
+//  * the next phase's weight chunks are loaded into registers right after a phase's epilogue,
+//    so the HBM stream overlaps the wait for the next phase's inputs;
+//  * RMSNorm is recomputed by every workgroup from the residual; RoPE + KV append are fused
+//    into the QKV epilogue (NEOX pairs live in adjacent packed rows); SwiGLU into the gate/up
+//    epilogue (gate/up rows interleaved); residual adds into the O / down epilogues; greedy
+//    argmax into the LM head;
+//  * attention: one workgroup per (kv group, key slice); its 8 waves split the slice into
+//    64-key chunks with an online softmax, all query heads of the GQA group sharing each K/V
+//    load; waves merge through LDS; slices (long contexts only) merge through an arrival
+//    counter, the last slice merging.
 #include "fl_common.h"
 #include <stdlib.h>
 #include <string.h>
@@ -27,35 +33,46 @@ namespace {
 
 constexpr int NT = 512;              // threads per workgroup
 constexpr int NWAVE = NT / FL_WAVE;  // waves per workgroup
-constexpr int MAXC = 12;             // max 16-byte weight chunks per thread in one GEMV phase
+// max 16-byte weight chunks per thread in each GEMV phase (registers holding one phase's
+// prefetched weights; a small O-phase array keeps attention free of spills)
+constexpr int MC_QKV = 4, MC_O = 4, MC_GU = 12, MC_D = 8;
+constexpr int MAXC = MC_GU;
 constexpr int XS_MAX = 8192;         // max staged activation length (bf16 elements)
 constexpr int ROWS_MAX = 256;        // max rows per workgroup in one GEMV phase
 constexpr int QPG_MAX = 8;           // max query heads per kv group
-constexpr int KC = 64;               // keys per attention unit (one per lane)
-constexpr int LM_MAXC = 8;           // max 16-byte chunks per lane of one LM-head row (D <= 4096)
+constexpr int KC = 64;               // keys per attention chunk (one per lane)
+constexpr int LM_MAXC = 6;           // max 16-byte chunks per lane of one LM-head row (D <= 3072)
 constexpr int LM_RB = 2;             // LM-head rows per wave per batch
+constexpr int MAX_SLICES = 64;       // attention key slices per kv group
 constexpr unsigned long long SPIN_TICKS = 200000000ull;  // 2 s of the 100 MHz realtime clock
-// LDS float workspace: GEMV per-chunk partials, or per-wave attention q/p tiles
-constexpr int WS_FLOATS = (MAXC * NT > NWAVE * 2 * QPG_MAX * 64) ? MAXC * NT : NWAVE * 2 * QPG_MAX * 64;
+// attention LDS (floats): q tiles, new k / v rows, per-wave p tiles and per-wave partials
+constexpr int ATT_Q = QPG_MAX * 64;
+constexpr int ATT_WP = QPG_MAX * 66;
+constexpr int ATT_FLOATS = ATT_Q + 128 + NWAVE * (QPG_MAX * 64 + ATT_WP);
+constexpr int WS_FLOATS = (MAXC * NT > ATT_FLOATS) ? MAXC * NT : ATT_FLOATS;
 
 struct DecodeParams {
   fl_weights w;
-  uint16_t *kc, *vc;        // [NL, NKV, S, 64]
-  uint16_t *h, *q, *attn, *act;
-  float* part;              // attention partials
-  uint32_t* cnt;            // [NKV] attention arrivals
-  unsigned long long* bar;  // grid barrier counter
-  unsigned long long* amax; // argmax key
-  uint32_t* done;           // final arrivals
-  int32_t* err;             // abort flag (barrier timeout)
+  uint16_t *kc, *vc;           // [NL, NKV, S, 64] bf16 cache
+  uint32_t *h, *attn, *act;    // tagged words: bf16 value | tag << 16
+  unsigned long long* qkv;     // tagged NEOX pairs: dim i | dim i+32 << 16 | tag << 32
+  float* part;                 // attention slice partials
+  uint32_t* cnt;               // [NKV] slice arrivals
+  unsigned long long* amax;    // argmax key
+  uint32_t* done;              // final arrivals
+  int32_t* err;                // abort flag (spin timeout / bad token)
   const int32_t* token_in;
   int32_t* token_out;
   float* logits;
   uint16_t* feat;
   int D, NH, NKV, F, V, NL, S, pos;
   float eps, emb_mult, attn_scale, resid_mult, logits_scaling;
-  unsigned long long bar_base;
+  uint32_t epoch;              // epoch of this launch's first phase (5 per layer)
+  unsigned long long* prof;    // optional per-workgroup phase timestamps (100 MHz clock)
+  int prof_slots;
 };
+
+__device__ __forceinline__ uint32_t tag_of(uint32_t epoch) { return epoch % 65535u + 1u; }
 
 __device__ __forceinline__ void row_range(int n, int wg, int G, int& r0, int& rows) {
   int R = (n + G - 1) / G;
@@ -65,30 +82,50 @@ __device__ __forceinline__ void row_range(int n, int wg, int G, int& r0, int& ro
   if (rows < 0) rows = 0;
 }
 
-// Grid barrier: one agent-scope counter, monotonic across launches (the host keeps the base).
-__device__ void grid_sync(const DecodeParams& p, unsigned long long& target) {
-  target += gridDim.x;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(p.bar, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-      const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-      unsigned it = 0;
-      while (__hip_atomic_load(p.bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-        __builtin_amdgcn_s_sleep(1);
-        if ((++it & 255u) == 0) {
-          if (__builtin_amdgcn_s_memrealtime() - t0 > SPIN_TICKS) {
-            __hip_atomic_store(p.err, (int32_t)FL_E_TIMEOUT, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            break;
-          }
-          if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-        }
+__device__ __forceinline__ void stamp(const DecodeParams& p, int& slot) {
+  if (p.prof && threadIdx.x == 0 && slot < p.prof_slots)
+    p.prof[(size_t)blockIdx.x * p.prof_slots + slot] = __builtin_amdgcn_s_memrealtime();
+  ++slot;
+}
+
+// Slow path of a tag wait: sleep-poll with a 2 s limit; a timeout (or an earlier error) is
+// recorded in p.err and the wait gives up, so a broken producer can never hang the GPU.
+template <typename T, typename Ok, typename Ld>
+__device__ __forceinline__ T spin_until(const DecodeParams& p, T v, Ok ok, Ld ld) {
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  unsigned it = 0;
+  while (!ok(v)) {
+    __builtin_amdgcn_s_sleep(2);
+    v = ld();
+    if ((++it & 63u) == 0) {
+      if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > SPIN_TICKS) {
+        __hip_atomic_store(p.err, (int32_t)FL_E_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
-  __syncthreads();
+  return v;
+}
+
+// four tagged words (16-byte aligned) once all carry `tag`
+__device__ __forceinline__ uint4 wait4(const DecodeParams& p, const uint32_t* a, uint32_t tag) {
+  auto ld = [a]() { return ld_coh_u128(a); };
+  auto ok = [tag](uint4 v) {
+    return ((v.x >> 16) == tag) & ((v.y >> 16) == tag) & ((v.z >> 16) == tag) & ((v.w >> 16) == tag);
+  };
+  uint4 v = ld();
+  if (!ok(v)) v = spin_until(p, v, ok, ld);
+  return v;
+}
+
+__device__ __forceinline__ unsigned long long wait_pair(const DecodeParams& p,
+                                                        const unsigned long long* a, uint32_t tag) {
+  auto ld = [a]() { return ld_coh_u64(a); };
+  auto ok = [tag](unsigned long long v) { return (uint32_t)(v >> 32) == tag; };
+  unsigned long long v = ld();
+  if (!ok(v)) v = spin_until(p, v, ok, ld);
+  return v;
 }
 
 __device__ __forceinline__ void wave_sync() {
@@ -97,31 +134,11 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// xs = RMSNorm(src) with gpt-fast's rounding (engine/model.py:231-242):
-//   n = bf16(x * rsqrt(mean(x^2) + eps)) ; out = bf16(n * w)
-// When use_mult, src is an embedding row and x = bf16(src * mult) (engine/model.py:138).
-__device__ void wg_norm(const uint16_t* __restrict__ src, bool use_mult, float mult,
-                        const uint16_t* __restrict__ nw, int D, float eps, uint16_t* xs,
-                        float* red) {
+// Second half of RMSNorm (engine/model.py:237-242): xs holds x (bf16), ss the partial sums of
+// x^2 of this thread; xs <- bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w).
+__device__ void norm_finish(float ss, const uint16_t* __restrict__ nw, int D, float eps,
+                            uint16_t* xs, float* red) {
   const int tid = threadIdx.x;
-  float ss = 0.0f;
-  for (int i = tid; i < (D >> 3); i += NT) {
-    const uint4 v = reinterpret_cast<const uint4*>(src)[i];
-    const uint32_t in[4] = {v.x, v.y, v.z, v.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float a = bflo(in[j]), b = bfhi(in[j]);
-      if (use_mult) {
-        a = rbf(a * mult);
-        b = rbf(b * mult);
-      }
-      ss += a * a;
-      ss += b * b;
-      o[j] = pack_bf16x2(a, b);
-    }
-    reinterpret_cast<uint4*>(xs)[i] = make_uint4(o[0], o[1], o[2], o[3]);
-  }
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
@@ -145,32 +162,81 @@ __device__ void wg_norm(const uint16_t* __restrict__ src, bool use_mult, float m
   __syncthreads();
 }
 
-// xs = src (bf16 vector of length n, n % 8 == 0)
-__device__ __forceinline__ void wg_stage(const uint16_t* __restrict__ src, int n, uint16_t* xs) {
-  for (int i = threadIdx.x; i < (n >> 3); i += NT)
-    reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(src)[i];
+// xs = RMSNorm(bf16(embed_row * mult))  (engine/model.py:138 then :237-242)
+__device__ void norm_embed(const uint16_t* __restrict__ erow, float mult,
+                           const uint16_t* __restrict__ nw, int D, float eps, uint16_t* xs,
+                           float* red) {
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < (D >> 3); i += NT) {
+    const uint4 v = reinterpret_cast<const uint4*>(erow)[i];
+    const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = rbf(bflo(in[j]) * mult), b = rbf(bfhi(in[j]) * mult);
+      ss += a * a;
+      ss += b * b;
+      o[j] = pack_bf16x2(a, b);
+    }
+    reinterpret_cast<uint4*>(xs)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  norm_finish(ss, nw, D, eps, xs, red);
+}
+
+// xs = RMSNorm(h) once every word of the tagged residual h carries `tag`
+__device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t tag,
+                            const uint16_t* __restrict__ nw, uint16_t* xs, float* red) {
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < (p.D >> 2); i += NT) {
+    const uint4 v = wait4(p, h + 4 * i, tag);
+    const float a0 = bflo(v.x), a1 = bflo(v.y), a2 = bflo(v.z), a3 = bflo(v.w);
+    ss += a0 * a0;
+    ss += a1 * a1;
+    ss += a2 * a2;
+    ss += a3 * a3;
+    reinterpret_cast<uint2*>(xs)[i] =
+        make_uint2((v.x & 0xFFFFu) | (v.y << 16), (v.z & 0xFFFFu) | (v.w << 16));
+  }
+  __syncthreads();
+  norm_finish(ss, nw, p.D, p.eps, xs, red);
+}
+
+// xs = values of the tagged vector src[0..n) once all carry `tag`
+__device__ void stage_tagged(const DecodeParams& p, const uint32_t* src, int n, uint32_t tag,
+                             uint16_t* xs) {
+  for (int i = threadIdx.x; i < (n >> 2); i += NT) {
+    const uint4 v = wait4(p, src + 4 * i, tag);
+    reinterpret_cast<uint2*>(xs)[i] =
+        make_uint2((v.x & 0xFFFFu) | (v.y << 16), (v.z & 0xFFFFu) | (v.w << 16));
+  }
   __syncthreads();
 }
 
 // Issue this workgroup's weight chunks for rows [r0, r0+rows) of a [N, K] int4 matrix.
+template <int MC>
 __device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ q,
                                           const uint32_t* __restrict__ sz, int r0, int rows, int K,
-                                          uint4 (&wr)[MAXC], uint32_t (&sr)[MAXC]) {
+                                          uint4 (&wr)[MC], uint32_t (&sr)[MC]) {
   const int total = rows * (K >> 5);
   const uint4* wb = reinterpret_cast<const uint4*>(q + (size_t)r0 * (K >> 3));
   const uint32_t* sb = sz + (size_t)r0 * (K >> 7);
 #pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
+  for (int i = 0; i < MC; ++i) {
     const int f = threadIdx.x + i * NT;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t z = 0u;
     if (f < total) {
-      wr[i] = wb[f];
-      sr[i] = sb[f >> 2];
+      v = wb[f];
+      z = sb[f >> 2];
     }
+    wr[i] = v;  // unconditional: the previous contents are dead here
+    sr[i] = z;
   }
 }
 
 // rs[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load; x staged in xs.
-__device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MAXC], const uint32_t (&sr)[MAXC],
+template <int MC>
+__device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
                                              int rows, int K, const uint16_t* xs, float* part,
                                              float* rs) {
   const int tid = threadIdx.x;
@@ -179,7 +245,7 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MAXC], const uint
   int c = tid % cpr;
   const int step = NT % cpr;
 #pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
+  for (int i = 0; i < MC; ++i) {
     const int f = tid + i * NT;
     if (f < total)
       part[f] = chunk_dot(wr[i], sr[i], reinterpret_cast<const uint4*>(xs + c * 32), 0.0f);
@@ -199,73 +265,144 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MAXC], const uint
   __syncthreads();
 }
 
+// slices of the key range [0, T) for one kv group: (number of slices, 64-key chunks per slice)
+__device__ __forceinline__ void attn_slices(int T, int NKV, int G, int& nsl, int& cps) {
+  const int nch = (T + KC - 1) / KC;
+  if (nch <= 2 * NWAVE) {
+    nsl = 1;
+  } else {
+    nsl = (nch + NWAVE - 1) / NWAVE;
+    const int cap = max(1, min(MAX_SLICES, G / NKV));
+    if (nsl > cap) nsl = cap;
+  }
+  cps = (nch + nsl - 1) / nsl;
+  nsl = (nch + cps - 1) / cps;
+}
+
 template <int QPG>
-__device__ void attention_phase(const DecodeParams& p, int l, float* wl) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
+                                float* ws) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = gridDim.x;
   const int T = p.pos + 1;
+  int nsl, cps;
+  attn_slices(T, p.NKV, G, nsl, cps);
   const int nch = (T + KC - 1) / KC;
-  const int units = p.NKV * nch;
-  float* qs = wl + wave * (2 * QPG_MAX * 64);
-  float* ps = qs + QPG_MAX * 64;
-  for (int u = wave * G + blockIdx.x; u < units; u += G * NWAVE) {
-    const int g = u / nch, ch = u - g * nch, t0 = ch * KC;
+  float* qs = ws;                                           // [QPG][64] this step's q of the group
+  float* kn = qs + ATT_Q;                                   // [64] this step's k of the group
+  float* vn = kn + 64;                                      // [64] this step's v of the group
+  float* ps = vn + 64 + wave * (QPG_MAX * 64);              // per-wave p tile
+  float* wpart = vn + 64 + NWAVE * (QPG_MAX * 64);          // [NWAVE][QPG][66]
+  __shared__ uint32_t s_old;
+  for (int u = blockIdx.x; u < p.NKV * nsl; u += G) {
+    const int g = u / nsl, sl = u - g * nsl;
     const size_t cbase = (size_t)(l * p.NKV + g) * p.S * 64;
     const uint16_t* kb = p.kc + cbase;
     const uint16_t* vb = p.vc + cbase;
-    for (int i = lane; i < QPG * 64; i += 64) qs[i] = bf2f(p.q[g * QPG * 64 + i]);
-    wave_sync();
-    // scores: lane = key
-    const int t = t0 + lane;
-    const bool valid = t < T;
-    float s[QPG];
-#pragma unroll
-    for (int h = 0; h < QPG; ++h) s[h] = 0.0f;
-    if (valid) {
-      const uint4* kr = reinterpret_cast<const uint4*>(kb + (size_t)t * 64);
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const uint4 kv = kr[jj];
-        const float kf[8] = {bflo(kv.x), bfhi(kv.x), bflo(kv.y), bfhi(kv.y),
-                             bflo(kv.z), bfhi(kv.z), bflo(kv.w), bfhi(kv.w)};
-#pragma unroll
-        for (int h = 0; h < QPG; ++h)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) s[h] = __builtin_fmaf(qs[h * 64 + jj * 8 + e], kf[e], s[h]);
-      }
+    // q / k / v of group g from this launch's QKV phase (tagged pairs)
+    for (int i = tid; i < (QPG + 2) * 32; i += NT) {
+      const int hq = i >> 5, j = i & 31;
+      const int hh = hq < QPG ? g * QPG + hq : (hq == QPG ? p.NH + g : p.NH + p.NKV + g);
+      const unsigned long long v = wait_pair(p, p.qkv + hh * 32 + j, qtag);
+      float* dst = hq < QPG ? qs + hq * 64 : (hq == QPG ? kn : vn);
+      dst[j] = bflo((uint32_t)v);
+      dst[j + 32] = bfhi((uint32_t)v);
     }
-    float mh[QPG], lh[QPG];
+    __syncthreads();
+    float m[QPG], lsum[QPG], acc[QPG][4];
 #pragma unroll
     for (int h = 0; h < QPG; ++h) {
-      const float sv = valid ? s[h] * p.attn_scale : -INFINITY;
-      const float m = wave_max(sv);
-      const float pv = valid ? expf(sv - m) : 0.0f;
-      lh[h] = wave_sum(pv);
-      mh[h] = m;
-      ps[h * 64 + lane] = pv;
-    }
-    wave_sync();
-    // P.V: lane = (4-dim slice j4, key lane group kg of 4)
-    const int j4 = lane & 15, kg = lane >> 4;
-    float acc[QPG][4];
-#pragma unroll
-    for (int h = 0; h < QPG; ++h)
+      m[h] = -INFINITY;
+      lsum[h] = 0.0f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[h][e] = 0.0f;
-#pragma unroll 4
-    for (int kk = 0; kk < KC / 4; ++kk) {
-      const int tt = kg + 4 * kk;
-      if (t0 + tt < T) {
-        const uint2 vv = *reinterpret_cast<const uint2*>(vb + (size_t)(t0 + tt) * 64 + j4 * 4);
-        const float vf[4] = {bflo(vv.x), bfhi(vv.x), bflo(vv.y), bfhi(vv.y)};
+    }
+    const int j4 = lane & 15, kg = lane >> 4;
+    const int c_end = min(nch, (sl + 1) * cps);
+    for (int c = sl * cps + wave; c < c_end; c += NWAVE) {
+      const int t0 = c * KC;
+      const int t = t0 + lane;
+      const bool valid = t < T;
+      const bool is_new = t == p.pos;
+      // issue this chunk's K row loads and V slice loads together (one memory round trip)
+      uint4 kv[8];
+      if (valid && !is_new) {
+        const uint4* kr = reinterpret_cast<const uint4*>(kb + (size_t)t * 64);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) kv[jj] = kr[jj];
+      }
+      uint2 vv[KC / 4];
+#pragma unroll
+      for (int kk = 0; kk < KC / 4; ++kk) {
+        const int tk = t0 + kg + 4 * kk;
+        vv[kk] = make_uint2(0u, 0u);
+        if (tk < T && tk != p.pos)
+          vv[kk] = *reinterpret_cast<const uint2*>(vb + (size_t)tk * 64 + j4 * 4);
+      }
+      float s[QPG];
+#pragma unroll
+      for (int h = 0; h < QPG; ++h) s[h] = 0.0f;
+      if (valid && !is_new) {
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float kf[8] = {bflo(kv[jj].x), bfhi(kv[jj].x), bflo(kv[jj].y), bfhi(kv[jj].y),
+                               bflo(kv[jj].z), bfhi(kv[jj].z), bflo(kv[jj].w), bfhi(kv[jj].w)};
+#pragma unroll
+          for (int h = 0; h < QPG; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[h] = __builtin_fmaf(qs[h * 64 + jj * 8 + e], kf[e], s[h]);
+          __builtin_amdgcn_sched_barrier(0);  // bound the q values held in registers
+        }
+      }
+      if (is_new) {
+        for (int d = 0; d < 64; ++d) {
+          const float kd = kn[d];
+#pragma unroll
+          for (int h = 0; h < QPG; ++h) s[h] = __builtin_fmaf(qs[h * 64 + d], kd, s[h]);
+        }
+      }
+      // online softmax update (per head; m and lsum are wave-uniform)
+      float corr[QPG];
+#pragma unroll
+      for (int h = 0; h < QPG; ++h) {
+        const float sv = valid ? s[h] * p.attn_scale : -INFINITY;
+        const float mc = wave_max(sv);
+        const float mn = fmaxf(m[h], mc);
+        corr[h] = expf(m[h] - mn);  // 0 on the first chunk (m = -inf)
+        const float pv = valid ? expf(sv - mn) : 0.0f;
+        lsum[h] = lsum[h] * corr[h] + wave_sum(pv);
+        m[h] = mn;
+        ps[h * 64 + lane] = pv;
+      }
+      wave_sync();
+#pragma unroll
+      for (int h = 0; h < QPG; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[h][e] *= corr[h];
+#pragma unroll
+      for (int kk = 0; kk < KC / 4; ++kk) {
+        const int tt = kg + 4 * kk;
+        const float vf[4] = {bflo(vv[kk].x), bfhi(vv[kk].x), bflo(vv[kk].y), bfhi(vv[kk].y)};
+#pragma unroll
+        for (int h = 0; h < QPG; ++h) {
+          const float pw = ps[h * 64 + tt];  // 0 for keys beyond T; the new key is added below
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[h][e] = __builtin_fmaf(pw, vf[e], acc[h][e]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (p.pos >= t0 && p.pos < t0 + KC && kg == ((p.pos - t0) & 3)) {  // the new key's value
+        const int tt = p.pos - t0;
 #pragma unroll
         for (int h = 0; h < QPG; ++h) {
           const float pw = ps[h * 64 + tt];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[h][e] = __builtin_fmaf(pw, vf[e], acc[h][e]);
+          for (int e = 0; e < 4; ++e) acc[h][e] = __builtin_fmaf(pw, vn[j4 * 4 + e], acc[h][e]);
         }
       }
+      wave_sync();  // ps is rewritten by the next chunk
     }
+    // per-wave partial (m, l, acc[64]) -> LDS
 #pragma unroll
     for (int h = 0; h < QPG; ++h)
 #pragma unroll
@@ -275,51 +412,90 @@ __device__ void attention_phase(const DecodeParams& p, int l, float* wl) {
         v += __shfl_xor(v, 32, 64);
         acc[h][e] = v;
       }
-    float* pp = p.part + (size_t)u * QPG * 66;
+    float* mywp = wpart + wave * ATT_WP;
     if (kg == 0) {
 #pragma unroll
       for (int h = 0; h < QPG; ++h)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) pp[h * 66 + 2 + j4 * 4 + e] = acc[h][e];
+        for (int e = 0; e < 4; ++e) mywp[h * 66 + 2 + j4 * 4 + e] = acc[h][e];
     }
     if (lane == 0) {
 #pragma unroll
       for (int h = 0; h < QPG; ++h) {
-        pp[h * 66] = mh[h];
-        pp[h * 66 + 1] = lh[h];
+        mywp[h * 66] = m[h];
+        mywp[h * 66 + 1] = lsum[h];
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    uint32_t old = 0;
-    if (lane == 0)
-      old = __hip_atomic_fetch_add(p.cnt + g, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, 0, 64);
-    if (old == (uint32_t)(nch - 1)) {
-      // last unit of group g: merge the nch partials (log-sum-exp rescale), fixed order
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      const float* gp = p.part + (size_t)g * nch * QPG * 66;
-      for (int h = 0; h < QPG; ++h) {
-        float M = -INFINITY;
-        for (int c = 0; c < nch; ++c) M = fmaxf(M, gp[(size_t)(c * QPG + h) * 66]);
-        float Ls = 0.0f, O = 0.0f;
-        for (int c = 0; c < nch; ++c) {
-          const float* cp = gp + (size_t)(c * QPG + h) * 66;
-          const float e = expf(cp[0] - M);
-          Ls += cp[1] * e;
-          O += cp[2 + lane] * e;
+    __syncthreads();
+    // merge the waves in a fixed order: thread (head hm, dim d)
+    float M = -INFINITY, Ls = 0.0f, O = 0.0f;
+    const int hm = tid >> 6, d = tid & 63;
+    if (hm < QPG) {
+      for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, wpart[w * ATT_WP + hm * 66]);
+      for (int w = 0; w < NWAVE; ++w) {
+        const float* wp = wpart + w * ATT_WP + hm * 66;
+        const float e = (wp[0] == -INFINITY) ? 0.0f : expf(wp[0] - M);
+        Ls += wp[1] * e;
+        O += wp[2 + d] * e;
+      }
+    }
+    if (nsl == 1) {
+      if (hm < QPG) st_coh_u32(p.attn + (g * QPG + hm) * 64 + d, f2bf(O / Ls) | (otag << 16));
+    } else {
+      // slice partial -> global; the last slice of the group to arrive merges all of them
+      float* pp = p.part + ((size_t)g * MAX_SLICES + sl) * QPG * 66;
+      if (hm < QPG) {
+        if (d == 0) {
+          st_coh_f32(pp + hm * 66, M);
+          st_coh_f32(pp + hm * 66 + 1, Ls);
         }
-        p.attn[(g * QPG + h) * 64 + lane] = (uint16_t)f2bf(O / Ls);
+        st_coh_f32(pp + hm * 66 + 2 + d, O);
       }
-      if (lane == 0) __hip_atomic_store(p.cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      wait_mem();
+      __syncthreads();
+      if (tid == 0)
+        s_old = __hip_atomic_fetch_add(p.cnt + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      if (s_old == (uint32_t)(nsl - 1)) {
+        if (hm < QPG) {
+          const float* gp = p.part + (size_t)g * MAX_SLICES * QPG * 66 + hm * 66;
+          float Mg = -INFINITY;
+          for (int c = 0; c < nsl; ++c) Mg = fmaxf(Mg, ld_coh_f32(gp + (size_t)c * QPG * 66));
+          float Lg = 0.0f, Og = 0.0f;
+          for (int c = 0; c < nsl; ++c) {
+            const float* cp = gp + (size_t)c * QPG * 66;
+            const float e = expf(ld_coh_f32(cp) - Mg);
+            Lg += ld_coh_f32(cp + 1) * e;
+            Og += ld_coh_f32(cp + 2 + d) * e;
+          }
+          st_coh_u32(p.attn + (g * QPG + hm) * 64 + d, f2bf(Og / Lg) | (otag << 16));
+        }
+        if (tid == 0) __hip_atomic_store(p.cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
-    wave_sync();
+    __syncthreads();  // LDS tiles are reused by the next unit
+  }
+}
+
+// tagged h[r0 .. r0+rows) = bf16(h + bf16(bf16(acc) * rm)), two rows per thread (r0, rows even)
+__device__ __forceinline__ void residual_epilogue(const DecodeParams& p, int r0, int rows,
+                                                  const float* rs, uint32_t tag) {
+  const int t = threadIdx.x;
+  if (2 * t < rows) {
+    unsigned long long* hp = reinterpret_cast<unsigned long long*>(p.h + r0) + t;
+    const unsigned long long hv = ld_coh_u64(hp);  // own rows: no tag wait needed
+    const float o0 = rbf(rbf(rs[2 * t]) * p.resid_mult);
+    const float o1 = rbf(rbf(rs[2 * t + 1]) * p.resid_mult);
+    const uint32_t n0 = f2bf(bflo((uint32_t)hv) + o0) | (tag << 16);
+    const uint32_t n1 = f2bf(bflo((uint32_t)(hv >> 32)) + o1) | (tag << 16);
+    st_coh_u64(hp, (unsigned long long)n0 | ((unsigned long long)n1 << 32));
   }
 }
 
 template <int QPG>
 __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
   __shared__ __align__(16) uint16_t xs[XS_MAX];
-  __shared__ __align__(16) float part[WS_FLOATS];
+  __shared__ __align__(16) float ws[WS_FLOATS];
   __shared__ float rs[ROWS_MAX];
   __shared__ float red[64];
   __shared__ unsigned long long kred[NWAVE];
@@ -328,7 +504,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
   const int D = p.D, F = p.F, NKV = p.NKV, NH = p.NH;
   const int NQKV = (NH + 2 * NKV) * 64;
   const int pos = p.pos;
-  unsigned long long target = p.bar_base;
+  int slot = 0;
+  stamp(p, slot);
   int token = *p.token_in;
   if (token < 0 || token >= p.V) {  // bad device-side token: record it, read row 0 (no fault)
     if (tid == 0 && wg == 0)
@@ -339,113 +516,124 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 
   int r0d, rowsd;  // this workgroup's rows of every [D]-output GEMV (O, down): it owns h there
   row_range(D, wg, G, r0d, rowsd);
-  // h = bf16(embed[token] * emb_mult) on the owned rows (engine/model.py:138)
-  for (int i = tid; i < rowsd; i += NT)
-    p.h[r0d + i] = (uint16_t)f2bf(bf2f(erow[r0d + i]) * p.emb_mult);
+  // h = bf16(embed[token] * emb_mult) on the owned rows (engine/model.py:138); only this
+  // workgroup reads these words before they are rewritten, so their tag is irrelevant
+  for (int i = tid; 2 * i < rowsd; i += NT) {
+    const uint32_t e2 = reinterpret_cast<const uint32_t*>(erow + r0d)[i];
+    const uint32_t a = f2bf(bflo(e2) * p.emb_mult), b = f2bf(bfhi(e2) * p.emb_mult);
+    st_coh_u64(reinterpret_cast<unsigned long long*>(p.h + r0d) + i,
+               (unsigned long long)a | ((unsigned long long)b << 32));
+  }
 
-  uint4 wr[MAXC];
-  uint32_t sr[MAXC];
+  uint4 w_qkv[MC_QKV], w_o[MC_O], w_gu[MC_GU], w_d[MC_D];
+  uint32_t s_qkv[MC_QKV], s_o[MC_O], s_gu[MC_GU], s_d[MC_D];
   int r0, rows;
   row_range(NQKV, wg, G, r0, rows);
-  gemv_load(p.w.wqkv_q, p.w.wqkv_sz, r0, rows, D, wr, sr);
+  gemv_load(p.w.wqkv_q, p.w.wqkv_sz, r0, rows, D, w_qkv, s_qkv);
 
   for (int l = 0; l < p.NL; ++l) {
+    const uint32_t e0 = p.epoch + 5u * (uint32_t)l;
+    const uint32_t t_prev = tag_of(e0 - 1), t_qkv = tag_of(e0), t_attn = tag_of(e0 + 1),
+                   t_h1 = tag_of(e0 + 2), t_act = tag_of(e0 + 3), t_h2 = tag_of(e0 + 4);
     // ---------------- P1: RMSNorm + QKV + RoPE + KV append ----------------
-    if (l == 0)
-      wg_norm(erow, true, p.emb_mult, p.w.attn_norm, D, p.eps, xs, red);
-    else
-      wg_norm(p.h, false, 1.0f, p.w.attn_norm + (size_t)l * D, D, p.eps, xs, red);
     row_range(NQKV, wg, G, r0, rows);
-    gemv_compute(wr, sr, rows, D, xs, part, rs);
-    if (tid < (rows >> 1)) {
-      const int srow = r0 + 2 * tid;
-      const int hh = srow >> 6, j = (srow & 63) >> 1;
-      const float a = rbf(rs[2 * tid]), b = rbf(rs[2 * tid + 1]);
-      float oa = a, ob = b;
-      if (hh < NH + NKV) {  // RoPE (engine/model.py:257-269 on NEOX pairs j, j+32)
-        const uint32_t cs = reinterpret_cast<const uint32_t*>(p.w.rope)[pos * 32 + j];
-        const float c = bflo(cs), sn = bfhi(cs);
-        oa = rbf(a * c - b * sn);
-        ob = rbf(b * c + a * sn);
+    if (rows > 0) {
+      if (l == 0)
+        norm_embed(erow, p.emb_mult, p.w.attn_norm, D, p.eps, xs, red);
+      else
+        norm_tagged(p, p.h, t_prev, p.w.attn_norm + (size_t)l * D, xs, red);
+      stamp(p, slot);
+      gemv_compute(w_qkv, s_qkv, rows, D, xs, ws, rs);
+      if (tid < (rows >> 1)) {
+        const int srow = r0 + 2 * tid;
+        const int hh = srow >> 6, j = (srow & 63) >> 1;
+        const float a = rbf(rs[2 * tid]), b = rbf(rs[2 * tid + 1]);
+        float oa = a, ob = b;
+        if (hh < NH + NKV) {  // RoPE (engine/model.py:257-269 on NEOX pairs j, j+32)
+          const uint32_t cs = reinterpret_cast<const uint32_t*>(p.w.rope)[pos * 32 + j];
+          const float c = bflo(cs), sn = bfhi(cs);
+          oa = rbf(a * c - b * sn);
+          ob = rbf(b * c + a * sn);
+        }
+        st_coh_u64(p.qkv + hh * 32 + j,
+                   (unsigned long long)pack_bf16x2(oa, ob) | ((unsigned long long)t_qkv << 32));
+        if (hh >= NH) {  // KV append for later launches (engine/model.py:89-98)
+          const int g = (hh < NH + NKV) ? hh - NH : hh - NH - NKV;
+          uint16_t* dst = ((hh < NH + NKV) ? p.kc : p.vc) + ((size_t)(l * NKV + g) * p.S + pos) * 64;
+          dst[j] = (uint16_t)f2bf(oa);
+          dst[j + 32] = (uint16_t)f2bf(ob);
+        }
       }
-      if (hh < NH) {
-        p.q[hh * 64 + j] = (uint16_t)f2bf(oa);
-        p.q[hh * 64 + j + 32] = (uint16_t)f2bf(ob);
-      } else {
-        const int g = (hh < NH + NKV) ? hh - NH : hh - NH - NKV;
-        uint16_t* dst = ((hh < NH + NKV) ? p.kc : p.vc) +
-                        ((size_t)(l * NKV + g) * p.S + pos) * 64;
-        dst[j] = (uint16_t)f2bf(oa);
-        dst[j + 32] = (uint16_t)f2bf(ob);
-      }
+    } else {
+      stamp(p, slot);
     }
-    __syncthreads();
-    row_range(D, wg, G, r0, rows);
-    gemv_load(p.w.wo_q + (size_t)l * D * (D >> 3), p.w.wo_sz + (size_t)l * D * (D >> 7), r0, rows,
-              D, wr, sr);
-    grid_sync(p, target);
+    stamp(p, slot);
 
     // ---------------- P2: GQA flash-decode attention ----------------
-    attention_phase<QPG>(p, l, part);
-    grid_sync(p, target);
+    // (the O weights are requested after it: attention needs the registers, and the O phase
+    // waits for every group's attention output anyway)
+    attention_phase<QPG>(p, l, t_qkv, t_attn, ws);
+    stamp(p, slot);
+    row_range(D, wg, G, r0, rows);
+    gemv_load(p.w.wo_q + (size_t)l * D * (D >> 3), p.w.wo_sz + (size_t)l * D * (D >> 7), r0, rows,
+              D, w_o, s_o);
 
     // ---------------- P3: O projection + residual ----------------
-    wg_stage(p.attn, D, xs);
-    row_range(D, wg, G, r0, rows);
-    gemv_compute(wr, sr, rows, D, xs, part, rs);
-    if (tid < rows) {  // h = bf16(h + bf16(bf16(o) * rm))  (engine/model.py:162)
-      const int r = r0 + tid;
-      const float o = rbf(rbf(rs[tid]) * p.resid_mult);
-      p.h[r] = (uint16_t)f2bf(bf2f(p.h[r]) + o);
+    if (rows > 0) {
+      stage_tagged(p, p.attn, D, t_attn, xs);
+      stamp(p, slot);
+      gemv_compute(w_o, s_o, rows, D, xs, ws, rs);
+      residual_epilogue(p, r0, rows, rs, t_h1);  // engine/model.py:162
+    } else {
+      stamp(p, slot);
     }
-    __syncthreads();
+    stamp(p, slot);
     row_range(2 * F, wg, G, r0, rows);
     gemv_load(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3), p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7),
-              r0, rows, D, wr, sr);
-    grid_sync(p, target);
+              r0, rows, D, w_gu, s_gu);
 
     // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
-    wg_norm(p.h, false, 1.0f, p.w.ffn_norm + (size_t)l * D, D, p.eps, xs, red);
-    row_range(2 * F, wg, G, r0, rows);
-    gemv_compute(wr, sr, rows, D, xs, part, rs);
-    if (tid < (rows >> 1)) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
-      const float g = rbf(rs[2 * tid]), u = rbf(rs[2 * tid + 1]);
-      p.act[(r0 >> 1) + tid] = (uint16_t)f2bf(rbf(silu_f(g)) * u);
+    if (rows > 0) {
+      norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red);
+      stamp(p, slot);
+      gemv_compute(w_gu, s_gu, rows, D, xs, ws, rs);
+      if (tid < (rows >> 1)) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
+        const float g = rbf(rs[2 * tid]), u = rbf(rs[2 * tid + 1]);
+        st_coh_u32(p.act + (r0 >> 1) + tid, f2bf(rbf(silu_f(g)) * u) | (t_act << 16));
+      }
+    } else {
+      stamp(p, slot);
     }
-    __syncthreads();
+    stamp(p, slot);
     row_range(D, wg, G, r0, rows);
     gemv_load(p.w.wd_q + (size_t)l * D * (F >> 3), p.w.wd_sz + (size_t)l * D * (F >> 7), r0, rows,
-              F, wr, sr);
-    grid_sync(p, target);
+              F, w_d, s_d);
 
     // ---------------- P5: down projection + residual ----------------
-    wg_stage(p.act, F, xs);
-    row_range(D, wg, G, r0, rows);
-    gemv_compute(wr, sr, rows, F, xs, part, rs);
-    if (tid < rows) {  // out = bf16(h + bf16(bf16(d) * rm))  (engine/model.py:163)
-      const int r = r0 + tid;
-      const float o = rbf(rbf(rs[tid]) * p.resid_mult);
-      p.h[r] = (uint16_t)f2bf(bf2f(p.h[r]) + o);
+    if (rows > 0) {
+      stage_tagged(p, p.act, F, t_act, xs);
+      stamp(p, slot);
+      gemv_compute(w_d, s_d, rows, F, xs, ws, rs);
+      residual_epilogue(p, r0, rows, rs, t_h2);  // engine/model.py:163
+    } else {
+      stamp(p, slot);
     }
-    __syncthreads();
+    stamp(p, slot);
     if (l + 1 < p.NL) {
       row_range(NQKV, wg, G, r0, rows);
       gemv_load(p.w.wqkv_q + (size_t)(l + 1) * NQKV * (D >> 3),
-                p.w.wqkv_sz + (size_t)(l + 1) * NQKV * (D >> 7), r0, rows, D, wr, sr);
+                p.w.wqkv_sz + (size_t)(l + 1) * NQKV * (D >> 7), r0, rows, D, w_qkv, s_qkv);
     }
-    grid_sync(p, target);
   }
 
   // ---------------- final norm + tied bf16 LM head + greedy argmax ----------------
-  wg_norm(p.h, false, 1.0f, p.w.final_norm, D, p.eps, xs, red);
-  if (p.feat && wg == 0)
-    for (int i = tid; i < D; i += NT) p.feat[i] = xs[i];
   const int lane = tid & 63, wave = tid >> 6;
   row_range(p.V, wg, G, r0, rows);
   const int nck = D >> 3;  // 16-byte chunks per row
+  constexpr int STEP = NWAVE * LM_RB;
+  uint4 ea[LM_RB][LM_MAXC], eb[LM_RB][LM_MAXC];
   unsigned long long best = 0ull;
-  for (int rb = wave * LM_RB; rb < rows; rb += NWAVE * LM_RB) {
-    uint4 ev[LM_RB][LM_MAXC];
+  auto lm_load = [&](uint4 (&ev)[LM_RB][LM_MAXC], int rb) {
 #pragma unroll
     for (int rr = 0; rr < LM_RB; ++rr) {
       const uint4* er = reinterpret_cast<const uint4*>(p.w.embed + (size_t)(r0 + rb + rr) * D);
@@ -455,13 +643,15 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
         if (rb + rr < rows && c < nck) ev[rr][i] = er[c];
       }
     }
+  };
+  auto lm_compute = [&](const uint4 (&ev)[LM_RB][LM_MAXC], int rb) {
 #pragma unroll
     for (int rr = 0; rr < LM_RB; ++rr) {
       float acc = 0.0f;
 #pragma unroll
       for (int i = 0; i < LM_MAXC; ++i) {
         const int c = lane + 64 * i;
-        if (rb + rr < rows && c < nck) {
+        if (c < nck) {
           const uint4 xv = reinterpret_cast<const uint4*>(xs)[c];
           acc = dot2_bf16(ev[rr][i].x, xv.x, acc);
           acc = dot2_bf16(ev[rr][i].y, xv.y, acc);
@@ -479,16 +669,30 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
         best = u64max(best, amax_key(lg, (uint32_t)r));
       }
     }
+  };
+  const int rb0 = wave * LM_RB;
+  if (rb0 < rows) lm_load(ea, rb0);  // first batch in flight while the final residual arrives
+  norm_tagged(p, p.h, tag_of(p.epoch + 5u * (uint32_t)p.NL - 1u), p.w.final_norm, xs, red);
+  stamp(p, slot);
+  if (p.feat && wg == 0)
+    for (int i = tid; i < D; i += NT) p.feat[i] = xs[i];
+  for (int rb = rb0; rb < rows; rb += 2 * STEP) {
+    if (rb + STEP < rows) lm_load(eb, rb + STEP);
+    lm_compute(ea, rb);
+    if (rb + 2 * STEP < rows) lm_load(ea, rb + 2 * STEP);
+    if (rb + STEP < rows) lm_compute(eb, rb + STEP);
   }
   if (lane == 0) kred[wave] = best;
   __syncthreads();
+  stamp(p, slot);
   if (tid == 0) {
     unsigned long long b = kred[0];
     for (int w = 1; w < NWAVE; ++w) b = u64max(b, kred[w]);
     __hip_atomic_fetch_max(p.amax, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t old = __hip_atomic_fetch_add(p.done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    wait_mem();
+    const uint32_t old = __hip_atomic_fetch_add(p.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == (uint32_t)(G - 1)) {
-      const unsigned long long fin = __hip_atomic_load(p.amax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned long long fin = ld_coh_u64(p.amax);
       *p.token_out = (int32_t)amax_index(fin);
       __hip_atomic_store(p.amax, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -511,10 +715,10 @@ decode_fn pick_decode(int qpg) {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-int phase_fits(int n, int k, int G) {
+int phase_fits(int n, int k, int G, int cap) {
   int R = (n + G - 1) / G;
   R += (R & 1);
-  return R <= ROWS_MAX && (long)R * (k >> 5) <= (long)MAXC * NT;
+  return R <= ROWS_MAX && (long)R * (k >> 5) <= (long)cap * NT;
 }
 
 }  // namespace
@@ -524,17 +728,18 @@ struct fl_state {
   int max_seq;
   int grid;
   int qpg;
-  int nbar;  // grid barriers per decode launch
   uint16_t *kc, *vc;
-  uint16_t *h, *q, *attn, *act;
+  uint32_t *h, *attn, *act;
+  unsigned long long* qkv;
   float* part;
   uint32_t* cnt;
-  unsigned long long* bar;
   unsigned long long* amax;
   uint32_t* done;
   int32_t* err;
-  unsigned long long bar_base;
-  void* blocks[8];
+  uint32_t epoch;
+  unsigned long long* prof;
+  int prof_slots;
+  void* blocks[16];
   int nblocks;
 };
 
@@ -542,6 +747,7 @@ namespace {
 template <typename T>
 int dev_alloc(fl_state* st, T** p, size_t count) {
   void* v = nullptr;
+  if (st->nblocks >= (int)(sizeof(st->blocks) / sizeof(st->blocks[0]))) return FL_E_ARG;
   if (hipMalloc(&v, count * sizeof(T) + 256) != hipSuccess) return FL_E_HIP;
   if (hipMemset(v, 0, count * sizeof(T) + 256) != hipSuccess) return FL_E_HIP;
   st->blocks[st->nblocks++] = v;
@@ -587,8 +793,8 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   if (occ < 1 || cu < 1) return FL_E_LAUNCH;
   const int G = cu;
   const int D = d->dim, F = d->inter, NQKV = (d->n_head + 2 * d->n_kv_head) * FL_HEAD_DIM;
-  if (!phase_fits(NQKV, D, G) || !phase_fits(D, D, G) || !phase_fits(2 * F, D, G) ||
-      !phase_fits(D, F, G))
+  if (!phase_fits(NQKV, D, G, MC_QKV) || !phase_fits(D, D, G, MC_O) ||
+      !phase_fits(2 * F, D, G, MC_GU) || !phase_fits(D, F, G, MC_D))
     return FL_E_ARG;
   fl_state* st = (fl_state*)calloc(1, sizeof(fl_state));
   if (!st) return FL_E_HIP;
@@ -596,19 +802,17 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   st->max_seq = max_seq;
   st->grid = G;
   st->qpg = qpg;
-  st->nbar = 5 * d->n_layer;
   st->kc = k_cache;
   st->vc = v_cache;
-  const int nch_max = (max_seq + FL_MAX_VERIFY + KC - 1) / KC;
+  st->epoch = 1;
   int rc = FL_OK;
   if (rc == FL_OK) rc = dev_alloc(st, &st->h, (size_t)D * FL_MAX_VERIFY);
-  if (rc == FL_OK) rc = dev_alloc(st, &st->q, (size_t)NQKV * FL_MAX_VERIFY);
+  if (rc == FL_OK) rc = dev_alloc(st, &st->qkv, (size_t)(NQKV / 2) * FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->attn, (size_t)D * FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->act, (size_t)F * FL_MAX_VERIFY);
   if (rc == FL_OK)
-    rc = dev_alloc(st, &st->part, (size_t)d->n_kv_head * nch_max * QPG_MAX * 66 * FL_MAX_VERIFY);
+    rc = dev_alloc(st, &st->part, (size_t)d->n_kv_head * MAX_SLICES * QPG_MAX * 66 * FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->cnt, (size_t)d->n_kv_head * FL_MAX_VERIFY);
-  if (rc == FL_OK) rc = dev_alloc(st, &st->bar, 1);
   if (rc == FL_OK) rc = dev_alloc(st, &st->amax, FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->done, 1);
   if (rc == FL_OK) rc = dev_alloc(st, &st->err, 1);
@@ -637,8 +841,23 @@ int fl_state_reset(fl_state* st, void* stream) {
     return FL_E_HIP;
   if (hipMemsetAsync(st->done, 0, sizeof(uint32_t), s) != hipSuccess) return FL_E_HIP;
   if (hipMemsetAsync(st->err, 0, sizeof(int32_t), s) != hipSuccess) return FL_E_HIP;
-  if (hipMemsetAsync(st->bar, 0, sizeof(unsigned long long), s) != hipSuccess) return FL_E_HIP;
-  st->bar_base = 0;
+  return FL_OK;
+}
+
+int fl_state_profile(fl_state* st, uint64_t* buf, int32_t slots_per_wg, int32_t* grid) {
+  if (!st || (buf && slots_per_wg <= 0)) return FL_E_ARG;
+  st->prof = reinterpret_cast<unsigned long long*>(buf);
+  st->prof_slots = buf ? slots_per_wg : 0;
+  if (grid) *grid = st->grid;
+  return FL_OK;
+}
+
+int fl_state_buffers(fl_state* st, uint16_t** h, uint16_t** qkv, uint16_t** attn, uint16_t** act) {
+  if (!st) return FL_E_ARG;
+  if (h) *h = reinterpret_cast<uint16_t*>(st->h);
+  if (qkv) *qkv = reinterpret_cast<uint16_t*>(st->qkv);
+  if (attn) *attn = reinterpret_cast<uint16_t*>(st->attn);
+  if (act) *act = reinterpret_cast<uint16_t*>(st->act);
   return FL_OK;
 }
 
@@ -663,12 +882,11 @@ int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, i
   p.kc = st->kc;
   p.vc = st->vc;
   p.h = st->h;
-  p.q = st->q;
+  p.qkv = st->qkv;
   p.attn = st->attn;
   p.act = st->act;
   p.part = st->part;
   p.cnt = st->cnt;
-  p.bar = st->bar;
   p.amax = st->amax;
   p.done = st->done;
   p.err = st->err;
@@ -689,13 +907,15 @@ int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, i
   p.attn_scale = st->d.attn_scale;
   p.resid_mult = st->d.resid_mult;
   p.logits_scaling = st->d.logits_scaling;
-  p.bar_base = st->bar_base;
+  p.epoch = st->epoch;
+  p.prof = st->prof;
+  p.prof_slots = st->prof_slots;
   void* args[] = {&p};
   const hipError_t e =
       hipLaunchCooperativeKernel(reinterpret_cast<const void*>(pick_decode(st->qpg)), dim3(st->grid),
                                  dim3(NT), args, 0, as_stream(stream));
   if (e != hipSuccess) return FL_E_LAUNCH;
-  st->bar_base += (unsigned long long)st->nbar * st->grid;
+  st->epoch += 5u * (uint32_t)st->d.n_layer;
   return FL_OK;
 }
 

@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void k_quantize(const uint16_t* __restrict__ w
     t = rbf(t / scale);
     float r = rbf(rintf(t));
     r = fminf(fmaxf(r, 0.0f), 15.0f);
-    word_q |= ((uint32_t)r) << (4 * e);
+    word_q |= ((uint32_t)r) << (4 * nib_pos(e));
   }
   if (valid) {
     q[word] = word_q;
@@ -58,17 +58,18 @@ __global__ __launch_bounds__(256) void k_quantize(const uint16_t* __restrict__ w
   }
 }
 
-// One thread per packed word: 8 bf16 outputs through the same dq8 the GEMVs use.
+// One thread per 16-byte chunk (4 packed words, 32 elements of one group): bf16 outputs through
+// the same dequantisation sequence the GEMVs use.
 __global__ __launch_bounds__(256) void k_dequant(const uint32_t* __restrict__ q,
                                                  const uint32_t* __restrict__ sz,
-                                                 uint16_t* __restrict__ out, int64_t nwords) {
-  const int64_t word = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (word >= nwords) return;
-  const uint32_t szw = sz[word >> 4];
-  const float s = bf2f(szw & 0xFFFFu), z = bf2f(szw >> 16);
-  uint32_t d[4];
-  dq8(q[word], s, z, -8.0f * s, d);
-  *reinterpret_cast<uint4*>(out + word * 8) = make_uint4(d[0], d[1], d[2], d[3]);
+                                                 uint16_t* __restrict__ out, int64_t nchunks) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= nchunks) return;
+  uint32_t d[4][4];
+  dq32(reinterpret_cast<const uint4*>(q)[c], dq_const(sz[c >> 2]), d);
+  uint4* o = reinterpret_cast<uint4*>(out + c * 32);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = make_uint4(d[0][i], d[1][i], d[2][i], d[3][i]);
 }
 
 // M=1 GEMV. A workgroup owns `rows_per_wg` consecutive rows, whose packed words form one
@@ -154,11 +155,11 @@ int fl_quantize_int4(const uint16_t* w, uint32_t* q, uint32_t* sz, int32_t n, in
 int fl_dequant_int4(const uint32_t* q, const uint32_t* sz, uint16_t* out, int32_t n, int32_t k,
                     void* stream) {
   if (!q || !sz || !out || n <= 0 || k <= 0 || (k % FL_GROUP) != 0) return FL_E_ARG;
-  const int64_t nwords = (int64_t)n * (k / 8);
-  const int64_t blocks = (nwords + 255) / 256;
+  const int64_t nchunks = (int64_t)n * (k / 32);
+  const int64_t blocks = (nchunks + 255) / 256;
   if (blocks > 0x7FFFFFFF) return FL_E_ARG;
   hipLaunchKernelGGL(k_dequant, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), q, sz,
-                     out, nwords);
+                     out, nchunks);
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
 

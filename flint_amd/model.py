@@ -131,6 +131,16 @@ class Transformer:
         except Exception:
             pass
 
+    def activations(self):
+        """Diagnostics: the last step's activations (h, qkv pair-interleaved, attn, act) as views
+        of the library's scratch (valid until the next launch)."""
+        ptrs = [_lib.ctypes.c_void_p() for _ in range(4)]
+        _lib.call("fl_state_buffers", self._state, *[_lib.ctypes.byref(p) for p in ptrs])
+        a = self.config
+        sizes = [a.dim, a.qkv_dim, a.dim, a.intermediate_size]
+        return {k: _lib.device_view(p.value, n, torch.bfloat16)
+                for k, p, n in zip(("h", "qkv", "attn", "act"), ptrs, sizes)}
+
     def check(self):
         """Raise if a kernel recorded an error (synchronises)."""
         _lib.call("fl_state_check", self._state, _lib.stream_ptr())

@@ -1,0 +1,62 @@
+"""Per-phase timing of the persistent decode kernel from in-kernel timestamps.
+
+Every workgroup stamps the 100 MHz real-time clock at kernel start, when each phase's inputs
+have arrived ("ready") and when its epilogue is done, then when the final norm's input has
+arrived and at the end. This turns them into per-phase input wait (time spent polling for the
+previous phase's tagged outputs: the synchronisation cost) and compute time, averaged over
+layers, plus the step total.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+
+TICK_US = 0.01  # 100 MHz
+# per layer: P1 ready, P1 done, P2 done, P3 ready, P3 done, P4 ready, P4 done, P5 ready, P5 done
+PER_LAYER = 9
+
+
+def slots_per_launch(n_layer):
+    return 3 + PER_LAYER * n_layer
+
+
+def enable(model, slots=None):
+    """Attach a timestamp buffer to the model's decode state; returns (buf, grid, slots)."""
+    slots = slots or slots_per_launch(model.config.n_layer)
+    grid = ctypes.c_int32()
+    ncu = ctypes.c_int32()
+    _lib.call("fl_device_info", ctypes.byref(ncu), None)
+    buf = torch.zeros(max(ncu.value, 1) * slots, dtype=torch.int64, device=model.device)
+    _lib.call("fl_state_profile", model._state, _lib.ptr(buf), slots, ctypes.byref(grid))
+    return buf, grid.value, slots
+
+
+def disable(model):
+    _lib.call("fl_state_profile", model._state, None, 0, None)
+
+
+def analyse(buf, grid, slots, n_layer):
+    t = buf[: grid * slots].view(grid, slots).double().cpu() * TICK_US
+    t = t - t[:, :1].min()
+    L = n_layer
+    lay = t[:, 1:1 + PER_LAYER * L].view(grid, L, PER_LAYER)
+    prev_done = torch.cat([t[:, :1], lay[:, :-1, 8]], dim=1)          # [grid, L]
+    rows = {
+        "qkv+rope": (lay[..., 0] - prev_done, lay[..., 1] - lay[..., 0]),
+        "attention": (None, lay[..., 2] - lay[..., 1]),
+        "o+resid": (lay[..., 3] - lay[..., 2], lay[..., 4] - lay[..., 3]),
+        "gateup+swiglu": (lay[..., 5] - lay[..., 4], lay[..., 6] - lay[..., 5]),
+        "down+resid": (lay[..., 7] - lay[..., 6], lay[..., 8] - lay[..., 7]),
+    }
+    out = {"total_us": float(t[:, -1].max()), "phases": {}}
+    for name, (wait, comp) in rows.items():
+        d = {"compute_mean_us": float(comp.mean()), "compute_max_us": float(comp.max(0).values.mean())}
+        if wait is not None:
+            d["input_wait_mean_us"] = float(wait.mean())
+        out["phases"][name] = d
+    layer_end = lay[..., 8].max(0).values
+    out["layer_critical_us"] = float((layer_end[1:] - layer_end[:-1]).mean()) if L > 1 else None
+    out["final_norm_wait_us"] = float((t[:, 1 + PER_LAYER * L] - lay[:, -1, 8]).mean())
+    out["lm_head_us"] = float((t[:, 2 + PER_LAYER * L] - t[:, 1 + PER_LAYER * L]).max())
+    return out

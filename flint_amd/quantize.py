@@ -76,11 +76,24 @@ def gemm_int4(q, sz, x, y=None):
     return y
 
 
+# bit position of element e (0..7) inside its packed word: element 2i at 4i, 2i+1 at 16+4i
+NIBBLE_SHIFT = [0, 16, 4, 20, 8, 24, 12, 28]
+
+
 def unpack_q(q):
     """int32 [N, K/8] packed words -> int32 [N, K] values in [0, 15] (host-side inspection)."""
-    shifts = torch.arange(0, 32, 4, device=q.device, dtype=torch.int32)
+    shifts = torch.tensor(NIBBLE_SHIFT, device=q.device, dtype=torch.int32)
     v = (q.unsqueeze(-1) >> shifts) & 0xF
     return v.reshape(q.shape[0], q.shape[1] * 8)
+
+
+def pack_q(vals):
+    """int32 [N, K] values in [0, 15] -> int32 [N, K/8] packed words (inverse of unpack_q)."""
+    n, k = vals.shape
+    v = vals.to(torch.int64).view(n, k // 8, 8)
+    shifts = torch.tensor(NIBBLE_SHIFT, device=vals.device, dtype=torch.int64)
+    words = (v << shifts).sum(-1)
+    return torch.where(words >= 2 ** 31, words - 2 ** 32, words).to(torch.int32)
 
 
 def unpack_sz(sz):

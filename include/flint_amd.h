@@ -7,7 +7,8 @@
  * FL_E* code. Nothing here is thread-safe for a shared fl_state.
  *
  * Weight layout (owned by this library; produced by fl_quantize_int4):
- *   q  : uint32 [N, K/8]    row-major; element k of a row sits in word k/8 at bits 4*(k%8)
+ *   q  : uint32 [N, K/8]    row-major; word j of a row holds elements 8j..8j+7, element
+ *                           8j+2i at bits 4i and element 8j+2i+1 at bits 16+4i (i = 0..3)
  *   sz : uint32 [N, K/128]  per (row, 128-group): bits 0..15 = scale (bf16),
  *                           bits 16..31 = zero (bf16)
  * Values follow gpt-fast's asymmetric group quantisation
@@ -102,6 +103,15 @@ int fl_state_create(const fl_model_desc* desc, int32_t max_seq, uint16_t* k_cach
 int fl_state_destroy(fl_state* st);
 /* Zero all scratch counters (not the KV cache). */
 int fl_state_reset(fl_state* st, void* stream);
+/* Diagnostics, no counterpart in the reference: when buf (device, uint64 [grid * slots_per_wg])
+ * is non-NULL, every later decode launch writes per-workgroup timestamps of the 100 MHz
+ * real-time clock: slot 0 at kernel start, then (arrive, leave) for every grid barrier, then
+ * the end of the LM head. NULL disables. *grid receives the number of workgroups. */
+int fl_state_profile(fl_state* st, uint64_t* buf, int32_t slots_per_wg, int32_t* grid);
+/* Diagnostics, no counterpart in the reference: device pointers of the last launch's
+ * activations: residual h [D], this step's q/k/v (pair-interleaved: word hh*32+i holds dims i and
+ * i+32 of head hh; heads [q | k | v]), attention output [D], SwiGLU output [F] (bf16). */
+int fl_state_buffers(fl_state* st, uint16_t** h, uint16_t** qkv, uint16_t** attn, uint16_t** act);
 /* Last error recorded by a kernel (FL_OK or FL_E_TIMEOUT); synchronises the stream. */
 int fl_state_check(fl_state* st, void* stream);
 

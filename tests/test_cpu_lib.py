@@ -67,13 +67,14 @@ def test_storage_permutations():
 
 
 def test_unpack_helpers_roundtrip():
-    from flint_amd.quantize import unpack_q, unpack_sz
+    from flint_amd.quantize import pack_q, unpack_q, unpack_sz
     vals = torch.randint(0, 16, (4, 64), dtype=torch.int32)
-    words = torch.zeros(4, 8, dtype=torch.int64)
-    for e in range(8):
-        words |= vals[:, e::8].to(torch.int64) << (4 * e)
-    words = torch.where(words >= 2 ** 31, words - 2 ** 32, words).to(torch.int32)
+    words = pack_q(vals)
     assert torch.equal(unpack_q(words), vals)
+    # element 2i of a word at bits 4i, element 2i+1 at bits 16+4i
+    one = torch.zeros(1, 8, dtype=torch.int32)
+    one[0, 3] = 5
+    assert int(pack_q(one)[0, 0]) == 5 << 20
     s = torch.randn(3, 2).to(torch.bfloat16)
     z = torch.randn(3, 2).to(torch.bfloat16)
     packed = (s.view(torch.int16).to(torch.int32) & 0xFFFF) | (z.view(torch.int16).to(torch.int32) << 16)
