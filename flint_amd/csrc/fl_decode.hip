@@ -281,7 +281,8 @@ __device__ __forceinline__ void attn_slices(int T, int NKV, int G, int& nsl, int
 
 template <int QPG>
 __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
-                                float* ws) {
+                                float* ws, int& slot) {
+  int t_in = 0, t_loop = 0, t_merge = 0;  // extra stamps: inputs ready, chunks done, merged
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = gridDim.x;
   const int T = p.pos + 1;
@@ -309,6 +310,7 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
       dst[j + 32] = bfhi((uint32_t)v);
     }
     __syncthreads();
+    if (!t_in) { t_in = 1; stamp(p, slot); }
     float m[QPG], lsum[QPG], acc[QPG][4];
 #pragma unroll
     for (int h = 0; h < QPG; ++h) {
@@ -403,6 +405,7 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
       wave_sync();  // ps is rewritten by the next chunk
     }
     // per-wave partial (m, l, acc[64]) -> LDS
+    if (!t_loop) { t_loop = 1; stamp(p, slot); }
 #pragma unroll
     for (int h = 0; h < QPG; ++h)
 #pragma unroll
@@ -474,7 +477,11 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
       }
     }
     __syncthreads();  // LDS tiles are reused by the next unit
+    if (!t_merge) { t_merge = 1; stamp(p, slot); }
   }
+  if (!t_in) stamp(p, slot);
+  if (!t_loop) stamp(p, slot);
+  if (!t_merge) stamp(p, slot);
 }
 
 // tagged h[r0 .. r0+rows) = bf16(h + bf16(bf16(acc) * rm)), two rows per thread (r0, rows even)
@@ -572,7 +579,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     // ---------------- P2: GQA flash-decode attention ----------------
     // (the O weights are requested after it: attention needs the registers, and the O phase
     // waits for every group's attention output anyway)
-    attention_phase<QPG>(p, l, t_qkv, t_attn, ws);
+    attention_phase<QPG>(p, l, t_qkv, t_attn, ws, slot);
     stamp(p, slot);
     row_range(D, wg, G, r0, rows);
     gemv_load(p.w.wo_q + (size_t)l * D * (D >> 3), p.w.wo_sz + (size_t)l * D * (D >> 7), r0, rows,

@@ -13,8 +13,9 @@ import torch
 from . import _lib
 
 TICK_US = 0.01  # 100 MHz
-# per layer: P1 ready, P1 done, P2 done, P3 ready, P3 done, P4 ready, P4 done, P5 ready, P5 done
-PER_LAYER = 9
+# per layer: P1 ready, P1 done, P2 inputs, P2 chunks, P2 merged, P2 done, P3 ready, P3 done,
+#            P4 ready, P4 done, P5 ready, P5 done
+PER_LAYER = 12
 
 
 def slots_per_launch(n_layer):
@@ -41,22 +42,33 @@ def analyse(buf, grid, slots, n_layer):
     t = t - t[:, :1].min()
     L = n_layer
     lay = t[:, 1:1 + PER_LAYER * L].view(grid, L, PER_LAYER)
-    prev_done = torch.cat([t[:, :1], lay[:, :-1, 8]], dim=1)          # [grid, L]
+    prev_done = torch.cat([t[:, :1], lay[:, :-1, 11]], dim=1)         # [grid, L]
     rows = {
         "qkv+rope": (lay[..., 0] - prev_done, lay[..., 1] - lay[..., 0]),
-        "attention": (None, lay[..., 2] - lay[..., 1]),
-        "o+resid": (lay[..., 3] - lay[..., 2], lay[..., 4] - lay[..., 3]),
-        "gateup+swiglu": (lay[..., 5] - lay[..., 4], lay[..., 6] - lay[..., 5]),
-        "down+resid": (lay[..., 7] - lay[..., 6], lay[..., 8] - lay[..., 7]),
+        "attention": (lay[..., 2] - lay[..., 1], lay[..., 5] - lay[..., 2]),
+        "o+resid": (lay[..., 6] - lay[..., 5], lay[..., 7] - lay[..., 6]),
+        "gateup+swiglu": (lay[..., 8] - lay[..., 7], lay[..., 9] - lay[..., 8]),
+        "down+resid": (lay[..., 10] - lay[..., 9], lay[..., 11] - lay[..., 10]),
     }
+    att = t.new_zeros(0)
+    busy = (lay[..., 5] - lay[..., 1]) > 0.5   # workgroups that ran an attention unit
+    if bool(busy.any()):
+        out_att = {
+            "inputs_wait_us": float((lay[..., 2] - lay[..., 1])[busy].mean()),
+            "chunks_us": float((lay[..., 3] - lay[..., 2])[busy].mean()),
+            "merge_us": float((lay[..., 4] - lay[..., 3])[busy].mean()),
+        }
+    else:
+        out_att = {}
     out = {"total_us": float(t[:, -1].max()), "phases": {}}
     for name, (wait, comp) in rows.items():
         d = {"compute_mean_us": float(comp.mean()), "compute_max_us": float(comp.max(0).values.mean())}
         if wait is not None:
             d["input_wait_mean_us"] = float(wait.mean())
         out["phases"][name] = d
-    layer_end = lay[..., 8].max(0).values
+    out["attention_units"] = out_att
+    layer_end = lay[..., 11].max(0).values
     out["layer_critical_us"] = float((layer_end[1:] - layer_end[:-1]).mean()) if L > 1 else None
-    out["final_norm_wait_us"] = float((t[:, 1 + PER_LAYER * L] - lay[:, -1, 8]).mean())
+    out["final_norm_wait_us"] = float((t[:, 1 + PER_LAYER * L] - lay[:, -1, 11]).mean())
     out["lm_head_us"] = float((t[:, 2 + PER_LAYER * L] - t[:, 1 + PER_LAYER * L]).max())
     return out
