@@ -178,25 +178,107 @@ __device__ __forceinline__ unsigned long long ld_coh_u64(const unsigned long lon
   return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
 }
+// Workgroup barrier that orders LDS accesses only. __syncthreads also waits for every global
+// load and store the wave has in flight (prefetched weights, published activations); this one
+// does not, so a barrier between LDS producers and consumers never stalls on HBM traffic.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // wait until every memory operation this wave issued has completed (stores acknowledged at
 // device scope); required before signalling other workgroups.
 __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
-// ---- wave reductions (wave64) ---------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// ---- cross-lane exchanges (wave64, VALU only) -------------------------------------------------
+// __shfl_xor lowers to ds_bpermute, an LDS round trip per step. These use DPP lane patterns
+// (within a 16-lane row) and gfx950's v_permlane16/32_swap (across rows) instead: one VALU op
+// each. Every helper returns, in lane i, the value of lane i ^ mask.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL,
+                                                    0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_xor1(float v) { return dpp_f<0xB1>(v); }   // quad_perm 1,0,3,2
+__device__ __forceinline__ float lane_xor2(float v) { return dpp_f<0x4E>(v); }   // quad_perm 2,3,0,1
+__device__ __forceinline__ float lane_xor8(float v) { return dpp_f<0x128>(v); }  // row_ror:8
+__device__ __forceinline__ float lane_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  // r[0]: odd rows replaced by the even rows below them, r[1]: even rows by the odd rows above
+  return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
+// v(i) + v(i ^ 16) and v(i) + v(i ^ 32) (and max): both swap results are the lane pair, so
+// one add gives the pair total in both lanes without a select
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// lane 7 - i within each group of 8 (after a 4-lane all-reduce, the other half's value)
+__device__ __forceinline__ float lane_half_mirror(float v) { return dpp_f<0x141>(v); }
+// lane 15 - i within each row of 16 (after an 8-lane all-reduce, the other half's value)
+__device__ __forceinline__ float lane_mirror(float v) { return dpp_f<0x140>(v); }
+
+// all-reduce over aligned groups of `width` lanes (width a power of two <= 64, wave-uniform).
+// Every lane of a group ends with the bit-identical result (each step adds two values whose
+// operands are the same pair in every lane). Fixed order.
+__device__ __forceinline__ float group_sum(float v, int width) {
+  if (width >= 2) v += lane_xor1(v);
+  if (width >= 4) v += lane_xor2(v);
+  if (width >= 8) v += lane_half_mirror(v);
+  if (width >= 16) v += lane_mirror(v);
+  if (width >= 32) v = xor16_sum(v);
+  if (width >= 64) v = xor32_sum(v);
   return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += lane_xor1(v);
+  v += lane_xor2(v);
+  v += lane_half_mirror(v);
+  v += lane_mirror(v);
+  v = xor16_sum(v);
+  return xor32_sum(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, lane_xor1(v));
+  v = fmaxf(v, lane_xor2(v));
+  v = fmaxf(v, lane_half_mirror(v));
+  v = fmaxf(v, lane_mirror(v));
+  v = xor16_max(v);
+  return xor32_max(v);
 }
-// sum over aligned groups of `width` lanes (width a power of two <= 64); fixed order
-__device__ __forceinline__ float group_sum(float v, int width) {
-  for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+// sum over the 8 lanes of a group of 8 (lanes 8a .. 8a+7)
+__device__ __forceinline__ float sum8(float v) {
+  v += lane_xor1(v);
+  v += lane_xor2(v);
+  return v + lane_half_mirror(v);
+}
+// sum / max over the lanes that share bits 0..2 of the lane id (lane i, i^8, ..., i^56)
+__device__ __forceinline__ float sum_stride8(float v) {
+  v += lane_xor8(v);
+  v = xor16_sum(v);
+  return xor32_sum(v);
+}
+__device__ __forceinline__ float max_stride8(float v) {
+  v = fmaxf(v, lane_xor8(v));
+  v = xor16_max(v);
+  return xor32_max(v);
 }
 
 // ---- argmax key: larger key = larger value, then smaller index --------------------------------

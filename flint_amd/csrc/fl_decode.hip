@@ -39,16 +39,12 @@ constexpr int MC_QKV = 4, MC_O = 4, MC_GU = 12, MC_D = 8;
 constexpr int MAXC = MC_GU;
 constexpr int XS_MAX = 8192;         // max staged activation length (bf16 elements)
 constexpr int ROWS_MAX = 256;        // max rows per workgroup in one GEMV phase
-constexpr int QPG_MAX = 8;           // max query heads per kv group
-constexpr int KC = 64;               // keys per attention chunk (one per lane)
 constexpr int LM_MAXC = 6;           // max 16-byte chunks per lane of one LM-head row (D <= 3072)
 constexpr int LM_RB = 2;             // LM-head rows per wave per batch
 constexpr int MAX_SLICES = 64;       // attention key slices per kv group
 constexpr unsigned long long SPIN_TICKS = 200000000ull;  // 2 s of the 100 MHz realtime clock
-// attention LDS (floats): q tiles, new k / v rows, per-wave p tiles and per-wave partials
-constexpr int ATT_Q = QPG_MAX * 64;
-constexpr int ATT_WP = QPG_MAX * 66;
-constexpr int ATT_FLOATS = ATT_Q + 128 + NWAVE * (QPG_MAX * 64 + ATT_WP);
+// attention LDS (floats): bf16 q / new k / new v rows, then per-wave partials
+constexpr int ATT_FLOATS = 96 + NWAVE * 66;
 constexpr int WS_FLOATS = (MAXC * NT > ATT_FLOATS) ? MAXC * NT : ATT_FLOATS;
 
 struct DecodeParams {
@@ -56,8 +52,7 @@ struct DecodeParams {
   uint16_t *kc, *vc;           // [NL, NKV, S, 64] bf16 cache
   uint32_t *h, *attn, *act;    // tagged words: bf16 value | tag << 16
   unsigned long long* qkv;     // tagged NEOX pairs: dim i | dim i+32 << 16 | tag << 32
-  float* part;                 // attention slice partials
-  uint32_t* cnt;               // [NKV] slice arrivals
+  unsigned long long* part;    // attention slice partials (tagged fp32 words)
   unsigned long long* amax;    // argmax key
   uint32_t* done;              // final arrivals
   int32_t* err;                // abort flag (spin timeout / bad token)
@@ -66,11 +61,26 @@ struct DecodeParams {
   float* logits;
   uint16_t* feat;
   int D, NH, NKV, F, V, NL, S, pos;
+  int att_spw;                 // attention: target 8-key steps per wave per slice
   float eps, emb_mult, attn_scale, resid_mult, logits_scaling;
   uint32_t epoch;              // epoch of this launch's first phase (5 per layer)
   unsigned long long* prof;    // optional per-workgroup phase timestamps (100 MHz clock)
   int prof_slots;
 };
+
+// threadIdx.x / gridDim.x through an empty asm. Index math derived from them is then redone
+// where it is used instead of being hoisted out of the layer loop, where dozens of per-chunk
+// offsets and predicates would stay live in registers for the whole launch.
+__device__ __forceinline__ int tid_here() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+__device__ __forceinline__ int grid_here() {
+  int g = gridDim.x;
+  asm volatile("" : "+s"(g));
+  return g;
+}
 
 __device__ __forceinline__ uint32_t tag_of(uint32_t epoch) { return epoch % 65535u + 1u; }
 
@@ -138,10 +148,10 @@ __device__ __forceinline__ void wave_sync() {
 // x^2 of this thread; xs <- bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w).
 __device__ void norm_finish(float ss, const uint16_t* __restrict__ nw, int D, float eps,
                             uint16_t* xs, float* red) {
-  const int tid = threadIdx.x;
+  const int tid = tid_here();
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
-  __syncthreads();
+  lds_barrier();
   float tot = 0.0f;
 #pragma unroll
   for (int w = 0; w < NWAVE; ++w) tot += red[w];
@@ -159,7 +169,7 @@ __device__ void norm_finish(float ss, const uint16_t* __restrict__ nw, int D, fl
     }
     reinterpret_cast<uint4*>(xs)[i] = make_uint4(o[0], o[1], o[2], o[3]);
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // xs = RMSNorm(bf16(embed_row * mult))  (engine/model.py:138 then :237-242)
@@ -167,7 +177,7 @@ __device__ void norm_embed(const uint16_t* __restrict__ erow, float mult,
                            const uint16_t* __restrict__ nw, int D, float eps, uint16_t* xs,
                            float* red) {
   float ss = 0.0f;
-  for (int i = threadIdx.x; i < (D >> 3); i += NT) {
+  for (int i = tid_here(); i < (D >> 3); i += NT) {
     const uint4 v = reinterpret_cast<const uint4*>(erow)[i];
     const uint32_t in[4] = {v.x, v.y, v.z, v.w};
     uint32_t o[4];
@@ -187,7 +197,7 @@ __device__ void norm_embed(const uint16_t* __restrict__ erow, float mult,
 __device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t tag,
                             const uint16_t* __restrict__ nw, uint16_t* xs, float* red) {
   float ss = 0.0f;
-  for (int i = threadIdx.x; i < (p.D >> 2); i += NT) {
+  for (int i = tid_here(); i < (p.D >> 2); i += NT) {
     const uint4 v = wait4(p, h + 4 * i, tag);
     const float a0 = bflo(v.x), a1 = bflo(v.y), a2 = bflo(v.z), a3 = bflo(v.w);
     ss += a0 * a0;
@@ -197,19 +207,19 @@ __device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t t
     reinterpret_cast<uint2*>(xs)[i] =
         make_uint2((v.x & 0xFFFFu) | (v.y << 16), (v.z & 0xFFFFu) | (v.w << 16));
   }
-  __syncthreads();
+  lds_barrier();
   norm_finish(ss, nw, p.D, p.eps, xs, red);
 }
 
 // xs = values of the tagged vector src[0..n) once all carry `tag`
 __device__ void stage_tagged(const DecodeParams& p, const uint32_t* src, int n, uint32_t tag,
                              uint16_t* xs) {
-  for (int i = threadIdx.x; i < (n >> 2); i += NT) {
+  for (int i = tid_here(); i < (n >> 2); i += NT) {
     const uint4 v = wait4(p, src + 4 * i, tag);
     reinterpret_cast<uint2*>(xs)[i] =
         make_uint2((v.x & 0xFFFFu) | (v.y << 16), (v.z & 0xFFFFu) | (v.w << 16));
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // Issue this workgroup's weight chunks for rows [r0, r0+rows) of a [N, K] int4 matrix.
@@ -220,9 +230,10 @@ __device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ q,
   const int total = rows * (K >> 5);
   const uint4* wb = reinterpret_cast<const uint4*>(q + (size_t)r0 * (K >> 3));
   const uint32_t* sb = sz + (size_t)r0 * (K >> 7);
+  const int tid = tid_here();
 #pragma unroll
   for (int i = 0; i < MC; ++i) {
-    const int f = threadIdx.x + i * NT;
+    const int f = tid + i * NT;
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
     uint32_t z = 0u;
     if (f < total) {
@@ -239,7 +250,7 @@ template <int MC>
 __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
                                              int rows, int K, const uint16_t* xs, float* part,
                                              float* rs) {
-  const int tid = threadIdx.x;
+  const int tid = tid_here();
   const int cpr = K >> 5;
   const int total = rows * cpr;
   int c = tid % cpr;
@@ -253,7 +264,7 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
     if (c >= cpr) c -= cpr;
     __builtin_amdgcn_sched_barrier(0);  // keep one chunk's temporaries live at a time
   }
-  __syncthreads();
+  lds_barrier();
   int L = 64;
   while (L * rows > NT) L >>= 1;
   const int row = tid / L, li = tid % L;
@@ -262,232 +273,217 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
     for (int j = li; j < cpr; j += L) acc += part[row * cpr + j];
   acc = group_sum(acc, L);
   if (row < rows && li == 0) rs[row] = acc;
-  __syncthreads();
+  lds_barrier();
 }
 
-// slices of the key range [0, T) for one kv group: (number of slices, 64-key chunks per slice)
-__device__ __forceinline__ void attn_slices(int T, int NKV, int G, int& nsl, int& cps) {
-  const int nch = (T + KC - 1) / KC;
-  if (nch <= 2 * NWAVE) {
-    nsl = 1;
-  } else {
-    nsl = (nch + NWAVE - 1) / NWAVE;
-    const int cap = max(1, min(MAX_SLICES, G / NKV));
-    if (nsl > cap) nsl = cap;
-  }
-  cps = (nch + nsl - 1) / nsl;
-  nsl = (nch + cps - 1) / cps;
+// Key slices of one query head. Keys are processed in 8-key steps (8 keys x 64 dims: one
+// 16-byte K load and one 16-byte V load per lane); a slice is one workgroup, whose 8 waves take
+// interleaved steps so that each group of 8 steps covers 64 consecutive keys. `spw` is the
+// target number of steps per wave: slices = ceil(steps / (8 * spw)), at most G / NH.
+__device__ __forceinline__ void attn_slices(int T, int NH, int G, int spw, int& nsl, int& sps) {
+  const int ns = (T + 7) >> 3;
+  const int per = NWAVE * spw;
+  nsl = (ns + per - 1) / per;
+  const int cap = max(1, min(MAX_SLICES, G / NH));
+  if (nsl > cap) nsl = cap;
+  sps = (ns + nsl - 1) / nsl;
+  nsl = (ns + sps - 1) / sps;
 }
 
-template <int QPG>
+// GQA flash-decode attention of one layer (engine/model.py:171-179: q.k^T * scale, softmax and
+// p.v in fp32 over keys 0..pos, bf16 output; head h reads kv group h / (NH / NKV)).
+// One workgroup per (query head, key slice): u = (j * nsl + sl) * NKV + g for head j of kv group
+// g, so all heads of a group run on workgroups u = g (mod NKV) -- with NKV = 8 and workgroups
+// dealt round-robin over the 8 XCDs, a group's K/V rows are fetched into one L2. At short
+// contexts every head is one slice, so no workgroup waits for another.
+// Lane (kk = lane / 8, ds = lane % 8) of a wave holds dims 8ds..8ds+7 of key kk of each step:
+// q . k is 4 dot2 plus a 3-step DPP sum over the key's 8 lanes, p.v is 8 FMAs, and the output
+// is summed over the 8 keys once at the end. The slice's K / V rows are requested before the
+// wait for this launch's q, so the cache reads overlap it; the new key / value (position pos,
+// appended to the cache by this same launch) come from the tagged q/k/v words instead. Softmax
+// uses the exact max of each round of RB steps with an online rescale between rounds. Waves
+// merge through LDS; slices > 0 publish (m, l, o) as tagged 64-bit words and slice 0 merges
+// them in slice order.
 __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
-                                float* ws, int& slot) {
-  int t_in = 0, t_loop = 0, t_merge = 0;  // extra stamps: inputs ready, chunks done, merged
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int G = gridDim.x;
+                                uint32_t ptag, float* ws, int& slot) {
+  constexpr int RB = 16;  // steps per wave per round (K/V held in registers)
+  const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+  const int kk = lane >> 3, ds = lane & 7;
   const int T = p.pos + 1;
-  int nsl, cps;
-  attn_slices(T, p.NKV, G, nsl, cps);
-  const int nch = (T + KC - 1) / KC;
-  float* qs = ws;                                           // [QPG][64] this step's q of the group
-  float* kn = qs + ATT_Q;                                   // [64] this step's k of the group
-  float* vn = kn + 64;                                      // [64] this step's v of the group
-  float* ps = vn + 64 + wave * (QPG_MAX * 64);              // per-wave p tile
-  float* wpart = vn + 64 + NWAVE * (QPG_MAX * 64);          // [NWAVE][QPG][66]
-  __shared__ uint32_t s_old;
-  for (int u = blockIdx.x; u < p.NKV * nsl; u += G) {
-    const int g = u / nsl, sl = u - g * nsl;
-    const size_t cbase = (size_t)(l * p.NKV + g) * p.S * 64;
-    const uint16_t* kb = p.kc + cbase;
-    const uint16_t* vb = p.vc + cbase;
-    // q / k / v of group g from this launch's QKV phase (tagged pairs)
-    for (int i = tid; i < (QPG + 2) * 32; i += NT) {
-      const int hq = i >> 5, j = i & 31;
-      const int hh = hq < QPG ? g * QPG + hq : (hq == QPG ? p.NH + g : p.NH + p.NKV + g);
-      const unsigned long long v = wait_pair(p, p.qkv + hh * 32 + j, qtag);
-      float* dst = hq < QPG ? qs + hq * 64 : (hq == QPG ? kn : vn);
-      dst[j] = bflo((uint32_t)v);
-      dst[j + 32] = bfhi((uint32_t)v);
-    }
-    __syncthreads();
-    if (!t_in) { t_in = 1; stamp(p, slot); }
-    float m[QPG], lsum[QPG], acc[QPG][4];
-#pragma unroll
-    for (int h = 0; h < QPG; ++h) {
-      m[h] = -INFINITY;
-      lsum[h] = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc[h][e] = 0.0f;
-    }
-    const int j4 = lane & 15, kg = lane >> 4;
-    const int c_end = min(nch, (sl + 1) * cps);
-    for (int c = sl * cps + wave; c < c_end; c += NWAVE) {
-      const int t0 = c * KC;
-      const int t = t0 + lane;
-      const bool valid = t < T;
-      const bool is_new = t == p.pos;
-      // issue this chunk's K row loads and V slice loads together (one memory round trip)
-      uint4 kv[8];
-      if (valid && !is_new) {
-        const uint4* kr = reinterpret_cast<const uint4*>(kb + (size_t)t * 64);
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) kv[jj] = kr[jj];
-      }
-      uint2 vv[KC / 4];
-#pragma unroll
-      for (int kk = 0; kk < KC / 4; ++kk) {
-        const int tk = t0 + kg + 4 * kk;
-        vv[kk] = make_uint2(0u, 0u);
-        if (tk < T && tk != p.pos)
-          vv[kk] = *reinterpret_cast<const uint2*>(vb + (size_t)tk * 64 + j4 * 4);
-      }
-      float s[QPG];
-#pragma unroll
-      for (int h = 0; h < QPG; ++h) s[h] = 0.0f;
-      if (valid && !is_new) {
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const float kf[8] = {bflo(kv[jj].x), bfhi(kv[jj].x), bflo(kv[jj].y), bfhi(kv[jj].y),
-                               bflo(kv[jj].z), bfhi(kv[jj].z), bflo(kv[jj].w), bfhi(kv[jj].w)};
-#pragma unroll
-          for (int h = 0; h < QPG; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) s[h] = __builtin_fmaf(qs[h * 64 + jj * 8 + e], kf[e], s[h]);
-          __builtin_amdgcn_sched_barrier(0);  // bound the q values held in registers
-        }
-      }
-      if (is_new) {
-        for (int d = 0; d < 64; ++d) {
-          const float kd = kn[d];
-#pragma unroll
-          for (int h = 0; h < QPG; ++h) s[h] = __builtin_fmaf(qs[h * 64 + d], kd, s[h]);
-        }
-      }
-      // online softmax update (per head; m and lsum are wave-uniform)
-      float corr[QPG];
-#pragma unroll
-      for (int h = 0; h < QPG; ++h) {
-        const float sv = valid ? s[h] * p.attn_scale : -INFINITY;
-        const float mc = wave_max(sv);
-        const float mn = fmaxf(m[h], mc);
-        corr[h] = expf(m[h] - mn);  // 0 on the first chunk (m = -inf)
-        const float pv = valid ? expf(sv - mn) : 0.0f;
-        lsum[h] = lsum[h] * corr[h] + wave_sum(pv);
-        m[h] = mn;
-        ps[h * 64 + lane] = pv;
-      }
-      wave_sync();
-#pragma unroll
-      for (int h = 0; h < QPG; ++h)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[h][e] *= corr[h];
-#pragma unroll
-      for (int kk = 0; kk < KC / 4; ++kk) {
-        const int tt = kg + 4 * kk;
-        const float vf[4] = {bflo(vv[kk].x), bfhi(vv[kk].x), bflo(vv[kk].y), bfhi(vv[kk].y)};
-#pragma unroll
-        for (int h = 0; h < QPG; ++h) {
-          const float pw = ps[h * 64 + tt];  // 0 for keys beyond T; the new key is added below
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[h][e] = __builtin_fmaf(pw, vf[e], acc[h][e]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (p.pos >= t0 && p.pos < t0 + KC && kg == ((p.pos - t0) & 3)) {  // the new key's value
-        const int tt = p.pos - t0;
-#pragma unroll
-        for (int h = 0; h < QPG; ++h) {
-          const float pw = ps[h * 64 + tt];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[h][e] = __builtin_fmaf(pw, vn[j4 * 4 + e], acc[h][e]);
-        }
-      }
-      wave_sync();  // ps is rewritten by the next chunk
-    }
-    // per-wave partial (m, l, acc[64]) -> LDS
-    if (!t_loop) { t_loop = 1; stamp(p, slot); }
-#pragma unroll
-    for (int h = 0; h < QPG; ++h)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float v = acc[h][e];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        acc[h][e] = v;
-      }
-    float* mywp = wpart + wave * ATT_WP;
-    if (kg == 0) {
-#pragma unroll
-      for (int h = 0; h < QPG; ++h)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mywp[h * 66 + 2 + j4 * 4 + e] = acc[h][e];
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int h = 0; h < QPG; ++h) {
-        mywp[h * 66] = m[h];
-        mywp[h * 66 + 1] = lsum[h];
-      }
-    }
-    __syncthreads();
-    // merge the waves in a fixed order: thread (head hm, dim d)
-    float M = -INFINITY, Ls = 0.0f, O = 0.0f;
-    const int hm = tid >> 6, d = tid & 63;
-    if (hm < QPG) {
-      for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, wpart[w * ATT_WP + hm * 66]);
-      for (int w = 0; w < NWAVE; ++w) {
-        const float* wp = wpart + w * ATT_WP + hm * 66;
-        const float e = (wp[0] == -INFINITY) ? 0.0f : expf(wp[0] - M);
-        Ls += wp[1] * e;
-        O += wp[2 + d] * e;
-      }
-    }
-    if (nsl == 1) {
-      if (hm < QPG) st_coh_u32(p.attn + (g * QPG + hm) * 64 + d, f2bf(O / Ls) | (otag << 16));
-    } else {
-      // slice partial -> global; the last slice of the group to arrive merges all of them
-      float* pp = p.part + ((size_t)g * MAX_SLICES + sl) * QPG * 66;
-      if (hm < QPG) {
-        if (d == 0) {
-          st_coh_f32(pp + hm * 66, M);
-          st_coh_f32(pp + hm * 66 + 1, Ls);
-        }
-        st_coh_f32(pp + hm * 66 + 2 + d, O);
-      }
-      wait_mem();
-      __syncthreads();
-      if (tid == 0)
-        s_old = __hip_atomic_fetch_add(p.cnt + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __syncthreads();
-      if (s_old == (uint32_t)(nsl - 1)) {
-        if (hm < QPG) {
-          const float* gp = p.part + (size_t)g * MAX_SLICES * QPG * 66 + hm * 66;
-          float Mg = -INFINITY;
-          for (int c = 0; c < nsl; ++c) Mg = fmaxf(Mg, ld_coh_f32(gp + (size_t)c * QPG * 66));
-          float Lg = 0.0f, Og = 0.0f;
-          for (int c = 0; c < nsl; ++c) {
-            const float* cp = gp + (size_t)c * QPG * 66;
-            const float e = expf(ld_coh_f32(cp) - Mg);
-            Lg += ld_coh_f32(cp + 1) * e;
-            Og += ld_coh_f32(cp + 2 + d) * e;
-          }
-          st_coh_u32(p.attn + (g * QPG + hm) * 64 + d, f2bf(Og / Lg) | (otag << 16));
-        }
-        if (tid == 0) __hip_atomic_store(p.cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    __syncthreads();  // LDS tiles are reused by the next unit
-    if (!t_merge) { t_merge = 1; stamp(p, slot); }
+  const int ns = (T + 7) >> 3;
+  int nsl, sps;
+  attn_slices(T, p.NH, grid_here(), p.att_spw, nsl, sps);
+  const int u = blockIdx.x;
+  if (u >= p.NH * nsl) {
+    stamp(p, slot);
+    stamp(p, slot);
+    stamp(p, slot);
+    return;
   }
-  if (!t_in) stamp(p, slot);
-  if (!t_loop) stamp(p, slot);
-  if (!t_merge) stamp(p, slot);
+  const int g = u % p.NKV, rest = u / p.NKV, sl = rest % nsl, j = rest / nsl;
+  const int hq = g * (p.NH / p.NKV) + j;
+  const int s0 = sl * sps, s1 = min(ns, s0 + sps);
+  const int nrounds = (s1 - s0 + NWAVE * RB - 1) / (NWAVE * RB);
+  const size_t cbase = (size_t)(l * p.NKV + g) * p.S * 64;
+  const uint4* kb = reinterpret_cast<const uint4*>(p.kc + cbase) + ds;  // key t: kb[8 t]
+  const uint4* vb = reinterpret_cast<const uint4*>(p.vc + cbase) + ds;
+
+  uint4 kr[RB], vr[RB];
+  auto issue = [&](int r) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int st = s0 + r * NWAVE * RB + wave + NWAVE * i;
+      if (st < s1) {  // wave-uniform
+        const int tc = min(st * 8 + kk, p.pos);  // keys >= T are masked below
+        kr[i] = kb[(size_t)tc * 8];
+        vr[i] = vb[(size_t)tc * 8];
+      }
+    }
+  };
+  issue(0);
+
+  // LDS: bf16 [3][64]: q of head hq, this step's new k and v of group g
+  uint16_t* qs = reinterpret_cast<uint16_t*>(ws);
+  float* wpart = ws + 96;  // [NWAVE][66]: m, l, o[64] per wave
+  if (tid < 96) {
+    const int r = tid >> 5, jj = tid & 31;
+    const int hh = r == 0 ? hq : (r == 1 ? p.NH + g : p.NH + p.NKV + g);
+    const unsigned long long v = wait_pair(p, p.qkv + hh * 32 + jj, qtag);
+    qs[r * 64 + jj] = (uint16_t)v;               // NEOX pair: dim jj ...
+    qs[r * 64 + jj + 32] = (uint16_t)(v >> 16);  // ... and dim jj + 32
+  }
+  lds_barrier();
+  stamp(p, slot);
+  const uint4 qv = reinterpret_cast<const uint4*>(qs)[ds];
+  const uint4 kn = reinterpret_cast<const uint4*>(qs + 64)[ds];
+  const uint4 vn = reinterpret_cast<const uint4*>(qs + 128)[ds];
+  // scores in the log2 domain: p = 2^(s * scale * log2(e) - m)
+  const float sc = p.attn_scale * 1.4426950408889634f;
+
+  float m = -INFINITY, lsum = 0.0f, o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+  for (int r = 0; r < nrounds; ++r) {
+    if (r > 0) issue(r);
+    float s[RB];
+    float rmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int st = s0 + r * NWAVE * RB + wave + NWAVE * i;
+      s[i] = -INFINITY;
+      if (st < s1) {
+        const int t = st * 8 + kk;
+        const uint4 kv = (t == p.pos) ? kn : kr[i];
+        float a = dot2_bf16(kv.x, qv.x, 0.0f);
+        a = dot2_bf16(kv.y, qv.y, a);
+        a = dot2_bf16(kv.z, qv.z, a);
+        a = dot2_bf16(kv.w, qv.w, a);
+        a = sum8(a);
+        s[i] = (t < T) ? a * sc : -INFINITY;
+        rmax = fmaxf(rmax, s[i]);
+      }
+    }
+    const float mn = fmaxf(m, max_stride8(rmax));
+    const float mu = (mn == -INFINITY) ? 0.0f : mn;  // no valid key yet: every p is 0
+    const float corr = __builtin_amdgcn_exp2f(m - mu);  // 0 while m = -inf
+    lsum *= corr;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= corr;
+    m = mn;
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int st = s0 + r * NWAVE * RB + wave + NWAVE * i;
+      if (st < s1) {
+        const int t = st * 8 + kk;
+        uint4 vv = (t == p.pos) ? vn : vr[i];
+        if (t >= T) vv = make_uint4(0u, 0u, 0u, 0u);  // rows past pos may hold anything
+        const float pw = __builtin_amdgcn_exp2f(s[i] - mu);
+        lsum += pw;
+        o[0] = __builtin_fmaf(pw, bflo(vv.x), o[0]);
+        o[1] = __builtin_fmaf(pw, bfhi(vv.x), o[1]);
+        o[2] = __builtin_fmaf(pw, bflo(vv.y), o[2]);
+        o[3] = __builtin_fmaf(pw, bfhi(vv.y), o[3]);
+        o[4] = __builtin_fmaf(pw, bflo(vv.z), o[4]);
+        o[5] = __builtin_fmaf(pw, bfhi(vv.z), o[5]);
+        o[6] = __builtin_fmaf(pw, bflo(vv.w), o[6]);
+        o[7] = __builtin_fmaf(pw, bfhi(vv.w), o[7]);
+      }
+    }
+  }
+  stamp(p, slot);
+  // sum over the 8 keys of a step (lanes kk = 0..7 with the same ds), then merge the waves
+  lsum = sum_stride8(lsum);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = sum_stride8(o[e]);
+  float* mywp = wpart + wave * 66;
+  if (kk == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mywp[2 + ds * 8 + e] = o[e];
+  }
+  if (lane == 0) {
+    mywp[0] = m;
+    mywp[1] = lsum;
+  }
+  lds_barrier();
+  if (tid < 64) {  // thread d: output dim d, waves merged in a fixed order
+    const int d = tid;
+    float M = -INFINITY, Ls = 0.0f, O = 0.0f;
+    for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, wpart[w * 66]);
+    for (int w = 0; w < NWAVE; ++w) {
+      const float* wp = wpart + w * 66;
+      const float e = (wp[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wp[0] - M);
+      Ls += wp[1] * e;
+      O += wp[2 + d] * e;
+    }
+    unsigned long long* hpart = p.part + (size_t)hq * MAX_SLICES * 66;
+    if (sl > 0) {
+      // publish this slice's (m, l, o) as tagged words: fp32 bits | 32-bit tag << 32
+      unsigned long long* pp = hpart + (size_t)sl * 66;
+      const unsigned long long tg = (unsigned long long)ptag << 32;
+      if (d == 0) {
+        st_coh_u64(pp, (unsigned long long)__float_as_uint(M) | tg);
+        st_coh_u64(pp + 1, (unsigned long long)__float_as_uint(Ls) | tg);
+      }
+      st_coh_u64(pp + 2 + d, (unsigned long long)__float_as_uint(O) | tg);
+    } else {
+      // slice 0 folds in slices 1 .. nsl-1 in order (online rescale), four slices per batch
+      for (int c0 = 1; c0 < nsl; c0 += 4) {
+        unsigned long long wm[4], wl[4], wo[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const unsigned long long* cp = hpart + (size_t)min(c0 + b, nsl - 1) * 66;
+          wm[b] = ld_coh_u64(cp);
+          wl[b] = ld_coh_u64(cp + 1);
+          wo[b] = ld_coh_u64(cp + 2 + d);
+        }
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          if (c0 + b >= nsl) break;
+          const unsigned long long* cp = hpart + (size_t)(c0 + b) * 66;
+          auto ok = [ptag](unsigned long long v) { return (uint32_t)(v >> 32) == ptag; };
+          if (!ok(wm[b])) wm[b] = spin_until(p, wm[b], ok, [cp]() { return ld_coh_u64(cp); });
+          if (!ok(wl[b])) wl[b] = spin_until(p, wl[b], ok, [cp]() { return ld_coh_u64(cp + 1); });
+          if (!ok(wo[b]))
+            wo[b] = spin_until(p, wo[b], ok, [cp, d]() { return ld_coh_u64(cp + 2 + d); });
+          const float mc = __uint_as_float((uint32_t)wm[b]);
+          const float Mn = fmaxf(M, mc);
+          const float ea = __builtin_amdgcn_exp2f(M - Mn), eb = __builtin_amdgcn_exp2f(mc - Mn);
+          Ls = Ls * ea + __uint_as_float((uint32_t)wl[b]) * eb;
+          O = O * ea + __uint_as_float((uint32_t)wo[b]) * eb;
+          M = Mn;
+        }
+      }
+      st_coh_u32(p.attn + hq * 64 + d, f2bf(O / Ls) | (otag << 16));
+    }
+  }
+  lds_barrier();  // LDS is reused by the next phase
+  stamp(p, slot);
 }
 
 // tagged h[r0 .. r0+rows) = bf16(h + bf16(bf16(acc) * rm)), two rows per thread (r0, rows even)
 __device__ __forceinline__ void residual_epilogue(const DecodeParams& p, int r0, int rows,
                                                   const float* rs, uint32_t tag) {
-  const int t = threadIdx.x;
+  const int t = tid_here();
   if (2 * t < rows) {
     unsigned long long* hp = reinterpret_cast<unsigned long long*>(p.h + r0) + t;
     const unsigned long long hv = ld_coh_u64(hp);  // own rows: no tag wait needed
@@ -499,7 +495,6 @@ __device__ __forceinline__ void residual_epilogue(const DecodeParams& p, int r0,
   }
 }
 
-template <int QPG>
 __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
   __shared__ __align__(16) uint16_t xs[XS_MAX];
   __shared__ __align__(16) float ws[WS_FLOATS];
@@ -543,7 +538,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     const uint32_t t_prev = tag_of(e0 - 1), t_qkv = tag_of(e0), t_attn = tag_of(e0 + 1),
                    t_h1 = tag_of(e0 + 2), t_act = tag_of(e0 + 3), t_h2 = tag_of(e0 + 4);
     // ---------------- P1: RMSNorm + QKV + RoPE + KV append ----------------
-    row_range(NQKV, wg, G, r0, rows);
+    row_range(NQKV, wg, grid_here(), r0, rows);
     if (rows > 0) {
       if (l == 0)
         norm_embed(erow, p.emb_mult, p.w.attn_norm, D, p.eps, xs, red);
@@ -579,9 +574,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     // ---------------- P2: GQA flash-decode attention ----------------
     // (the O weights are requested after it: attention needs the registers, and the O phase
     // waits for every group's attention output anyway)
-    attention_phase<QPG>(p, l, t_qkv, t_attn, ws, slot);
+    attention_phase(p, l, t_qkv, t_attn, e0 + 1u, ws, slot);
     stamp(p, slot);
-    row_range(D, wg, G, r0, rows);
+    row_range(D, wg, grid_here(), r0, rows);
     gemv_load(p.w.wo_q + (size_t)l * D * (D >> 3), p.w.wo_sz + (size_t)l * D * (D >> 7), r0, rows,
               D, w_o, s_o);
 
@@ -595,7 +590,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
       stamp(p, slot);
     }
     stamp(p, slot);
-    row_range(2 * F, wg, G, r0, rows);
+    row_range(2 * F, wg, grid_here(), r0, rows);
     gemv_load(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3), p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7),
               r0, rows, D, w_gu, s_gu);
 
@@ -612,7 +607,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
       stamp(p, slot);
     }
     stamp(p, slot);
-    row_range(D, wg, G, r0, rows);
+    row_range(D, wg, grid_here(), r0, rows);
     gemv_load(p.w.wd_q + (size_t)l * D * (F >> 3), p.w.wd_sz + (size_t)l * D * (F >> 7), r0, rows,
               F, w_d, s_d);
 
@@ -627,7 +622,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     }
     stamp(p, slot);
     if (l + 1 < p.NL) {
-      row_range(NQKV, wg, G, r0, rows);
+      row_range(NQKV, wg, grid_here(), r0, rows);
       gemv_load(p.w.wqkv_q + (size_t)(l + 1) * NQKV * (D >> 3),
                 p.w.wqkv_sz + (size_t)(l + 1) * NQKV * (D >> 7), r0, rows, D, w_qkv, s_qkv);
     }
@@ -666,8 +661,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
           acc = dot2_bf16(ev[rr][i].w, xv.w, acc);
         }
       }
-      acc = wave_sum(acc);
-      acc = __shfl(acc, 0, 64);
+      acc = wave_sum(acc);  // all-reduce: every lane holds the row's dot
       if (rb + rr < rows) {
         const int r = r0 + rb + rr;
         // logits = bf16(bf16(x . E^T) / logits_scaling)  (engine/model.py:144)
@@ -690,7 +684,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     if (rb + STEP < rows) lm_compute(eb, rb + STEP);
   }
   if (lane == 0) kred[wave] = best;
-  __syncthreads();
+  lds_barrier();
   stamp(p, slot);
   if (tid == 0) {
     unsigned long long b = kred[0];
@@ -704,19 +698,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
       __hip_atomic_store(p.amax, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-  }
-}
-
-typedef void (*decode_fn)(DecodeParams);
-
-decode_fn pick_decode(int qpg) {
-  switch (qpg) {
-    case 1: return k_decode<1>;
-    case 2: return k_decode<2>;
-    case 4: return k_decode<4>;
-    case 5: return k_decode<5>;
-    case 8: return k_decode<8>;
-    default: return nullptr;
   }
 }
 
@@ -734,12 +715,11 @@ struct fl_state {
   fl_model_desc d;
   int max_seq;
   int grid;
-  int qpg;
   uint16_t *kc, *vc;
   uint32_t *h, *attn, *act;
   unsigned long long* qkv;
-  float* part;
-  uint32_t* cnt;
+  unsigned long long* part;
+  int att_spw;
   unsigned long long* amax;
   uint32_t* done;
   int32_t* err;
@@ -770,7 +750,7 @@ int fl_device_info(int32_t* num_cu, int32_t* decode_grid) {
   if (hipGetDevice(&dev) != hipSuccess) return FL_E_HIP;
   if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return FL_E_HIP;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_decode<5>),
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_decode),
                                                    NT, 0) != hipSuccess)
     return FL_E_HIP;
   if (num_cu) *num_cu = cu;
@@ -788,14 +768,12 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   if (d->dim % FL_GROUP || d->inter % FL_GROUP || d->dim > XS_MAX || d->inter > XS_MAX ||
       d->dim > 64 * 8 * LM_MAXC || d->dim != d->n_head * FL_HEAD_DIM || d->n_head % d->n_kv_head)
     return FL_E_ARG;
-  const int qpg = d->n_head / d->n_kv_head;
-  if (!pick_decode(qpg) || qpg > QPG_MAX) return FL_E_ARG;
   int dev = 0, cu = 0, occ = 0;
   if (hipGetDevice(&dev) != hipSuccess) return FL_E_HIP;
   if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return FL_E_HIP;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &occ, reinterpret_cast<const void*>(pick_decode(qpg)), NT, 0) != hipSuccess)
+          &occ, reinterpret_cast<const void*>(k_decode), NT, 0) != hipSuccess)
     return FL_E_HIP;
   if (occ < 1 || cu < 1) return FL_E_LAUNCH;
   const int G = cu;
@@ -808,18 +786,21 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   st->d = *d;
   st->max_seq = max_seq;
   st->grid = G;
-  st->qpg = qpg;
   st->kc = k_cache;
   st->vc = v_cache;
   st->epoch = 1;
+  st->att_spw = 8;
+  if (const char* e = getenv("FLINT_AMD_ATT_STEPS")) {  // tuning knob: steps per wave per slice
+    const int v = atoi(e);
+    if (v >= 1 && v <= 64) st->att_spw = v;
+  }
   int rc = FL_OK;
   if (rc == FL_OK) rc = dev_alloc(st, &st->h, (size_t)D * FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->qkv, (size_t)(NQKV / 2) * FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->attn, (size_t)D * FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->act, (size_t)F * FL_MAX_VERIFY);
   if (rc == FL_OK)
-    rc = dev_alloc(st, &st->part, (size_t)d->n_kv_head * MAX_SLICES * QPG_MAX * 66 * FL_MAX_VERIFY);
-  if (rc == FL_OK) rc = dev_alloc(st, &st->cnt, (size_t)d->n_kv_head * FL_MAX_VERIFY);
+    rc = dev_alloc(st, &st->part, (size_t)d->n_head * MAX_SLICES * 66 * FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->amax, FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->done, 1);
   if (rc == FL_OK) rc = dev_alloc(st, &st->err, 1);
@@ -842,8 +823,6 @@ int fl_state_destroy(fl_state* st) {
 int fl_state_reset(fl_state* st, void* stream) {
   if (!st) return FL_E_ARG;
   hipStream_t s = as_stream(stream);
-  if (hipMemsetAsync(st->cnt, 0, sizeof(uint32_t) * st->d.n_kv_head * FL_MAX_VERIFY, s) != hipSuccess)
-    return FL_E_HIP;
   if (hipMemsetAsync(st->amax, 0, sizeof(unsigned long long) * FL_MAX_VERIFY, s) != hipSuccess)
     return FL_E_HIP;
   if (hipMemsetAsync(st->done, 0, sizeof(uint32_t), s) != hipSuccess) return FL_E_HIP;
@@ -893,7 +872,7 @@ int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, i
   p.attn = st->attn;
   p.act = st->act;
   p.part = st->part;
-  p.cnt = st->cnt;
+  p.att_spw = st->att_spw;
   p.amax = st->amax;
   p.done = st->done;
   p.err = st->err;
@@ -919,7 +898,7 @@ int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, i
   p.prof_slots = st->prof_slots;
   void* args[] = {&p};
   const hipError_t e =
-      hipLaunchCooperativeKernel(reinterpret_cast<const void*>(pick_decode(st->qpg)), dim3(st->grid),
+      hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode), dim3(st->grid),
                                  dim3(NT), args, 0, as_stream(stream));
   if (e != hipSuccess) return FL_E_LAUNCH;
   st->epoch += 5u * (uint32_t)st->d.n_layer;

@@ -67,6 +67,29 @@ def analyse(buf, grid, slots, n_layer):
             d["input_wait_mean_us"] = float(wait.mean())
         out["phases"][name] = d
     out["attention_units"] = out_att
+    # hand-offs: when the last producer finished (relative to the median producer: imbalance) and
+    # when consumers saw its outputs (relative to the last producer: exchange latency)
+    prod_done = {"h->qkv": prev_done, "qkv->attention": lay[..., 1], "attn->o": lay[..., 4],
+                 "h1->gateup": lay[..., 7], "act->down": lay[..., 9]}
+    cons_ready = {"h->qkv": lay[..., 0], "qkv->attention": lay[..., 2], "attn->o": lay[..., 6],
+                  "h1->gateup": lay[..., 8], "act->down": lay[..., 10]}
+    trans = {}
+    for name in prod_done:
+        pd, cr = prod_done[name], cons_ready[name]
+        if name == "attn->o":
+            pd = torch.where(busy, pd, torch.full_like(pd, -1e30))
+        if name == "qkv->attention":
+            cr = torch.where(busy, cr, torch.full_like(cr, float("nan")))
+        last = pd.max(0).values                                     # [L]
+        med = pd.median(0).values if name != "attn->o" else last
+        rel = cr - last
+        trans[name] = {
+            "producer_spread_us": float((last - med).mean()),
+            "first_consumer_us": float(torch.nan_to_num(rel, nan=1e30).min(0).values.mean()),
+            "median_consumer_us": float(rel.nanmedian(0).values.mean()),
+            "last_consumer_us": float(torch.nan_to_num(rel, nan=-1e30).max(0).values.mean()),
+        }
+    out["handoffs"] = trans
     layer_end = lay[..., 11].max(0).values
     out["layer_critical_us"] = float((layer_end[1:] - layer_end[:-1]).mean()) if L > 1 else None
     out["final_norm_wait_us"] = float((t[:, 1 + PER_LAYER * L] - lay[:, -1, 11]).mean())

@@ -112,3 +112,37 @@ def test_greedy_decode_parity(dev, name, prompt_len, steps):
         assert ok
     log(f"{name}: {steps} greedy steps, {ties} noise-floor tie steps, worst max|dlogit|={worst:.3e}")
     assert ties <= 4
+
+
+@pytest.mark.parametrize("steps_per_wave", [1, 3])
+def test_decode_multi_slice_attention(dev, monkeypatch, steps_per_wave):
+    """Attention split over several key slices per head (slices > 0 publish tagged partials,
+    slice 0 merges them): forced by a small steps-per-wave target, at contexts that give 2 to 16
+    slices, including a partly filled last step."""
+    monkeypatch.setenv("FLINT_AMD_ATT_STEPS", str(steps_per_wave))
+    args, sd, eng, orc = make_pair("tiny", seed=5)
+    eng.setup_caches(1, 1024)
+    orc.setup_caches(eng.max_seq_length)
+    for pos in (9, 100, 517, 1000):
+        fill_kv_random(eng, orc, pos, seed=pos)
+        tok = (13 * pos + 1) % args.vocab_size
+        am_e, am_o, (ok, d, within, same), lg, lo, fe, fo = _step_compare(eng, orc, tok, pos)
+        log(f"spw={steps_per_wave} pos={pos}: max|dlogit|={d:.3e} ({within:.1%} within 2e-2) "
+            f"argmax eng={am_e} oracle={am_o}")
+        assert ok
+        assert am_e == am_o or near_tie(lo)
+
+
+@pytest.mark.parametrize("pos", [4095, 8191])
+def test_decode_long_context(dev, pos):
+    """BASELINE config 3 shape (one layer of the 3B model, 40 Q / 8 KV heads) at context 4096 and
+    8192: several slices per head and several rounds per wave."""
+    args, sd, eng, orc = make_pair("flint-3b-l1", seed=2)
+    eng.setup_caches(1, 8192)
+    orc.setup_caches(eng.max_seq_length)
+    fill_kv_random(eng, orc, pos, seed=11)
+    am_e, am_o, (ok, d, within, same), lg, lo, fe, fo = _step_compare(eng, orc, 1234, pos)
+    log(f"3b-l1 pos={pos}: max|dlogit|={d:.3e} ({within:.1%} within 2e-2) argmax eng={am_e} "
+        f"oracle={am_o}")
+    assert ok
+    assert am_e == am_o or near_tie(lo)
