@@ -178,6 +178,27 @@ __device__ __forceinline__ unsigned long long ld_coh_u64(const unsigned long lon
   return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
 }
+// ---- range-checked loads ----------------------------------------------------------------------
+// A raw buffer resource over [base, base + bytes): loads at offsets past the end return 0 and
+// touch no memory. Prefetch loops use them instead of `if (in range) load`, which keeps them
+// branch-free so the compiler can count outstanding loads exactly (a load issued under a branch
+// makes later waits conservative: wait-for-all instead of wait-for-the-older-ones).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);  // raw buffer, 32-bit data format
+}
+__device__ __forceinline__ uint4 buf_ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+// device-coherent variant (sc1: served past the non-coherent per-XCD L2s, like an agent-scope
+// relaxed atomic load); each aligned dword of the result is read atomically
+__device__ __forceinline__ uint4 buf_ld128_coh(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
+}
+
 // Workgroup barrier that orders LDS accesses only. __syncthreads also waits for every global
 // load and store the wave has in flight (prefetched weights, published activations); this one
 // does not, so a barrier between LDS producers and consumers never stalls on HBM traffic.
@@ -195,10 +216,11 @@ __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 // __shfl_xor lowers to ds_bpermute, an LDS round trip per step. These use DPP lane patterns
 // (within a 16-lane row) and gfx950's v_permlane16/32_swap (across rows) instead: one VALU op
 // each. Every helper returns, in lane i, the value of lane i ^ mask.
+// (every pattern used reads a valid lane, so the "old" operand is never selected; passing 0 lets
+// the compiler fold the move into the consuming add / max as one DPP instruction)
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL,
-                                                    0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 __device__ __forceinline__ float lane_xor1(float v) { return dpp_f<0xB1>(v); }   // quad_perm 1,0,3,2
 __device__ __forceinline__ float lane_xor2(float v) { return dpp_f<0x4E>(v); }   // quad_perm 2,3,0,1

@@ -118,17 +118,6 @@ __device__ __forceinline__ T spin_until(const DecodeParams& p, T v, Ok ok, Ld ld
   return v;
 }
 
-// four tagged words (16-byte aligned) once all carry `tag`
-__device__ __forceinline__ uint4 wait4(const DecodeParams& p, const uint32_t* a, uint32_t tag) {
-  auto ld = [a]() { return ld_coh_u128(a); };
-  auto ok = [tag](uint4 v) {
-    return ((v.x >> 16) == tag) & ((v.y >> 16) == tag) & ((v.z >> 16) == tag) & ((v.w >> 16) == tag);
-  };
-  uint4 v = ld();
-  if (!ok(v)) v = spin_until(p, v, ok, ld);
-  return v;
-}
-
 __device__ __forceinline__ unsigned long long wait_pair(const DecodeParams& p,
                                                         const unsigned long long* a, uint32_t tag) {
   auto ld = [a]() { return ld_coh_u64(a); };
@@ -193,20 +182,48 @@ __device__ void norm_embed(const uint16_t* __restrict__ erow, float mult,
   norm_finish(ss, nw, D, eps, xs, red);
 }
 
+// Stage the tagged vector src[0..n) (n % 4 == 0, n <= XS_MAX) into xs as bf16 once every word
+// carries `tag`, and return this thread's sum of squares of its values. Each thread requests
+// all of its 16-byte groups at once (coherent range-checked loads) and checks them afterwards,
+// so a vector that is already complete costs one round trip, not one per group.
+constexpr int POLL_MAX = XS_MAX / 4 / NT;
+__device__ __forceinline__ float poll_stage(const DecodeParams& p, const uint32_t* src, int n,
+                                            uint32_t tag, uint16_t* xs) {
+  const int tid = tid_here();
+  const auto rsrc = buf_rsrc(src, (uint32_t)n * 4u);
+  asm volatile("" ::: "memory");  // keep the requests after this workgroup's earlier stores
+  uint4 v[POLL_MAX];
+#pragma unroll
+  for (int i = 0; i < POLL_MAX; ++i) v[i] = buf_ld128_coh(rsrc, (uint32_t)(tid + i * NT) * 16u);
+  auto ok = [tag](uint4 w) {
+    return ((w.x >> 16) == tag) & ((w.y >> 16) == tag) & ((w.z >> 16) == tag) & ((w.w >> 16) == tag);
+  };
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < POLL_MAX; ++i) {
+    const int g = tid + i * NT;
+    if (g < (n >> 2)) {
+      uint4 w = v[i];
+      if (!ok(w)) {
+        const uint32_t* a = src + 4 * g;
+        w = spin_until(p, w, ok, [a]() { return ld_coh_u128(a); });
+      }
+      const float a0 = bflo(w.x), a1 = bflo(w.y), a2 = bflo(w.z), a3 = bflo(w.w);
+      ss += a0 * a0;
+      ss += a1 * a1;
+      ss += a2 * a2;
+      ss += a3 * a3;
+      reinterpret_cast<uint2*>(xs)[g] =
+          make_uint2((w.x & 0xFFFFu) | (w.y << 16), (w.z & 0xFFFFu) | (w.w << 16));
+    }
+  }
+  return ss;
+}
+
 // xs = RMSNorm(h) once every word of the tagged residual h carries `tag`
 __device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t tag,
                             const uint16_t* __restrict__ nw, uint16_t* xs, float* red) {
-  float ss = 0.0f;
-  for (int i = tid_here(); i < (p.D >> 2); i += NT) {
-    const uint4 v = wait4(p, h + 4 * i, tag);
-    const float a0 = bflo(v.x), a1 = bflo(v.y), a2 = bflo(v.z), a3 = bflo(v.w);
-    ss += a0 * a0;
-    ss += a1 * a1;
-    ss += a2 * a2;
-    ss += a3 * a3;
-    reinterpret_cast<uint2*>(xs)[i] =
-        make_uint2((v.x & 0xFFFFu) | (v.y << 16), (v.z & 0xFFFFu) | (v.w << 16));
-  }
+  const float ss = poll_stage(p, h, p.D, tag, xs);
   lds_barrier();
   norm_finish(ss, nw, p.D, p.eps, xs, red);
 }
@@ -214,11 +231,7 @@ __device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t t
 // xs = values of the tagged vector src[0..n) once all carry `tag`
 __device__ void stage_tagged(const DecodeParams& p, const uint32_t* src, int n, uint32_t tag,
                              uint16_t* xs) {
-  for (int i = tid_here(); i < (n >> 2); i += NT) {
-    const uint4 v = wait4(p, src + 4 * i, tag);
-    reinterpret_cast<uint2*>(xs)[i] =
-        make_uint2((v.x & 0xFFFFu) | (v.y << 16), (v.z & 0xFFFFu) | (v.w << 16));
-  }
+  poll_stage(p, src, n, tag, xs);
   lds_barrier();
 }
 
@@ -227,21 +240,14 @@ template <int MC>
 __device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ q,
                                           const uint32_t* __restrict__ sz, int r0, int rows, int K,
                                           uint4 (&wr)[MC], uint32_t (&sr)[MC]) {
-  const int total = rows * (K >> 5);
-  const uint4* wb = reinterpret_cast<const uint4*>(q + (size_t)r0 * (K >> 3));
-  const uint32_t* sb = sz + (size_t)r0 * (K >> 7);
+  const auto wb = buf_rsrc(q + (size_t)r0 * (K >> 3), (uint32_t)rows * (K >> 1));
+  const auto sb = buf_rsrc(sz + (size_t)r0 * (K >> 7), (uint32_t)rows * (K >> 5));
   const int tid = tid_here();
 #pragma unroll
-  for (int i = 0; i < MC; ++i) {
-    const int f = tid + i * NT;
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    uint32_t z = 0u;
-    if (f < total) {
-      v = wb[f];
-      z = sb[f >> 2];
-    }
-    wr[i] = v;  // unconditional: the previous contents are dead here
-    sr[i] = z;
+  for (int i = 0; i < MC; ++i) {  // chunks past this workgroup's rows read as 0
+    const uint32_t f = (uint32_t)(tid + i * NT);
+    wr[i] = buf_ld128(wb, f * 16u);
+    sr[i] = buf_ld32(sb, (f >> 2) * 4u);
   }
 }
 
@@ -276,18 +282,19 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
   lds_barrier();
 }
 
-// Key slices of one query head. Keys are processed in 8-key steps (8 keys x 64 dims: one
-// 16-byte K load and one 16-byte V load per lane); a slice is one workgroup, whose 8 waves take
-// interleaved steps so that each group of 8 steps covers 64 consecutive keys. `spw` is the
-// target number of steps per wave: slices = ceil(steps / (8 * spw)), at most G / NH.
-__device__ __forceinline__ void attn_slices(int T, int NH, int G, int spw, int& nsl, int& sps) {
-  const int ns = (T + 7) >> 3;
+// Key slices of one query head over the cached keys 0..pos-1. Keys are processed in 8-key steps
+// (8 keys x 64 dims: one 16-byte K load and one 16-byte V load per lane); a slice is one
+// workgroup, whose 8 waves take interleaved steps so that each group of 8 steps covers 64
+// consecutive keys. `spw` is the target number of steps per wave: slices = ceil(steps /
+// (8 * spw)), at most G / NH, at least 1 (the new key at pos always has a slice).
+__device__ __forceinline__ void attn_slices(int pos, int NH, int G, int spw, int& nsl, int& sps) {
+  const int ns = (pos + 7) >> 3;
   const int per = NWAVE * spw;
-  nsl = (ns + per - 1) / per;
+  nsl = max(1, (ns + per - 1) / per);
   const int cap = max(1, min(MAX_SLICES, G / NH));
   if (nsl > cap) nsl = cap;
   sps = (ns + nsl - 1) / nsl;
-  nsl = (ns + sps - 1) / sps;
+  nsl = sps > 0 ? max(1, (ns + sps - 1) / sps) : 1;
 }
 
 // GQA flash-decode attention of one layer (engine/model.py:171-179: q.k^T * scale, softmax and
@@ -298,21 +305,21 @@ __device__ __forceinline__ void attn_slices(int T, int NH, int G, int spw, int& 
 // contexts every head is one slice, so no workgroup waits for another.
 // Lane (kk = lane / 8, ds = lane % 8) of a wave holds dims 8ds..8ds+7 of key kk of each step:
 // q . k is 4 dot2 plus a 3-step DPP sum over the key's 8 lanes, p.v is 8 FMAs, and the output
-// is summed over the 8 keys once at the end. The slice's K / V rows are requested before the
-// wait for this launch's q, so the cache reads overlap it; the new key / value (position pos,
-// appended to the cache by this same launch) come from the tagged q/k/v words instead. Softmax
-// uses the exact max of each round of RB steps with an online rescale between rounds. Waves
-// merge through LDS; slices > 0 publish (m, l, o) as tagged 64-bit words and slice 0 merges
-// them in slice order.
+// is summed over the 8 keys once at the end. The slice's cached K / V rows (keys < pos) are
+// requested before the wait for this launch's q, so the cache reads overlap it. The new key
+// (position pos, appended to the cache by this same launch) comes from the tagged q/k/v words
+// and is folded in by wave 0 of slice 0 as one extra key. Softmax uses the exact max of each
+// round of steps with an online rescale between rounds and for the new key. Waves merge through
+// LDS; slices > 0 publish (m, l, o) as tagged 64-bit words and slice 0 merges them in order.
 __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
                                 uint32_t ptag, float* ws, int& slot) {
-  constexpr int RB = 16;  // steps per wave per round (K/V held in registers)
+  constexpr int RG = 4, NG = 3, RB = RG * NG;  // steps per wave per round, in groups of RG
   const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
   const int kk = lane >> 3, ds = lane & 7;
-  const int T = p.pos + 1;
-  const int ns = (T + 7) >> 3;
+  const int pos = p.pos;
+  const int ns = (pos + 7) >> 3;
   int nsl, sps;
-  attn_slices(T, p.NH, grid_here(), p.att_spw, nsl, sps);
+  attn_slices(pos, p.NH, grid_here(), p.att_spw, nsl, sps);
   const int u = blockIdx.x;
   if (u >= p.NH * nsl) {
     stamp(p, slot);
@@ -324,23 +331,24 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
   const int hq = g * (p.NH / p.NKV) + j;
   const int s0 = sl * sps, s1 = min(ns, s0 + sps);
   const int nrounds = (s1 - s0 + NWAVE * RB - 1) / (NWAVE * RB);
-  const size_t cbase = (size_t)(l * p.NKV + g) * p.S * 64;
-  const uint4* kb = reinterpret_cast<const uint4*>(p.kc + cbase) + ds;  // key t: kb[8 t]
-  const uint4* vb = reinterpret_cast<const uint4*>(p.vc + cbase) + ds;
+  // this slice's cached rows: keys [8 s0, min(8 s1, pos)); loads outside read as 0
+  const int k0 = s0 * 8, k1 = min(s1 * 8, pos);
+  const size_t cbase = ((size_t)(l * p.NKV + g) * p.S + k0) * 64;
+  const uint32_t kbytes = (uint32_t)max(k1 - k0, 0) * 128u;
+  const auto kb = buf_rsrc(p.kc + cbase, kbytes);
+  const auto vb = buf_rsrc(p.vc + cbase, kbytes);
 
   uint4 kr[RB], vr[RB];
+  auto step_of = [&](int r, int i) { return s0 + r * NWAVE * RB + wave + NWAVE * i; };
   auto issue = [&](int r) {
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
-      const int st = s0 + r * NWAVE * RB + wave + NWAVE * i;
-      if (st < s1) {  // wave-uniform
-        const int tc = min(st * 8 + kk, p.pos);  // keys >= T are masked below
-        kr[i] = kb[(size_t)tc * 8];
-        vr[i] = vb[(size_t)tc * 8];
-      }
+      const uint32_t off = (uint32_t)((step_of(r, i) * 8 + kk - k0) * 128 + ds * 16);
+      kr[i] = buf_ld128(kb, off);
+      vr[i] = buf_ld128(vb, off);
     }
   };
-  issue(0);
+  if (nrounds > 0) issue(0);
 
   // LDS: bf16 [3][64]: q of head hq, this step's new k and v of group g
   uint16_t* qs = reinterpret_cast<uint16_t*>(ws);
@@ -354,9 +362,10 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
   }
   lds_barrier();
   stamp(p, slot);
-  const uint4 qv = reinterpret_cast<const uint4*>(qs)[ds];
-  const uint4 kn = reinterpret_cast<const uint4*>(qs + 64)[ds];
-  const uint4 vn = reinterpret_cast<const uint4*>(qs + 128)[ds];
+  const uint32_t* qs32 = reinterpret_cast<const uint32_t*>(ws);
+  uint32_t qv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) qv[e] = qs32[ds * 4 + e];
   // scores in the log2 domain: p = 2^(s * scale * log2(e) - m)
   const float sc = p.attn_scale * 1.4426950408889634f;
 
@@ -368,19 +377,20 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
     float s[RB];
     float rmax = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < RB; ++i) {
-      const int st = s0 + r * NWAVE * RB + wave + NWAVE * i;
-      s[i] = -INFINITY;
-      if (st < s1) {
-        const int t = st * 8 + kk;
-        const uint4 kv = (t == p.pos) ? kn : kr[i];
-        float a = dot2_bf16(kv.x, qv.x, 0.0f);
-        a = dot2_bf16(kv.y, qv.y, a);
-        a = dot2_bf16(kv.z, qv.z, a);
-        a = dot2_bf16(kv.w, qv.w, a);
-        a = sum8(a);
-        s[i] = (t < T) ? a * sc : -INFINITY;
-        rmax = fmaxf(rmax, s[i]);
+    for (int gi = 0; gi < NG; ++gi) {
+      if (step_of(r, gi * RG) < s1) {
+#pragma unroll
+        for (int ii = 0; ii < RG; ++ii) {
+          const int i = gi * RG + ii;
+          const int st = step_of(r, i);
+          float a = dot2_bf16(kr[i].x, qv[0], 0.0f);
+          a = dot2_bf16(kr[i].y, qv[1], a);
+          a = dot2_bf16(kr[i].z, qv[2], a);
+          a = dot2_bf16(kr[i].w, qv[3], a);
+          a = sum8(a);
+          s[i] = (st < s1 && st * 8 + kk < pos) ? a * sc : -INFINITY;
+          rmax = fmaxf(rmax, s[i]);
+        }
       }
     }
     const float mn = fmaxf(m, max_stride8(rmax));
@@ -391,24 +401,42 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
     for (int e = 0; e < 8; ++e) o[e] *= corr;
     m = mn;
 #pragma unroll
-    for (int i = 0; i < RB; ++i) {
-      const int st = s0 + r * NWAVE * RB + wave + NWAVE * i;
-      if (st < s1) {
-        const int t = st * 8 + kk;
-        uint4 vv = (t == p.pos) ? vn : vr[i];
-        if (t >= T) vv = make_uint4(0u, 0u, 0u, 0u);  // rows past pos may hold anything
-        const float pw = __builtin_amdgcn_exp2f(s[i] - mu);
-        lsum += pw;
-        o[0] = __builtin_fmaf(pw, bflo(vv.x), o[0]);
-        o[1] = __builtin_fmaf(pw, bfhi(vv.x), o[1]);
-        o[2] = __builtin_fmaf(pw, bflo(vv.y), o[2]);
-        o[3] = __builtin_fmaf(pw, bfhi(vv.y), o[3]);
-        o[4] = __builtin_fmaf(pw, bflo(vv.z), o[4]);
-        o[5] = __builtin_fmaf(pw, bfhi(vv.z), o[5]);
-        o[6] = __builtin_fmaf(pw, bflo(vv.w), o[6]);
-        o[7] = __builtin_fmaf(pw, bfhi(vv.w), o[7]);
+    for (int gi = 0; gi < NG; ++gi) {
+      if (step_of(r, gi * RG) < s1) {
+#pragma unroll
+        for (int ii = 0; ii < RG; ++ii) {
+          const int i = gi * RG + ii;
+          const float pw = __builtin_amdgcn_exp2f(s[i] - mu);
+          lsum += pw;
+          o[0] = __builtin_fmaf(pw, bflo(vr[i].x), o[0]);
+          o[1] = __builtin_fmaf(pw, bfhi(vr[i].x), o[1]);
+          o[2] = __builtin_fmaf(pw, bflo(vr[i].y), o[2]);
+          o[3] = __builtin_fmaf(pw, bfhi(vr[i].y), o[3]);
+          o[4] = __builtin_fmaf(pw, bflo(vr[i].z), o[4]);
+          o[5] = __builtin_fmaf(pw, bfhi(vr[i].z), o[5]);
+          o[6] = __builtin_fmaf(pw, bflo(vr[i].w), o[6]);
+          o[7] = __builtin_fmaf(pw, bfhi(vr[i].w), o[7]);
+        }
       }
     }
+  }
+  if (sl == 0 && wave == 0) {  // the new key / value at pos (lanes kk = 0 carry its p)
+    float a = dot2_bf16(qs32[32 + ds * 4], qv[0], 0.0f);
+    a = dot2_bf16(qs32[32 + ds * 4 + 1], qv[1], a);
+    a = dot2_bf16(qs32[32 + ds * 4 + 2], qv[2], a);
+    a = dot2_bf16(qs32[32 + ds * 4 + 3], qv[3], a);
+    const float sn = sum8(a) * sc;
+    const float mn = fmaxf(m, sn);
+    const float corr = __builtin_amdgcn_exp2f(m - mn);  // 0 while m = -inf
+    const float pn = (kk == 0) ? __builtin_amdgcn_exp2f(sn - mn) : 0.0f;
+    lsum = lsum * corr + pn;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t vw = qs32[64 + ds * 4 + e];
+      o[2 * e] = __builtin_fmaf(pn, bflo(vw), o[2 * e] * corr);
+      o[2 * e + 1] = __builtin_fmaf(pn, bfhi(vw), o[2 * e + 1] * corr);
+    }
+    m = mn;
   }
   stamp(p, slot);
   // sum over the 8 keys of a step (lanes kk = 0..7 with the same ds), then merge the waves
@@ -480,18 +508,21 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
   stamp(p, slot);
 }
 
-// tagged h[r0 .. r0+rows) = bf16(h + bf16(bf16(acc) * rm)), two rows per thread (r0, rows even)
+// h[r0 .. r0+rows) = bf16(h + bf16(bf16(acc) * rm)), two rows per thread (r0, rows even). The
+// workgroup owns these rows for the whole step (O and down share the row split), so their
+// current values live in registers (ha, hb) and only the tagged result is stored.
 __device__ __forceinline__ void residual_epilogue(const DecodeParams& p, int r0, int rows,
-                                                  const float* rs, uint32_t tag) {
+                                                  const float* rs, uint32_t tag, float& ha,
+                                                  float& hb) {
   const int t = tid_here();
   if (2 * t < rows) {
-    unsigned long long* hp = reinterpret_cast<unsigned long long*>(p.h + r0) + t;
-    const unsigned long long hv = ld_coh_u64(hp);  // own rows: no tag wait needed
     const float o0 = rbf(rbf(rs[2 * t]) * p.resid_mult);
     const float o1 = rbf(rbf(rs[2 * t + 1]) * p.resid_mult);
-    const uint32_t n0 = f2bf(bflo((uint32_t)hv) + o0) | (tag << 16);
-    const uint32_t n1 = f2bf(bflo((uint32_t)(hv >> 32)) + o1) | (tag << 16);
-    st_coh_u64(hp, (unsigned long long)n0 | ((unsigned long long)n1 << 32));
+    ha = rbf(ha + o0);
+    hb = rbf(hb + o1);
+    const uint32_t n0 = f2bf(ha) | (tag << 16), n1 = f2bf(hb) | (tag << 16);
+    st_coh_u64(reinterpret_cast<unsigned long long*>(p.h + r0) + t,
+               (unsigned long long)n0 | ((unsigned long long)n1 << 32));
   }
 }
 
@@ -518,13 +549,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 
   int r0d, rowsd;  // this workgroup's rows of every [D]-output GEMV (O, down): it owns h there
   row_range(D, wg, G, r0d, rowsd);
-  // h = bf16(embed[token] * emb_mult) on the owned rows (engine/model.py:138); only this
-  // workgroup reads these words before they are rewritten, so their tag is irrelevant
-  for (int i = tid; 2 * i < rowsd; i += NT) {
-    const uint32_t e2 = reinterpret_cast<const uint32_t*>(erow + r0d)[i];
-    const uint32_t a = f2bf(bflo(e2) * p.emb_mult), b = f2bf(bfhi(e2) * p.emb_mult);
-    st_coh_u64(reinterpret_cast<unsigned long long*>(p.h + r0d) + i,
-               (unsigned long long)a | ((unsigned long long)b << 32));
+  // h = bf16(embed[token] * emb_mult) on the owned rows (engine/model.py:138), held in registers
+  float ha = 0.0f, hb = 0.0f;
+  if (2 * tid < rowsd) {
+    const uint32_t e2 = reinterpret_cast<const uint32_t*>(erow + r0d)[tid];
+    ha = rbf(bflo(e2) * p.emb_mult);
+    hb = rbf(bfhi(e2) * p.emb_mult);
   }
 
   uint4 w_qkv[MC_QKV], w_o[MC_O], w_gu[MC_GU], w_d[MC_D];
@@ -537,6 +567,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     const uint32_t e0 = p.epoch + 5u * (uint32_t)l;
     const uint32_t t_prev = tag_of(e0 - 1), t_qkv = tag_of(e0), t_attn = tag_of(e0 + 1),
                    t_h1 = tag_of(e0 + 2), t_act = tag_of(e0 + 3), t_h2 = tag_of(e0 + 4);
+    // Each phase polls for its inputs first and only then requests the weights of the next GEMV
+    // phase: vector loads complete in order, so weights requested before a poll would delay
+    // the poll's result by their whole transfer; requested after it, they stream in during this
+    // phase's compute.
+    int r0n, rowsn;
     // ---------------- P1: RMSNorm + QKV + RoPE + KV append ----------------
     row_range(NQKV, wg, grid_here(), r0, rows);
     if (rows > 0) {
@@ -544,7 +579,15 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
         norm_embed(erow, p.emb_mult, p.w.attn_norm, D, p.eps, xs, red);
       else
         norm_tagged(p, p.h, t_prev, p.w.attn_norm + (size_t)l * D, xs, red);
-      stamp(p, slot);
+    }
+    stamp(p, slot);
+    // this thread's RoPE (cos, sin) pair, requested before the O weights (in-order returns)
+    const uint32_t rope_cs = buf_ld32(buf_rsrc(p.w.rope + (size_t)pos * 64, 128u),
+                                      (uint32_t)(((r0 + 2 * tid) & 63) >> 1) * 4u);
+    row_range(D, wg, grid_here(), r0n, rowsn);
+    gemv_load(p.w.wo_q + (size_t)l * D * (D >> 3), p.w.wo_sz + (size_t)l * D * (D >> 7), r0n,
+              rowsn, D, w_o, s_o);
+    if (rows > 0) {
       gemv_compute(w_qkv, s_qkv, rows, D, xs, ws, rs);
       if (tid < (rows >> 1)) {
         const int srow = r0 + 2 * tid;
@@ -552,7 +595,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
         const float a = rbf(rs[2 * tid]), b = rbf(rs[2 * tid + 1]);
         float oa = a, ob = b;
         if (hh < NH + NKV) {  // RoPE (engine/model.py:257-269 on NEOX pairs j, j+32)
-          const uint32_t cs = reinterpret_cast<const uint32_t*>(p.w.rope)[pos * 32 + j];
+          const uint32_t cs = rope_cs;
           const float c = bflo(cs), sn = bfhi(cs);
           oa = rbf(a * c - b * sn);
           ob = rbf(b * c + a * sn);
@@ -566,66 +609,56 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
           dst[j + 32] = (uint16_t)f2bf(ob);
         }
       }
-    } else {
-      stamp(p, slot);
     }
     stamp(p, slot);
 
     // ---------------- P2: GQA flash-decode attention ----------------
-    // (the O weights are requested after it: attention needs the registers, and the O phase
-    // waits for every group's attention output anyway)
     attention_phase(p, l, t_qkv, t_attn, e0 + 1u, ws, slot);
     stamp(p, slot);
-    row_range(D, wg, grid_here(), r0, rows);
-    gemv_load(p.w.wo_q + (size_t)l * D * (D >> 3), p.w.wo_sz + (size_t)l * D * (D >> 7), r0, rows,
-              D, w_o, s_o);
 
     // ---------------- P3: O projection + residual ----------------
+    row_range(D, wg, grid_here(), r0, rows);
+    if (rows > 0) stage_tagged(p, p.attn, D, t_attn, xs);
+    stamp(p, slot);
+    row_range(2 * F, wg, grid_here(), r0n, rowsn);
+    gemv_load(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3), p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7),
+              r0n, rowsn, D, w_gu, s_gu);
     if (rows > 0) {
-      stage_tagged(p, p.attn, D, t_attn, xs);
-      stamp(p, slot);
       gemv_compute(w_o, s_o, rows, D, xs, ws, rs);
-      residual_epilogue(p, r0, rows, rs, t_h1);  // engine/model.py:162
-    } else {
-      stamp(p, slot);
+      residual_epilogue(p, r0, rows, rs, t_h1, ha, hb);  // engine/model.py:162
     }
     stamp(p, slot);
-    row_range(2 * F, wg, grid_here(), r0, rows);
-    gemv_load(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3), p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7),
-              r0, rows, D, w_gu, s_gu);
 
     // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
+    row_range(2 * F, wg, grid_here(), r0, rows);
+    if (rows > 0) norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red);
+    stamp(p, slot);
+    row_range(D, wg, grid_here(), r0n, rowsn);
+    gemv_load(p.w.wd_q + (size_t)l * D * (F >> 3), p.w.wd_sz + (size_t)l * D * (F >> 7), r0n,
+              rowsn, F, w_d, s_d);
     if (rows > 0) {
-      norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red);
-      stamp(p, slot);
       gemv_compute(w_gu, s_gu, rows, D, xs, ws, rs);
       if (tid < (rows >> 1)) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
         const float g = rbf(rs[2 * tid]), u = rbf(rs[2 * tid + 1]);
         st_coh_u32(p.act + (r0 >> 1) + tid, f2bf(rbf(silu_f(g)) * u) | (t_act << 16));
       }
-    } else {
-      stamp(p, slot);
     }
     stamp(p, slot);
-    row_range(D, wg, grid_here(), r0, rows);
-    gemv_load(p.w.wd_q + (size_t)l * D * (F >> 3), p.w.wd_sz + (size_t)l * D * (F >> 7), r0, rows,
-              F, w_d, s_d);
 
     // ---------------- P5: down projection + residual ----------------
-    if (rows > 0) {
-      stage_tagged(p, p.act, F, t_act, xs);
-      stamp(p, slot);
-      gemv_compute(w_d, s_d, rows, F, xs, ws, rs);
-      residual_epilogue(p, r0, rows, rs, t_h2);  // engine/model.py:163
-    } else {
-      stamp(p, slot);
-    }
+    row_range(D, wg, grid_here(), r0, rows);
+    if (rows > 0) stage_tagged(p, p.act, F, t_act, xs);
     stamp(p, slot);
     if (l + 1 < p.NL) {
-      row_range(NQKV, wg, grid_here(), r0, rows);
+      row_range(NQKV, wg, grid_here(), r0n, rowsn);
       gemv_load(p.w.wqkv_q + (size_t)(l + 1) * NQKV * (D >> 3),
-                p.w.wqkv_sz + (size_t)(l + 1) * NQKV * (D >> 7), r0, rows, D, w_qkv, s_qkv);
+                p.w.wqkv_sz + (size_t)(l + 1) * NQKV * (D >> 7), r0n, rowsn, D, w_qkv, s_qkv);
     }
+    if (rows > 0) {
+      gemv_compute(w_d, s_d, rows, F, xs, ws, rs);
+      residual_epilogue(p, r0, rows, rs, t_h2, ha, hb);  // engine/model.py:163
+    }
+    stamp(p, slot);
   }
 
   // ---------------- final norm + tied bf16 LM head + greedy argmax ----------------
@@ -635,14 +668,15 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
   constexpr int STEP = NWAVE * LM_RB;
   uint4 ea[LM_RB][LM_MAXC], eb[LM_RB][LM_MAXC];
   unsigned long long best = 0ull;
-  auto lm_load = [&](uint4 (&ev)[LM_RB][LM_MAXC], int rb) {
+  const auto eb_r = buf_rsrc(p.w.embed + (size_t)r0 * D, (uint32_t)rows * (uint32_t)D * 2u);
+  auto lm_load = [&](uint4 (&ev)[LM_RB][LM_MAXC], int rb) {  // rows past `rows` read as 0
 #pragma unroll
     for (int rr = 0; rr < LM_RB; ++rr) {
-      const uint4* er = reinterpret_cast<const uint4*>(p.w.embed + (size_t)(r0 + rb + rr) * D);
 #pragma unroll
       for (int i = 0; i < LM_MAXC; ++i) {
         const int c = lane + 64 * i;
-        if (rb + rr < rows && c < nck) ev[rr][i] = er[c];
+        const uint32_t off = (c < nck) ? (uint32_t)((rb + rr) * D + c * 8) * 2u : 0xFFFFFFF0u;
+        ev[rr][i] = buf_ld128(eb_r, off);
       }
     }
   };
@@ -789,7 +823,7 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   st->kc = k_cache;
   st->vc = v_cache;
   st->epoch = 1;
-  st->att_spw = 8;
+  st->att_spw = 12;
   if (const char* e = getenv("FLINT_AMD_ATT_STEPS")) {  // tuning knob: steps per wave per slice
     const int v = atoi(e);
     if (v >= 1 && v <= 64) st->att_spw = v;
