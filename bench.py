@@ -20,6 +20,22 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0
+METRIC = "batch-1 decode tok/s + achieved HBM GB/s (MBU) at ctx 512, 1\u00d7MI355X"
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "k_decode_traffic_flint3b_ctx512.txt")
+
+
+def measured_traffic(config, ctx):
+    """HBM bytes per decode launch from the committed rocprofv3 PMC summary (FETCH_SIZE +
+    WRITE_SIZE per dispatch, scaled by the copy-kernel calibration), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            vals = dict(line.split(":", 1) for line in f if ":" in line)
+        if vals.get("config", "").strip() != f"{config} ctx {ctx}":
+            return None
+        return int(float(vals["traffic_bytes_per_launch"]))
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def log(msg):
@@ -75,6 +91,9 @@ def main():
     ap.add_argument("--config", default="flint-3b")
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="after timing, run one device-to-device copy of this many MiB (the "
+                         "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {a.gpus} is not supported (batch-1 decode "
@@ -127,6 +146,16 @@ def main():
     log(f"{tok_s:.1f} tok/s, {ms * 1e3:.1f} us/step, {achieved:.0f} GB/s algorithmic "
         f"(wall {a.steps / wall:.1f} tok/s)")
 
+    if a.copy_probe_mb > 0:
+        n = a.copy_probe_mb * (1 << 20)
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: {n} bytes device-to-device")
+        del src, dst
+
     cpu = None
     if not a.no_cpu_baseline:
         try:
@@ -135,7 +164,7 @@ def main():
         except Exception as e:  # the GPU figure stands on its own
             log(f"cpu baseline failed: {e!r}")
     out = {
-        "metric": "batch-1 decode tok/s + achieved HBM GB/s (MBU) at ctx 512, 1xMI355X",
+        "metric": METRIC,
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -145,14 +174,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4w/bf16",
+        "dtype": "bf16",
         "data": "synthetic (seeded random int4 weights, seeded uniform prompt ids)",
         "config": {"workload": f"{a.config}: 40-layer int4 g128 greedy decode, prompt {a.ctx}, "
                                f"{a.steps} timed tokens (BASELINE config 2)",
-                   "ctx": a.ctx, "global_batch": 1, "parallelism": "none (1 GPU)"},
+                   "ctx": a.ctx, "weights": "int4 groupsize 128, bf16 scale+zero; tied bf16 "
+                   "LM head", "accumulate": "fp32", "global_batch": 1,
+                   "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic(a.config, a.ctx)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

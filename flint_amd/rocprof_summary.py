@@ -1,10 +1,13 @@
-"""Condense a `rocprofv3 --kernel-trace --stats -f csv` run into the short text kept under profiles/.
+"""Condense rocprofv3 CSV output into the short text kept under profiles/.
 
-    python -m flint_amd.rocprof_summary <rocprof output dir> [--kernel k_decode] [--last N]
-
-Prints the per-kernel stats table (calls, total, average, min, max) and, for the named kernel,
-the average duration of its last N dispatches (the timed window of a bench run, whose earlier
-dispatches are prefill / warmup at other context lengths).
+    python -m flint_amd.rocprof_summary <dir> [--kernel k_decode] [--last N]
+        from `rocprofv3 --kernel-trace --stats -f csv`: the per-kernel stats table and, for the
+        named kernel, the average duration of its last N dispatches (the timed window of a
+        bench run, whose earlier dispatches are prefill / warmup at other context lengths);
+    python -m flint_amd.rocprof_summary --traffic <fetch dir> <write dir> --copy-bytes B ...
+        from two `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of a bench command that
+        ends with a device-to-device copy of B bytes: HBM bytes per dispatch of the kernel, each
+        counter scaled by what it reads for the copy (which reads B and writes B bytes).
 """
 import argparse
 import csv
@@ -57,13 +60,55 @@ def summarise(d, kernel="k_decode", last=0, top=8):
     return "\n".join(out)
 
 
+def _counter_rows(d):
+    path = _find(d, "counter_collection.csv")
+    with open(path) as f:
+        return path, list(csv.DictReader(f))
+
+
+def _per_dispatch(rows, pattern):
+    vals = {}
+    for r in rows:
+        if pattern in r["Kernel_Name"]:
+            k = int(r.get("Dispatch_Id") or r.get("Correlation_Id") or 0)
+            vals[k] = vals.get(k, 0.0) + float(r["Counter_Value"])
+    return [vals[k] for k in sorted(vals)]
+
+
+def traffic(fetch_dir, write_dir, kernel, last, copy_bytes, config, copy_kernel="copyBuffer"):
+    out = [f"config: {config}"]
+    tot = 0.0
+    for name, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        path, rows = _counter_rows(d)
+        k = _per_dispatch(rows, kernel)
+        c = _per_dispatch(rows, copy_kernel)
+        if not k or not c:
+            raise RuntimeError(f"{name}: no {kernel} or {copy_kernel} dispatches in {path}")
+        win = k[-last:] if last else k
+        kib = sum(win) / len(win)
+        factor = c[-1] * 1024.0 / copy_bytes  # counter bytes per byte the copy moved
+        bytes_ = kib * 1024.0 / factor
+        tot += bytes_
+        out.append(f"{name}_kib_per_dispatch: {kib:.1f}  (mean of last {len(win)} of {len(k)})")
+        out.append(f"{name}_copy_kib: {c[-1]:.1f}  (copy of {copy_bytes} bytes; scale {factor:.4f})")
+        out.append(f"{name}_bytes_per_launch: {bytes_:.0f}")
+    out.append(f"traffic_bytes_per_launch: {tot:.0f}")
+    return "\n".join(out)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("dir")
+    ap.add_argument("dir", nargs="*")
     ap.add_argument("--kernel", default="k_decode")
     ap.add_argument("--last", type=int, default=0)
+    ap.add_argument("--traffic", action="store_true")
+    ap.add_argument("--copy-bytes", type=int, default=0)
+    ap.add_argument("--config", default="")
     a = ap.parse_args(argv)
-    print(summarise(a.dir, a.kernel, a.last))
+    if a.traffic:
+        print(traffic(a.dir[0], a.dir[1], a.kernel, a.last, a.copy_bytes, a.config))
+    else:
+        print(summarise(a.dir[0], a.kernel, a.last))
 
 
 if __name__ == "__main__":
