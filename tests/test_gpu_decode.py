@@ -146,3 +146,32 @@ def test_decode_long_context(dev, pos):
         f"oracle={am_o}")
     assert ok
     assert am_e == am_o or near_tie(lo)
+
+
+def test_engine_matches_reference_golden(dev):
+    """The HIP engine against the golden vectors of the reference forward itself
+    (tests/golden/tiny_forward.pt: engine/model.py Transformer on a tiny Granite-multiplier
+    configuration): every position of the prompt and of the decode steps, one decode launch
+    each, within the north star's 2e-2 and with identical argmax."""
+    import os
+    from flint_amd.model import Transformer
+    from flint_amd.synth import ModelArgs, synth_weights
+    fx = torch.load(os.path.join(os.path.dirname(__file__), "golden", "tiny_forward.pt"),
+                    weights_only=True)
+    args = ModelArgs(**fx["config"])
+    sd = synth_weights(args, seed=fx["seed"])
+    eng = Transformer.from_weights(args, sd, dev)
+    eng.setup_caches(1, args.block_size)
+    logits = torch.empty(args.vocab_size, dtype=torch.float32, device=dev)
+    worst = 0.0
+    for st in fx["steps"]:
+        for m, t in enumerate(st["tokens"].tolist()):
+            out = eng.decode_step(torch.tensor([t], dtype=torch.int32, device=dev), st["pos"] + m,
+                                  logits=logits)
+            eng.check()
+            ref = st["logits"][m].float()
+            d = float((logits.cpu() - ref).abs().max())
+            worst = max(worst, d)
+            assert d <= LOGIT_TOL, (st["pos"] + m, d)
+            assert int(out.item()) == int(torch.argmax(ref))
+    log(f"golden: worst |dlogit| {worst:.3e}")
