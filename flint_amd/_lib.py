@@ -16,7 +16,7 @@ ERRORS = {
     -3: "FL_E_M (verify width out of range)",
     -4: "FL_E_LAUNCH (HIP launch failed)",
     -5: "FL_E_HIP (HIP runtime error)",
-    -6: "FL_E_TIMEOUT (grid barrier spin limit hit)",
+    -6: "FL_E_TIMEOUT (an inter-workgroup wait hit its time limit)",
 }
 MAX_VERIFY = 16
 HEAD_DIM = 64

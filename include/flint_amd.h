@@ -32,7 +32,7 @@ enum {
   FL_E_M = -3,          /* verify width M outside 1..FL_MAX_VERIFY                             */
   FL_E_LAUNCH = -4,     /* HIP launch failed (e.g. cooperative grid cannot be co-resident)     */
   FL_E_HIP = -5,        /* other HIP runtime error (allocation, copy)                          */
-  FL_E_TIMEOUT = -6     /* a grid barrier spin limit was hit in an earlier launch (state is bad) */
+  FL_E_TIMEOUT = -6     /* an inter-workgroup wait hit its 2 s limit in an earlier launch       */
 };
 
 #define FL_MAX_VERIFY 16
@@ -105,8 +105,10 @@ int fl_state_destroy(fl_state* st);
 int fl_state_reset(fl_state* st, void* stream);
 /* Diagnostics, no counterpart in the reference: when buf (device, uint64 [grid * slots_per_wg])
  * is non-NULL, every later decode launch writes per-workgroup timestamps of the 100 MHz
- * real-time clock: slot 0 at kernel start, then (arrive, leave) for every grid barrier, then
- * the end of the LM head. NULL disables. *grid receives the number of workgroups. */
+ * real-time clock: slot 0 at kernel start, then 12 per layer (for each of the 5 phases when its
+ * inputs have arrived and when its epilogue is done, plus the attention phase's inputs / loop /
+ * merge), then the final norm's input arrival and the end of the LM head. NULL disables.
+ * *grid receives the number of workgroups. */
 int fl_state_profile(fl_state* st, uint64_t* buf, int32_t slots_per_wg, int32_t* grid);
 /* Diagnostics, no counterpart in the reference: device pointers of the last launch's
  * activations: residual h [D], this step's q/k/v (pair-interleaved: word hh*32+i holds dims i and
