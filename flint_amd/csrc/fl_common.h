@@ -60,7 +60,8 @@ __device__ __forceinline__ DqConst dq_const(uint32_t szw) {
 // fixed: the three-address (VOP3P) v_dot2_f32_bf16 needs no copy of its shared accumulator, and
 // every value is consumed at least three instructions after it is written (a VOP3P dot reading
 // a VGPR written just before it must be separated from the write; the compiler does not track
-// that across inline asm).
+// that across inline asm). The block ends with two wait states, so the outputs may feed an
+// MFMA or a VOP3P instruction right away (the compiler sees no VALU write inside the asm).
 template <int J>
 __device__ __forceinline__ void dq_step4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
                                          const DqConst& k, uint32_t magic, uint32_t one_lo,
@@ -103,7 +104,8 @@ __device__ __forceinline__ void dq_step4(uint32_t w0, uint32_t w1, uint32_t w2, 
       "v_cvt_pk_bf16_f32 %[o0], %[d00], %[d01]\n\t"
       "v_cvt_pk_bf16_f32 %[o1], %[d10], %[d11]\n\t"
       "v_cvt_pk_bf16_f32 %[o2], %[d20], %[d21]\n\t"
-      "v_cvt_pk_bf16_f32 %[o3], %[d30], %[d31]"
+      "v_cvt_pk_bf16_f32 %[o3], %[d30], %[d31]\n\t"
+      "s_nop 1"
       : [m0] "=&v"(m0), [m1] "=&v"(m1), [m2] "=&v"(m2), [m3] "=&v"(m3),
         [p00] "=&v"(p00), [p01] "=&v"(p01), [p10] "=&v"(p10), [p11] "=&v"(p11),
         [p20] "=&v"(p20), [p21] "=&v"(p21), [p30] "=&v"(p30), [p31] "=&v"(p31),
@@ -141,6 +143,28 @@ __device__ __forceinline__ float chunk_dot(const uint4 w, uint32_t szw, const ui
     acc = dot2_bf16(d[3][i], x[i].w, acc);
   }
   return acc;
+}
+
+// ---- int4 x bf16 on the matrix cores (M <= 16 activation rows) --------------------------------
+// v_mfma_f32_16x16x32_bf16 lane layout (wave64): A fragment of lane l = row l%16, k (l/16)*8..+8;
+// B fragment = column l%16, the same k; result D = column l%16, rows (l/16)*4 + 0..3.
+// One 16-byte chunk (4 packed words = 32 weights of one 128-group) feeds four MFMA steps: lane
+// (r = l%16, c = l/16) holds chunk c of group u of weight row r, and MFMA step e contracts the
+// 32 k-values {128u + 32c + 8e + t}, so word e of the chunk is the B fragment and the matching
+// 16 bytes of each activation row the A fragment (a permuted k order; every k appears once).
+typedef __bf16 fl_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float fl_f32x4 __attribute__((ext_vector_type(4)));
+
+// acc += X(rows, the chunk's 32 k) . W(this lane's row, same k)^T; d from dq32, xa[e] = 8 bf16
+// of this lane's activation row at k = 128u + 32c + 8e
+__device__ __forceinline__ void mfma_chunk(const uint32_t (&d)[4][4], const uint4 (&xa)[4],
+                                           fl_f32x4& acc) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint4 bw = make_uint4(d[0][e], d[1][e], d[2][e], d[3][e]);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(fl_bf16x8, xa[e]),
+                                                  __builtin_bit_cast(fl_bf16x8, bw), acc, 0, 0, 0);
+  }
 }
 
 // nibble position of element e (0..7) within its packed word

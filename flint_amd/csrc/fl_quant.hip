@@ -133,6 +133,54 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(const uint32_t* __restric
   if (row < rows && li == 0) y[r0 + row] = (uint16_t)f2bf(acc);
 }
 
+// Y[M, N] = bf16(X[M, K] . dq[N, K]^T), 1 <= M <= 16, on the matrix cores: one workgroup of 4
+// waves per 16-row tile of W; the waves take the K/128 groups round-robin, each lane dequantises
+// one 16-byte chunk per group (row n0 + l%16, chunk l/16) and feeds it to four MFMA steps, so
+// every weight is read and dequantised once for all M rows. Activation fragments are read from
+// global memory (rows >= M and rows >= N come back as zero from range-checked loads); the four
+// waves' partial tiles are summed in LDS in a fixed order.
+constexpr int kGemmWaves = 4;
+
+__global__ __launch_bounds__(64 * kGemmWaves) void k_gemm(const uint32_t* __restrict__ q,
+                                                          const uint32_t* __restrict__ sz,
+                                                          const uint16_t* __restrict__ x,
+                                                          uint16_t* __restrict__ y, int m, int n,
+                                                          int k) {
+  __shared__ float part[kGemmWaves][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, c = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int rows = min(16, n - n0);
+  const int groups = k >> 7;
+  const auto wr = buf_rsrc(q + (size_t)n0 * (k >> 3), (uint32_t)rows * (uint32_t)(k >> 1));
+  const auto sr = buf_rsrc(sz + (size_t)n0 * groups, (uint32_t)rows * (uint32_t)groups * 4u);
+  const auto xr = buf_rsrc(x, (uint32_t)m * (uint32_t)k * 2u);
+  const uint32_t woff = (uint32_t)r * (uint32_t)(k >> 1) + (uint32_t)c * 16u;   // bytes
+  const uint32_t xoff = (uint32_t)r * (uint32_t)k * 2u + (uint32_t)c * 64u;     // bytes
+  fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int u = wave; u < groups; u += kGemmWaves) {
+    const uint4 w = buf_ld128(wr, woff + (uint32_t)u * 64u);
+    const uint32_t s = buf_ld32(sr, ((uint32_t)r * (uint32_t)groups + (uint32_t)u) * 4u);
+    uint4 xa[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xa[e] = buf_ld128(xr, xoff + (uint32_t)u * 256u + (uint32_t)e * 16u);
+    uint32_t d[4][4];
+    dq32(w, dq_const(s), d);
+    mfma_chunk(d, xa, acc);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) part[wave][(c * 4 + i) * 16 + r] = acc[i];
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < 256) {
+    const int row = t >> 4, col = t & 15;  // activation row (token), weight row in the tile
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kGemmWaves; ++w) v += part[w][t];
+    if (row < m && col < rows) y[(size_t)row * n + n0 + col] = (uint16_t)f2bf(v);
+  }
+}
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 }  // namespace
@@ -176,6 +224,16 @@ int fl_gemv_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint1
   const size_t shm = (size_t)k * 2 + (size_t)rows * cpr * 4;
   hipLaunchKernelGGL(k_gemv, dim3(blocks), dim3(kGemvThreads), shm, as_stream(stream), q, sz, x, y,
                      n, k, rows);
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+}
+
+int fl_gemm_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint16_t* y, int32_t m,
+                 int32_t n, int32_t k, void* stream) {
+  if (!q || !sz || !x || !y || n <= 0 || k <= 0 || (k % FL_GROUP) != 0) return FL_E_ARG;
+  if (m < 1 || m > FL_MAX_VERIFY) return FL_E_M;
+  if ((int64_t)n * (k / 2) > 0xFFFFFFFFll || (int64_t)m * k * 2 > 0xFFFFFFFFll) return FL_E_ARG;
+  hipLaunchKernelGGL(k_gemm, dim3((n + 15) / 16), dim3(64 * kGemmWaves), 0, as_stream(stream), q,
+                     sz, x, y, m, n, k);
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
 

@@ -3,11 +3,6 @@
 
 extern "C" {
 
-int fl_gemm_int4(const uint32_t*, const uint32_t*, const uint16_t*, uint16_t*, int32_t, int32_t,
-                 int32_t, void*) {
-  return FL_E_ARG;
-}
-
 int fl_verify(const fl_weights*, fl_state*, const int32_t*, int32_t, const int32_t*,
               const uint8_t*, int32_t, int32_t*, float*, uint16_t*, void*) {
   return FL_E_ARG;

@@ -89,3 +89,45 @@ def test_gemv_matches_oracle_linear(dev):
     mism = (y != ref).float().mean().item()
     log(f"gemv vs oracle linear: max|diff|={diff:.3e} mismatch={mism:.2e}")
     assert mism < 2e-3 and diff < 2e-2
+
+
+GEMM_CASES = [(3584, 2560, 5), (2560, 8192, 8), (16384, 2560, 16), (24, 384, 3), (8, 128, 1),
+              (2560, 2560, 2)]
+
+
+@pytest.mark.parametrize("n,k,m", GEMM_CASES)
+def test_gemm_vs_fp64(dev, n, k, m):
+    """M-row int4 GEMM on the matrix cores (verify's weight-read-once product): every output within
+    the fp32-accumulation bound of the exact product with the bit-exact dequantised weights."""
+    from flint_amd.quantize import quantize_int4, gemm_int4
+    from oracle import quant
+    w = _weights(n, k, 7)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    log(f"gemm n={n} k={k} m={m}")
+    q, sz = quantize_int4(w.to(dev))
+    y = gemm_int4(q, sz, x.to(dev)).cpu()
+    assert y.shape == (m, n)
+    dq = quant.dq_linear_weight(w).double()
+    ref = x.double() @ dq.t()
+    bound = k * 2.0 ** -24 * (x.double().abs() @ dq.abs().t()) + ref.abs() * 2.0 ** -8 + 1e-30
+    err = (y.double() - ref).abs()
+    assert bool((err <= bound).all()), float((err / bound).max())
+    mism = (y != ref.float().to(torch.bfloat16)).float().mean().item()
+    log(f"  bf16 mismatch rate vs fp64-rounded: {mism:.2e}")
+    assert mism < 2e-3
+
+
+def test_gemm_rows_match_gemv(dev):
+    """Row m of the M-row GEMM equals the M=1 GEMV of x[m] up to fp32 summation order."""
+    from flint_amd.quantize import quantize_int4, gemm_int4, gemv_int4
+    n, k, m = 3584, 2560, 8
+    w = _weights(n, k, 9)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(10)).to(torch.bfloat16)
+    q, sz = quantize_int4(w.to(dev))
+    y = gemm_int4(q, sz, x.to(dev)).cpu()
+    for i in range(m):
+        yv = gemv_int4(q, sz, x[i].contiguous().to(dev)).cpu()
+        d = (y[i].float() - yv.float()).abs()
+        assert float(d.max()) <= float(yv.float().abs().max()) * 2.0 ** -7
+        assert float((d > 0).float().mean()) < 2e-3
