@@ -66,6 +66,12 @@ struct DecodeParams {
   uint32_t epoch;              // epoch of this launch's first phase (5 per layer)
   unsigned long long* prof;    // optional per-workgroup phase timestamps (100 MHz clock)
   int prof_slots;
+  // verify only: M tokens, their RoPE depths, the [M][M] tree mask, per-token argmax output
+  int M;
+  const int32_t* tokens;
+  const int32_t* depth;
+  const uint8_t* amask;
+  int32_t* tokens_out;
 };
 
 // threadIdx.x / gridDim.x through an empty asm. Index math derived from them is then redone
@@ -735,6 +741,519 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
   }
 }
 
+// ================================ speculative verify ==================================
+// M <= 16 tokens through all layers in one persistent cooperative launch (reference
+// kernels/verify_mega.cu:106-244 verify_mega<M>): token m sits at cache slot pos+m, takes RoPE
+// position pos+depth[m] and attends to the cache [0, pos) plus the new tokens j with
+// amask[m][j] != 0. Same tag protocol and five phases per layer as k_decode. Every GEMM runs on
+// the matrix cores: a workgroup takes 16-row weight tiles, its 8 waves split the K groups, each
+// lane dequantises one 16-byte chunk per group and feeds four v_mfma_f32_16x16x32_bf16 steps
+// against the M token rows staged in LDS (rows >= M read a zero row), so each weight is read and
+// dequantised once for all M tokens. The tied LM head is an MFMA tile over the bf16 embedding.
+
+// dynamic LDS of k_verify: staged token rows [M + 1][D + 8] bf16 (row M stays zero), per-wave
+// tile partials [8][256] floats, then attention staging: q [64], new k [16][64], new v [16][64]
+// (bf16) and the unit's mask row [16]
+inline size_t verify_lds_bytes(int M, int D) {
+  const size_t xs = ((size_t)(M + 1) * (D + 8) * 2 + 15) & ~(size_t)15;
+  return xs + NWAVE * 256 * 4 + (64 + 2 * FL_MAX_VERIFY * 64) * 2 + FL_MAX_VERIFY;
+}
+
+// xs[m][k - k0] (row stride ld) = values of the tagged rows src[m * stride + k], m < M,
+// k0 <= k < k0 + kn (kn % 4 == 0), once every word carries `tag`; four 16-byte groups per thread
+// are requested before any is checked
+__device__ void stage_rows(const DecodeParams& p, const uint32_t* src, int stride, int M, int k0,
+                           int kn, uint32_t tag, uint16_t* xs, int ld) {
+  const int tid = tid_here();
+  const int gpr = kn >> 2, total = M * gpr;
+  auto ok = [tag](uint4 w) {
+    return ((w.x >> 16) == tag) & ((w.y >> 16) == tag) & ((w.z >> 16) == tag) & ((w.w >> 16) == tag);
+  };
+  for (int base = 0; base < total; base += 4 * NT) {
+    uint4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = min(base + tid + i * NT, total - 1);
+      const int m = idx / gpr, g = idx - m * gpr;
+      v[i] = ld_coh_u128(src + (size_t)m * stride + k0 + 4 * g);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = base + tid + i * NT;
+      if (idx < total) {
+        const int m = idx / gpr, g = idx - m * gpr;
+        uint4 w = v[i];
+        if (!ok(w)) {
+          const uint32_t* a = src + (size_t)m * stride + k0 + 4 * g;
+          w = spin_until(p, w, ok, [a]() { return ld_coh_u128(a); });
+        }
+        reinterpret_cast<uint2*>(xs + m * ld)[g] =
+            make_uint2((w.x & 0xFFFFu) | (w.y << 16), (w.z & 0xFFFFu) | (w.w << 16));
+      }
+    }
+  }
+}
+
+// rows m < M of xs: x <- bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)  (engine/model.py:237-242),
+// one wave per row
+__device__ void norm_rows(uint16_t* xs, int ld, int M, int D, const uint16_t* __restrict__ nw,
+                          float eps) {
+  const int lane = tid_here() & 63, wave = tid_here() >> 6;
+  for (int m = wave; m < M; m += NWAVE) {
+    uint4* row = reinterpret_cast<uint4*>(xs + m * ld);
+    float ss = 0.0f;
+    for (int i = lane; i < (D >> 3); i += 64) {
+      const uint4 v = row[i];
+      const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ss += bflo(in[j]) * bflo(in[j]);
+        ss += bfhi(in[j]) * bfhi(in[j]);
+      }
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)D + eps);
+    for (int i = lane; i < (D >> 3); i += 64) {
+      const uint4 v = row[i];
+      const uint4 g = reinterpret_cast<const uint4*>(nw)[i];
+      const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+      const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float na = rbf(bflo(in[j]) * r), nb = rbf(bfhi(in[j]) * r);
+        o[j] = pack_bf16x2(na * bflo(gw[j]), nb * bfhi(gw[j]));
+      }
+      row[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// acc += X(token rows of xs) . dq(rows n0 .. n0+rows of a [N, K] int4 matrix)^T over the groups
+// g0 .. g0+ng-1 (ng <= 32) of the K block staged in xs (xs column 0 = group g0); this wave takes
+// groups g0 + wave + 8i
+__device__ __forceinline__ void tile_mma_int4(const uint32_t* __restrict__ q,
+                                              const uint32_t* __restrict__ sz, int n0, int rows,
+                                              int K, int g0, int ng, const uint16_t* xs, int ld,
+                                              int M, fl_f32x4& acc) {
+  constexpr int GPW = 4;
+  const int lane = tid_here() & 63, wave = tid_here() >> 6;
+  const int r = lane & 15, c = lane >> 4;
+  const int groups = K >> 7;
+  const auto wr = buf_rsrc(q + (size_t)n0 * (K >> 3), (uint32_t)rows * (uint32_t)(K >> 1));
+  const auto sr = buf_rsrc(sz + (size_t)n0 * groups, (uint32_t)rows * (uint32_t)groups * 4u);
+  uint4 w[GPW];
+  uint32_t s[GPW];
+#pragma unroll
+  for (int i = 0; i < GPW; ++i) {
+    const int u = wave + NWAVE * i;
+    const uint32_t gg = (uint32_t)(g0 + u);
+    const bool in = u < ng;
+    w[i] = buf_ld128(wr, in ? (uint32_t)r * (uint32_t)(K >> 1) + gg * 64u + (uint32_t)c * 16u : 0xFFFFFFF0u);
+    s[i] = buf_ld32(sr, in ? ((uint32_t)r * (uint32_t)groups + gg) * 4u : 0xFFFFFFF0u);
+  }
+  const uint16_t* xrow = xs + (r < M ? r : M) * ld + c * 32;
+#pragma unroll
+  for (int i = 0; i < GPW; ++i) {
+    const int u = wave + NWAVE * i;
+    if (u < ng) {  // wave-uniform
+      uint4 xa[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xa[e] = *reinterpret_cast<const uint4*>(xrow + u * 128 + e * 8);
+      uint32_t d[4][4];
+      dq32(w[i], dq_const(s[i]), d);
+      mfma_chunk(d, xa, acc);
+    }
+  }
+}
+
+// the waves' tile partials -> part[wave][token * 16 + row]; ends with a barrier
+__device__ __forceinline__ void tile_publish(float* part, const fl_f32x4& acc) {
+  const int lane = tid_here() & 63, wave = tid_here() >> 6;
+  const int r = lane & 15, c = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) part[wave * 256 + (c * 4 + i) * 16 + r] = acc[i];
+  lds_barrier();
+}
+// sum over the waves (fixed order) of entry t = token * 16 + row
+__device__ __forceinline__ float tile_sum(const float* part, int t) {
+  float v = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) v += part[w * 256 + t];
+  return v;
+}
+
+// attention of every (query head, token) unit (engine/model.py:171-179 over the verify key set)
+__device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
+                                 uint16_t* att, uint8_t* amk, float* wpart) {
+  constexpr int RB = 12;
+  const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+  const int kk = lane >> 3, ds = lane & 7;
+  const int M = p.M, pos = p.pos, NH = p.NH, NKV = p.NKV, QPG = p.NH / p.NKV;
+  const int HALF = (NH + 2 * NKV) * 32;  // tagged pairs per token
+  const int ns = (pos + 7) >> 3;         // 8-key steps over the cached keys [0, pos)
+  const int nrounds = (ns + NWAVE * RB - 1) / (NWAVE * RB);
+  const float sc = p.attn_scale * 1.4426950408889634f;
+  const uint32_t* att32 = reinterpret_cast<const uint32_t*>(att);
+  for (int u = blockIdx.x; u < NH * M; u += gridDim.x) {
+    const int g = u % NKV, rest = u / NKV, j = rest % QPG, m = rest / QPG;
+    const int hq = g * QPG + j;
+    const size_t cbase = (size_t)(l * NKV + g) * p.S * 64;
+    const auto kb = buf_rsrc(p.kc + cbase, (uint32_t)pos * 128u);
+    const auto vb = buf_rsrc(p.vc + cbase, (uint32_t)pos * 128u);
+    uint4 kr[RB], vr[RB];
+    auto issue = [&](int r) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const uint32_t off = (uint32_t)(((r * NWAVE * RB + wave + NWAVE * i) * 8 + kk) * 128 + ds * 16);
+        kr[i] = buf_ld128(kb, off);
+        vr[i] = buf_ld128(vb, off);
+      }
+    };
+    if (nrounds > 0) issue(0);
+    // LDS: q of (hq, token m), then new k / v of group g for tokens 0..M-1 (bf16 [16][64] each)
+    for (int i = tid; i < 32 + 64 * M; i += NT) {
+      int hh, tok, d, dst;
+      if (i < 32) {
+        hh = hq, tok = m, d = i, dst = 0;
+      } else {
+        const int i2 = i - 32, which = i2 / (32 * M), r2 = i2 - which * 32 * M;
+        tok = r2 >> 5, d = r2 & 31;
+        hh = which ? NH + NKV + g : NH + g;
+        dst = 64 + which * FL_MAX_VERIFY * 64 + tok * 64;
+      }
+      const unsigned long long v = wait_pair(p, p.qkv + (size_t)tok * HALF + hh * 32 + d, qtag);
+      att[dst + d] = (uint16_t)v;
+      att[dst + d + 32] = (uint16_t)(v >> 16);
+    }
+    if (tid < M) amk[tid] = p.amask[m * M + tid];
+    lds_barrier();
+    uint32_t qv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[e] = att32[ds * 4 + e];
+    float mx = -INFINITY, lsum = 0.0f, o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+    for (int r = 0; r < nrounds; ++r) {
+      if (r > 0) issue(r);
+      float s[RB];
+      float rmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int st = r * NWAVE * RB + wave + NWAVE * i;
+        float a = dot2_bf16(kr[i].x, qv[0], 0.0f);
+        a = dot2_bf16(kr[i].y, qv[1], a);
+        a = dot2_bf16(kr[i].z, qv[2], a);
+        a = dot2_bf16(kr[i].w, qv[3], a);
+        a = sum8(a);
+        s[i] = (st * 8 + kk < pos) ? a * sc : -INFINITY;
+        rmax = fmaxf(rmax, s[i]);
+      }
+      const float mn = fmaxf(mx, max_stride8(rmax));
+      const float mu = (mn == -INFINITY) ? 0.0f : mn;
+      const float corr = __builtin_amdgcn_exp2f(mx - mu);
+      lsum *= corr;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= corr;
+      mx = mn;
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const float pw = __builtin_amdgcn_exp2f(s[i] - mu);
+        lsum += pw;
+        o[0] = __builtin_fmaf(pw, bflo(vr[i].x), o[0]);
+        o[1] = __builtin_fmaf(pw, bfhi(vr[i].x), o[1]);
+        o[2] = __builtin_fmaf(pw, bflo(vr[i].y), o[2]);
+        o[3] = __builtin_fmaf(pw, bfhi(vr[i].y), o[3]);
+        o[4] = __builtin_fmaf(pw, bflo(vr[i].z), o[4]);
+        o[5] = __builtin_fmaf(pw, bfhi(vr[i].z), o[5]);
+        o[6] = __builtin_fmaf(pw, bflo(vr[i].w), o[6]);
+        o[7] = __builtin_fmaf(pw, bfhi(vr[i].w), o[7]);
+      }
+    }
+    if (wave == 0) {  // the new tokens' keys, 8 per step, masked by amask[m][.]
+      for (int s0 = 0; s0 < M; s0 += 8) {
+        const int jn = s0 + kk;
+        const bool valid = jn < M && amk[min(jn, M - 1)] != 0;
+        const int js = min(jn, M - 1);
+        const uint32_t* kw = att32 + 32 + js * 32 + ds * 4;
+        const uint32_t* vw = att32 + 32 + FL_MAX_VERIFY * 32 + js * 32 + ds * 4;
+        float a = dot2_bf16(kw[0], qv[0], 0.0f);
+        a = dot2_bf16(kw[1], qv[1], a);
+        a = dot2_bf16(kw[2], qv[2], a);
+        a = dot2_bf16(kw[3], qv[3], a);
+        a = sum8(a);
+        const float sn = valid ? a * sc : -INFINITY;
+        const float mn = fmaxf(mx, max_stride8(sn));
+        const float mu = (mn == -INFINITY) ? 0.0f : mn;
+        const float corr = __builtin_amdgcn_exp2f(mx - mu);
+        const float pw = __builtin_amdgcn_exp2f(sn - mu);
+        lsum = lsum * corr + pw;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[2 * e] = __builtin_fmaf(pw, bflo(vw[e]), o[2 * e] * corr);
+          o[2 * e + 1] = __builtin_fmaf(pw, bfhi(vw[e]), o[2 * e + 1] * corr);
+        }
+        mx = mn;
+      }
+    }
+    lsum = sum_stride8(lsum);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = sum_stride8(o[e]);
+    float* mywp = wpart + wave * 66;
+    if (kk == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mywp[2 + ds * 8 + e] = o[e];
+    }
+    if (lane == 0) {
+      mywp[0] = mx;
+      mywp[1] = lsum;
+    }
+    lds_barrier();
+    if (tid < 64) {
+      float M_ = -INFINITY, Ls = 0.0f, O = 0.0f;
+      for (int w = 0; w < NWAVE; ++w) M_ = fmaxf(M_, wpart[w * 66]);
+      for (int w = 0; w < NWAVE; ++w) {
+        const float* wp = wpart + w * 66;
+        const float e = (wp[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wp[0] - M_);
+        Ls += wp[1] * e;
+        O += wp[2 + tid] * e;
+      }
+      st_coh_u32(p.attn + (size_t)m * p.D + hq * 64 + tid, f2bf(O / Ls) | (otag << 16));
+    }
+    lds_barrier();
+  }
+}
+
+__global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
+  extern __shared__ __align__(16) unsigned char vsm[];
+  const int tid = threadIdx.x, wg = blockIdx.x, G = gridDim.x;
+  const int D = p.D, F = p.F, NH = p.NH, NKV = p.NKV, M = p.M, pos = p.pos;
+  const int NQKV = (NH + 2 * NKV) * 64, HALF = NQKV / 2;
+  const int ld = D + 8;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(vsm);
+  float* part = reinterpret_cast<float*>(vsm + (((size_t)(M + 1) * ld * 2 + 15) & ~(size_t)15));
+  uint16_t* att = reinterpret_cast<uint16_t*>(part + NWAVE * 256);
+  uint8_t* amk = reinterpret_cast<uint8_t*>(att + 64 + 2 * FL_MAX_VERIFY * 64);
+  for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + M * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
+
+  auto token_at = [&](int m) {
+    int t = p.tokens[m];
+    if (t < 0 || t >= p.V) {
+      if (tid == 0 && wg == 0)
+        __hip_atomic_store(p.err, (int32_t)FL_E_ARG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      t = 0;
+    }
+    return t;
+  };
+  auto rope_pos = [&](int m) {
+    int r = pos + p.depth[m];
+    if (r < 0 || r >= p.w.rope_len) {
+      if (tid == 0 && wg == 0)
+        __hip_atomic_store(p.err, (int32_t)FL_E_POS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      r = min(max(r, 0), p.w.rope_len - 1);
+    }
+    return r;
+  };
+
+  for (int l = 0; l < p.NL; ++l) {
+    const uint32_t e0 = p.epoch + 5u * (uint32_t)l;
+    const uint32_t t_prev = tag_of(e0 - 1), t_qkv = tag_of(e0), t_attn = tag_of(e0 + 1),
+                   t_h1 = tag_of(e0 + 2), t_act = tag_of(e0 + 3), t_h2 = tag_of(e0 + 4);
+    // ---------------- P1: RMSNorm + QKV + RoPE + KV append ----------------
+    if (wg < NQKV / 16) {
+      if (l == 0) {  // bf16(embed[token] * emb_mult)  (engine/model.py:138)
+        for (int i = tid; i < M * (D >> 1); i += NT) {
+          const int m = i / (D >> 1), c = i - m * (D >> 1);
+          const uint32_t e2 = reinterpret_cast<const uint32_t*>(p.w.embed + (size_t)token_at(m) * D)[c];
+          reinterpret_cast<uint32_t*>(xs + m * ld)[c] =
+              pack_bf16x2(rbf(bflo(e2) * p.emb_mult), rbf(bfhi(e2) * p.emb_mult));
+        }
+      } else {
+        stage_rows(p, p.h, D, M, 0, D, t_prev, xs, ld);
+      }
+      lds_barrier();
+      norm_rows(xs, ld, M, D, p.w.attn_norm + (size_t)l * D, p.eps);
+      lds_barrier();
+      for (int t = wg; t < NQKV / 16; t += G) {
+        const int n0 = t * 16;
+        fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        tile_mma_int4(p.w.wqkv_q + (size_t)l * NQKV * (D >> 3), p.w.wqkv_sz + (size_t)l * NQKV * (D >> 7),
+                      n0, 16, D, 0, D >> 7, xs, ld, M, acc);
+        tile_publish(part, acc);
+        if (tid < 128) {  // (token, NEOX pair) of the tile
+          const int m = tid >> 3, pp = tid & 7;
+          if (m < M) {
+            const float a = rbf(tile_sum(part, m * 16 + 2 * pp)), b = rbf(tile_sum(part, m * 16 + 2 * pp + 1));
+            const int srow = n0 + 2 * pp;
+            const int hh = srow >> 6, j = (srow & 63) >> 1;
+            float oa = a, ob = b;
+            if (hh < NH + NKV) {  // RoPE at pos + depth[m] (engine/model.py:257-269)
+              const uint32_t cs = reinterpret_cast<const uint32_t*>(p.w.rope)[rope_pos(m) * 32 + j];
+              const float cc = bflo(cs), sn = bfhi(cs);
+              oa = rbf(a * cc - b * sn);
+              ob = rbf(b * cc + a * sn);
+            }
+            st_coh_u64(p.qkv + (size_t)m * HALF + hh * 32 + j,
+                       (unsigned long long)pack_bf16x2(oa, ob) | ((unsigned long long)t_qkv << 32));
+            if (hh >= NH) {  // KV append at slot pos + m
+              const int g = (hh < NH + NKV) ? hh - NH : hh - NH - NKV;
+              uint16_t* dst = ((hh < NH + NKV) ? p.kc : p.vc) + ((size_t)(l * NKV + g) * p.S + pos + m) * 64;
+              dst[j] = (uint16_t)f2bf(oa);
+              dst[j + 32] = (uint16_t)f2bf(ob);
+            }
+          }
+        }
+        lds_barrier();
+      }
+    }
+    // ---------------- P2: attention ----------------
+    attention_verify(p, l, t_qkv, t_attn, att, amk, part);
+    // ---------------- P3: O projection + residual ----------------
+    if (wg < D / 16) {
+      stage_rows(p, p.attn, D, M, 0, D, t_attn, xs, ld);
+      lds_barrier();
+      for (int t = wg; t < D / 16; t += G) {
+        const int n0 = t * 16;
+        fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        tile_mma_int4(p.w.wo_q + (size_t)l * D * (D >> 3), p.w.wo_sz + (size_t)l * D * (D >> 7), n0, 16,
+                      D, 0, D >> 7, xs, ld, M, acc);
+        tile_publish(part, acc);
+        if (tid < 256) {
+          const int m = tid >> 4, n = tid & 15;
+          if (m < M) {
+            const int row = n0 + n;
+            float hold;
+            if (l == 0) {
+              hold = rbf(bf2f(p.w.embed[(size_t)token_at(m) * D + row]) * p.emb_mult);
+            } else {  // this thread wrote the word in the previous layer's down phase
+              hold = bflo(ld_coh_u32(p.h + (size_t)m * D + row));
+            }
+            const float o = rbf(rbf(tile_sum(part, tid)) * p.resid_mult);
+            st_coh_u32(p.h + (size_t)m * D + row, f2bf(hold + o) | (t_h1 << 16));
+          }
+        }
+        lds_barrier();
+      }
+    }
+    // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
+    if (wg < (2 * F) / 16) {
+      stage_rows(p, p.h, D, M, 0, D, t_h1, xs, ld);
+      lds_barrier();
+      norm_rows(xs, ld, M, D, p.w.ffn_norm + (size_t)l * D, p.eps);
+      lds_barrier();
+      for (int t = wg; t < (2 * F) / 16; t += G) {
+        const int n0 = t * 16;
+        fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        tile_mma_int4(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3), p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7),
+                      n0, 16, D, 0, D >> 7, xs, ld, M, acc);
+        tile_publish(part, acc);
+        if (tid < 128) {
+          const int m = tid >> 3, pp = tid & 7;
+          if (m < M) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
+            const float gg = rbf(tile_sum(part, m * 16 + 2 * pp)), uu = rbf(tile_sum(part, m * 16 + 2 * pp + 1));
+            st_coh_u32(p.act + (size_t)m * F + (n0 >> 1) + pp, f2bf(rbf(silu_f(gg)) * uu) | (t_act << 16));
+          }
+        }
+        lds_barrier();
+      }
+    }
+    // ---------------- P5: down projection + residual (K staged in blocks of D) ----------------
+    if (wg < D / 16) {
+      for (int t = wg; t < D / 16; t += G) {
+        const int n0 = t * 16;
+        fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k0 = 0; k0 < F; k0 += D) {
+          const int kn = min(D, F - k0);
+          stage_rows(p, p.act, F, M, k0, kn, t_act, xs, ld);
+          lds_barrier();
+          tile_mma_int4(p.w.wd_q + (size_t)l * D * (F >> 3), p.w.wd_sz + (size_t)l * D * (F >> 7), n0, 16,
+                        F, k0 >> 7, kn >> 7, xs, ld, M, acc);
+          lds_barrier();
+        }
+        tile_publish(part, acc);
+        if (tid < 256) {
+          const int m = tid >> 4, n = tid & 15;
+          if (m < M) {
+            const int row = n0 + n;
+            const float hold = bflo(ld_coh_u32(p.h + (size_t)m * D + row));  // written in P3 by this thread
+            const float o = rbf(rbf(tile_sum(part, tid)) * p.resid_mult);
+            st_coh_u32(p.h + (size_t)m * D + row, f2bf(hold + o) | (t_h2 << 16));
+          }
+        }
+        lds_barrier();
+      }
+    }
+  }
+
+  // ---------------- final norm + tied bf16 LM head + per-token argmax ----------------
+  const int ntile = (p.V + 15) / 16;
+  unsigned long long best = 0ull;
+  if (wg < ntile || (p.feat && wg == 0)) {
+    stage_rows(p, p.h, D, M, 0, D, tag_of(p.epoch + 5u * (uint32_t)p.NL - 1u), xs, ld);
+    lds_barrier();
+    norm_rows(xs, ld, M, D, p.w.final_norm, p.eps);
+    lds_barrier();
+    if (p.feat && wg == 0)
+      for (int i = tid; i < M * D; i += NT) p.feat[i] = xs[(i / D) * ld + (i % D)];
+    const int lane = tid & 63, wave = tid >> 6, r = lane & 15, c = lane >> 4;
+    const int ksteps = D >> 5;
+    for (int t = wg; t < ntile; t += G) {
+      const int n0 = t * 16;
+      const int rows = min(16, p.V - n0);
+      const auto er = buf_rsrc(p.w.embed + (size_t)n0 * D, (uint32_t)rows * (uint32_t)D * 2u);
+      const uint16_t* xrow = xs + (r < M ? r : M) * ld + c * 8;
+      fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      constexpr int SPW = 16;  // k-steps per wave (D <= 4096)
+      uint4 bw[SPW];
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) {
+        const int s = wave + NWAVE * i;
+        bw[i] = buf_ld128(er, s < ksteps ? (uint32_t)(r * D + s * 32 + c * 8) * 2u : 0xFFFFFFF0u);
+      }
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) {
+        const int s = wave + NWAVE * i;
+        if (s < ksteps) {
+          const uint4 xa = *reinterpret_cast<const uint4*>(xrow + s * 32);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(fl_bf16x8, xa),
+                                                        __builtin_bit_cast(fl_bf16x8, bw[i]), acc, 0, 0, 0);
+        }
+      }
+      tile_publish(part, acc);
+      if (tid < 256) {
+        const int m = tid >> 4, n = tid & 15;
+        if (m < M && n < rows) {
+          // logits = bf16(bf16(x . E^T) / logits_scaling)  (engine/model.py:144)
+          const float lg = rbf(rbf(tile_sum(part, tid)) / p.logits_scaling);
+          if (p.logits) p.logits[(size_t)m * p.V + n0 + n] = lg;
+          best = u64max(best, amax_key(lg, (uint32_t)(n0 + n)));
+        }
+      }
+      lds_barrier();
+    }
+  }
+  // per-token argmax: the 16 threads of a token row are lanes 16k..16k+15 of one wave
+  if (tid < 256) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) best = u64max(best, (unsigned long long)__shfl_xor(best, o, 64));
+    const int m = tid >> 4;
+    if ((tid & 15) == 0 && m < M && best != 0ull)
+      __hip_atomic_fetch_max(p.amax + m, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  wait_mem();
+  lds_barrier();
+  if (tid == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(p.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == (uint32_t)(G - 1)) {
+      for (int m = 0; m < M; ++m) {
+        p.tokens_out[m] = (int32_t)amax_index(ld_coh_u64(p.amax + m));
+        __hip_atomic_store(p.amax + m, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 int phase_fits(int n, int k, int G, int cap) {
@@ -754,6 +1273,7 @@ struct fl_state {
   unsigned long long* qkv;
   unsigned long long* part;
   int att_spw;
+  int verify_ok;  // k_verify's dynamic LDS fits and a grid of it is co-resident
   unsigned long long* amax;
   uint32_t* done;
   int32_t* err;
@@ -774,6 +1294,47 @@ int dev_alloc(fl_state* st, T** p, size_t count) {
   st->blocks[st->nblocks++] = v;
   *p = reinterpret_cast<T*>(v);
   return FL_OK;
+}
+}  // namespace
+
+namespace {
+bool weights_ok(const fl_weights* w) {
+  return w && w->wqkv_q && w->wqkv_sz && w->wo_q && w->wo_sz && w->wgu_q && w->wgu_sz && w->wd_q &&
+         w->wd_sz && w->attn_norm && w->ffn_norm && w->final_norm && w->embed && w->rope &&
+         w->rope_len > 0;
+}
+
+DecodeParams base_params(const fl_weights* w, fl_state* st, int pos) {
+  DecodeParams p;
+  memset(&p, 0, sizeof(p));
+  p.w = *w;
+  p.kc = st->kc;
+  p.vc = st->vc;
+  p.h = st->h;
+  p.qkv = st->qkv;
+  p.attn = st->attn;
+  p.act = st->act;
+  p.part = st->part;
+  p.att_spw = st->att_spw;
+  p.amax = st->amax;
+  p.done = st->done;
+  p.err = st->err;
+  p.D = st->d.dim;
+  p.NH = st->d.n_head;
+  p.NKV = st->d.n_kv_head;
+  p.F = st->d.inter;
+  p.V = st->d.vocab;
+  p.NL = st->d.n_layer;
+  p.S = st->max_seq;
+  p.pos = pos;
+  p.eps = st->d.norm_eps;
+  p.emb_mult = st->d.emb_mult;
+  p.attn_scale = st->d.attn_scale;
+  p.resid_mult = st->d.resid_mult;
+  p.logits_scaling = st->d.logits_scaling;
+  p.epoch = st->epoch;
+  p.M = 1;
+  return p;
 }
 }  // namespace
 
@@ -827,6 +1388,20 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   if (const char* e = getenv("FLINT_AMD_ATT_STEPS")) {  // tuning knob: steps per wave per slice
     const int v = atoi(e);
     if (v >= 1 && v <= 64) st->att_spw = v;
+  }
+  // speculative verify: its dynamic LDS (token rows staged for the matrix cores) must fit, and a
+  // full grid of it must be co-resident
+  st->verify_ok = 0;
+  if (D <= 4096) {
+    const size_t vl = verify_lds_bytes(FL_MAX_VERIFY, D);
+    int vocc = 0;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_verify),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)vl) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&vocc, reinterpret_cast<const void*>(k_verify),
+                                                     NT, vl) == hipSuccess &&
+        vocc >= 1)
+      st->verify_ok = 1;
+    (void)hipGetLastError();
   }
   int rc = FL_OK;
   if (rc == FL_OK) rc = dev_alloc(st, &st->h, (size_t)D * FL_MAX_VERIFY);
@@ -891,49 +1466,43 @@ int fl_state_check(fl_state* st, void* stream) {
 
 int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, int32_t pos,
                    int32_t* token_out, float* logits, uint16_t* feat, void* stream) {
-  if (!w || !st || !token_in || !token_out) return FL_E_ARG;
-  if (!w->wqkv_q || !w->wqkv_sz || !w->wo_q || !w->wo_sz || !w->wgu_q || !w->wgu_sz || !w->wd_q ||
-      !w->wd_sz || !w->attn_norm || !w->ffn_norm || !w->final_norm || !w->embed || !w->rope)
-    return FL_E_ARG;
+  if (!st || !token_in || !token_out || !weights_ok(w)) return FL_E_ARG;
   if (pos < 0 || pos >= st->max_seq || pos >= w->rope_len) return FL_E_POS;
-  DecodeParams p;
-  memset(&p, 0, sizeof(p));
-  p.w = *w;
-  p.kc = st->kc;
-  p.vc = st->vc;
-  p.h = st->h;
-  p.qkv = st->qkv;
-  p.attn = st->attn;
-  p.act = st->act;
-  p.part = st->part;
-  p.att_spw = st->att_spw;
-  p.amax = st->amax;
-  p.done = st->done;
-  p.err = st->err;
+  DecodeParams p = base_params(w, st, pos);
   p.token_in = token_in;
   p.token_out = token_out;
   p.logits = logits;
   p.feat = feat;
-  p.D = st->d.dim;
-  p.NH = st->d.n_head;
-  p.NKV = st->d.n_kv_head;
-  p.F = st->d.inter;
-  p.V = st->d.vocab;
-  p.NL = st->d.n_layer;
-  p.S = st->max_seq;
-  p.pos = pos;
-  p.eps = st->d.norm_eps;
-  p.emb_mult = st->d.emb_mult;
-  p.attn_scale = st->d.attn_scale;
-  p.resid_mult = st->d.resid_mult;
-  p.logits_scaling = st->d.logits_scaling;
-  p.epoch = st->epoch;
   p.prof = st->prof;
   p.prof_slots = st->prof_slots;
   void* args[] = {&p};
   const hipError_t e =
       hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode), dim3(st->grid),
                                  dim3(NT), args, 0, as_stream(stream));
+  if (e != hipSuccess) return FL_E_LAUNCH;
+  st->epoch += 5u * (uint32_t)st->d.n_layer;
+  return FL_OK;
+}
+
+int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t m,
+              const int32_t* depth, const uint8_t* amask, int32_t pos, int32_t* tokens_out,
+              float* logits, uint16_t* feat, void* stream) {
+  if (!st || !tokens || !depth || !amask || !tokens_out || !weights_ok(w)) return FL_E_ARG;
+  if (m < 1 || m > FL_MAX_VERIFY) return FL_E_M;
+  if (pos < 0 || pos + m > st->max_seq) return FL_E_POS;
+  if (!st->verify_ok) return FL_E_ARG;
+  DecodeParams p = base_params(w, st, pos);
+  p.M = m;
+  p.tokens = tokens;
+  p.depth = depth;
+  p.amask = amask;
+  p.tokens_out = tokens_out;
+  p.logits = logits;
+  p.feat = feat;
+  void* args[] = {&p};
+  const hipError_t e = hipLaunchCooperativeKernel(
+      reinterpret_cast<const void*>(k_verify), dim3(st->grid), dim3(NT), args,
+      (unsigned)verify_lds_bytes(m, st->d.dim), as_stream(stream));
   if (e != hipSuccess) return FL_E_LAUNCH;
   st->epoch += 5u * (uint32_t)st->d.n_layer;
   return FL_OK;
