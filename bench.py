@@ -82,6 +82,49 @@ def cpu_baseline(args, sd, ctx, steps):
                       f"40-layer model via aten::_weight_int4pack_mm_for_cpu; {model}"}
 
 
+def verify_latency(model, args, dev, ctx=1024, reps=20):
+    """accept-agnostic latency of one speculative verify pass over M = k+1
+    tokens (k = 4, 7; chain mask) at context `ctx`, beside the M = 1 decode step latency at the
+    same context. The cache prefix is synthetic (random bf16 rows): the timing depends only on
+    its length."""
+    need = ctx + 32
+    if model.max_seq_length < need:
+        model.setup_caches(1, need)
+    g = torch.Generator(device=dev).manual_seed(77)
+    model.k_cache[:, :, :ctx].normal_(generator=g)
+    model.v_cache[:, :, :ctx].normal_(generator=g)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / reps
+
+    tok = torch.randint(0, args.vocab_size, (16,), device=dev, dtype=torch.int32, generator=g)
+    out = torch.empty(1, dtype=torch.int32, device=dev)
+    dec_us = timed(lambda: model.decode_step(tok[:1], ctx, token_out=out))
+    res = {}
+    for m in (5, 8):
+        logits = torch.empty(m, args.vocab_size, dtype=torch.float32, device=dev)
+        feat = torch.empty(m, args.dim, dtype=torch.bfloat16, device=dev)
+        touts = torch.empty(m, dtype=torch.int32, device=dev)
+        depth = torch.arange(m, dtype=torch.int32, device=dev)
+        amask = torch.tril(torch.ones(m, m, dtype=torch.uint8, device=dev))
+        res[str(m)] = round(timed(lambda: model.verify(tok[:m], ctx, depth=depth, amask=amask,
+                                                       logits=logits, feat=feat,
+                                                       tokens_out=touts)), 1)
+    model.check()
+    return {"ctx": ctx, "decode_us": round(dec_us, 1), "verify_us": res,
+            "cost_vs_decode": {k: round(v / dec_us, 3) for k, v in res.items()}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -91,6 +134,8 @@ def main():
     ap.add_argument("--config", default="flint-3b")
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-verify", action="store_true",
+                    help="skip the speculative-verify latency of BASELINE config 4")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="after timing, run one device-to-device copy of this many MiB (the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -109,7 +154,7 @@ def main():
     sd = synth_weights(args, seed=0, device=dev)
     model = Transformer.from_weights(args, sd, dev)
     torch.cuda.synchronize()
-    total = a.ctx + a.warmup + a.steps + 8
+    total = max(a.ctx + a.warmup + a.steps + 8, 1024 + 32)  # + config 4's verify context
     model.setup_caches(1, total)
     g = torch.Generator().manual_seed(1234)
     prompt = torch.randint(0, args.vocab_size, (a.ctx,), generator=g, dtype=torch.int32).to(dev)
@@ -145,6 +190,12 @@ def main():
     achieved = mean_bytes / (ms * 1e-3) / 1e9
     log(f"{tok_s:.1f} tok/s, {ms * 1e3:.1f} us/step, {achieved:.0f} GB/s algorithmic "
         f"(wall {a.steps / wall:.1f} tok/s)")
+
+    verify = None
+    if not a.no_verify:
+        verify = verify_latency(model, args, dev)
+        log(f"verify at ctx {verify['ctx']}: decode {verify['decode_us']} us, "
+            f"verify {verify['verify_us']} us")
 
     if a.copy_probe_mb > 0:
         n = a.copy_probe_mb * (1 << 20)
@@ -185,6 +236,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(a.config, a.ctx)},
         "cpu_baseline": cpu,
+        "verify": verify,
     }
     print(json.dumps(out), flush=True)
 
