@@ -1267,7 +1267,8 @@ int phase_fits(int n, int k, int G, int cap) {
 struct fl_state {
   fl_model_desc d;
   int max_seq;
-  int grid;
+  int grid;   // decode workgroups (1 per CU)
+  int vgrid;  // verify workgroups (1 per CU)
   uint16_t *kc, *vc;
   uint32_t *h, *attn, *act;
   unsigned long long* qkv;
@@ -1381,6 +1382,7 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   st->d = *d;
   st->max_seq = max_seq;
   st->grid = G;
+  st->vgrid = cu;
   st->kc = k_cache;
   st->vc = v_cache;
   st->epoch = 1;
@@ -1501,7 +1503,7 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
   p.feat = feat;
   void* args[] = {&p};
   const hipError_t e = hipLaunchCooperativeKernel(
-      reinterpret_cast<const void*>(k_verify), dim3(st->grid), dim3(NT), args,
+      reinterpret_cast<const void*>(k_verify), dim3(st->vgrid), dim3(NT), args,
       (unsigned)verify_lds_bytes(m, st->d.dim), as_stream(stream));
   if (e != hipSuccess) return FL_E_LAUNCH;
   st->epoch += 5u * (uint32_t)st->d.n_layer;

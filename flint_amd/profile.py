@@ -26,9 +26,9 @@ def enable(model, slots=None):
     """Attach a timestamp buffer to the model's decode state; returns (buf, grid, slots)."""
     slots = slots or slots_per_launch(model.config.n_layer)
     grid = ctypes.c_int32()
-    ncu = ctypes.c_int32()
-    _lib.call("fl_device_info", ctypes.byref(ncu), None)
-    buf = torch.zeros(max(ncu.value, 1) * slots, dtype=torch.int64, device=model.device)
+    ncu, dgrid = ctypes.c_int32(), ctypes.c_int32()
+    _lib.call("fl_device_info", ctypes.byref(ncu), ctypes.byref(dgrid))
+    buf = torch.zeros(max(dgrid.value, ncu.value, 1) * slots, dtype=torch.int64, device=model.device)
     _lib.call("fl_state_profile", model._state, _lib.ptr(buf), slots, ctypes.byref(grid))
     return buf, grid.value, slots
 
