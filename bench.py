@@ -5,7 +5,9 @@ One "step" = one decoded token = ONE persistent cooperative kernel launch (fl_de
 the 40-layer 3B-class synthetic int4 model: all layers, final norm, tied bf16 LM head, greedy
 argmax. Tokens chain on the device (step i reads the token step i-1 wrote), so the timed loop
 has no host synchronisation. Weights are seeded random (no checkpoint exists); the prompt is
-512 seeded-uniform token ids prefilled before timing.
+512 seeded-uniform token ids prefilled before timing (through the verify kernel, 16 tokens per
+launch). After the timed decode, BASELINE config 4's speculative-verify latency (k = 4, 7 at
+context 1024) is measured beside the decode latency at the same context.
 
 Prints ONE JSON line (the driver's contract) with `roofline` (HBM-bound: algorithmic bytes per
 step / measured step time vs 8 TB/s) and `cpu_baseline` (the reference int4 decode path on the
@@ -160,12 +162,13 @@ def main():
     prompt = torch.randint(0, args.vocab_size, (a.ctx,), generator=g, dtype=torch.int32).to(dev)
     seq = torch.empty(a.ctx + a.warmup + a.steps, dtype=torch.int32, device=dev)
     seq[:a.ctx] = prompt
-    log(f"prefill {a.ctx} tokens")
-    scratch = torch.empty(1, dtype=torch.int32, device=dev)
-    for i in range(a.ctx - 1):
-        model.decode_step(seq[i:i + 1], i, token_out=scratch)
+    log(f"prefill {a.ctx} tokens (verify kernel, 16 tokens per launch)")
+    from flint_amd.generate import prefill
+    t0 = time.perf_counter()
+    prefill(model, seq[:a.ctx - 1], 0)
     torch.cuda.synchronize()
     model.check()
+    log(f"prefill took {1000 * (time.perf_counter() - t0):.1f} ms")
     p0 = a.ctx - 1
     log(f"warmup {a.warmup} steps")
     for i in range(a.warmup):

@@ -3,19 +3,41 @@
 Mirrors reference engine/generate.py:57-81,137-206 (prefill / decode_one_token / decode_n_tokens /
 generate) for greedy sampling and chat.py:71-96 (logits_at / pick / respond). Tokens stay on
 the device between steps: step i reads the token step i-1 wrote, so the loop issues launches
-back-to-back with no host synchronisation (gpt-fast's decode loop has none either).
+back-to-back with no host synchronisation (gpt-fast's decode loop has none either). The prompt
+is prefilled through the speculative-verify kernel, up to 16 tokens per launch.
 """
 import torch
 
 
-def prefill(model, x, input_pos):
+def prefill(model, x, input_pos, chunk=16):
     """Feed prompt tokens x (int32 device [T]) at positions input_pos[0]..; returns the greedy next
-    token (int32 device [1]). Prefill is one decode step per prompt token (reference chat.py:85-86)."""
+    token (int32 device [1]) after the last one (reference engine/generate.py:57-60, which runs
+    the prompt through one forward). The prompt goes through the verify kernel `chunk` (<= 16)
+    tokens per launch with a causal mask: each launch reads every weight once for the whole
+    chunk and appends the chunk's K/V rows."""
+    from . import _lib
     x = x.reshape(-1).to(device=model.device, dtype=torch.int32)
     p0 = int(input_pos.reshape(-1)[0]) if torch.is_tensor(input_pos) else int(input_pos)
+    chunk = max(1, min(int(chunk), _lib.MAX_VERIFY))
+    n = x.numel()
     out = torch.empty(1, dtype=torch.int32, device=model.device)
-    for i in range(x.numel()):
-        model.decode_step(x[i:i + 1], p0 + i, token_out=out)
+    if n == 0:
+        return out
+    cache = getattr(model, "_prefill_masks", None)
+    if cache is None:
+        cache = model._prefill_masks = {}
+    for s in range(0, n, chunk):
+        m = min(chunk, n - s)
+        if m not in cache:
+            cache[m] = (torch.arange(m, dtype=torch.int32, device=model.device),
+                        torch.tril(torch.ones(m, m, dtype=torch.uint8, device=model.device)),
+                        torch.empty(m, model.config.vocab_size, dtype=torch.float32, device=model.device),
+                        torch.empty(m, model.config.dim, dtype=torch.bfloat16, device=model.device),
+                        torch.empty(m, dtype=torch.int32, device=model.device))
+        depth, amask, logits, feat, toks = cache[m]
+        model.verify(x[s:s + m], p0 + s, depth=depth, amask=amask, logits=logits, feat=feat,
+                     tokens_out=toks)
+    out.copy_(toks[m - 1:m])
     return out
 
 
