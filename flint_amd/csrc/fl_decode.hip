@@ -257,11 +257,34 @@ __device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ q,
   }
 }
 
-// rs[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load; x staged in xs.
-template <int MC>
+// The next GEMV phase's weight chunks for rows [r0, r0+rows) of a [N, K] int4 matrix, requested
+// a few at a time while this phase computes (a wave that requests a whole phase's chunks at once
+// stalls on issue until the memory pipeline drains). on = false requests nothing (empty ranges).
+struct NextW {
+  __amdgpu_buffer_rsrc_t wb, sb;
+};
+__device__ __forceinline__ NextW next_w(const uint32_t* q, const uint32_t* sz, int r0, int rows,
+                                        int K, bool on) {
+  NextW n;
+  n.wb = buf_rsrc(q + (size_t)r0 * (K >> 3), on ? (uint32_t)rows * (K >> 1) : 0u);
+  n.sb = buf_rsrc(sz + (size_t)r0 * (K >> 7), on ? (uint32_t)rows * (K >> 5) : 0u);
+  return n;
+}
+template <int MCN>
+__device__ __forceinline__ void next_load(const NextW& n, int j, uint4 (&wn)[MCN],
+                                          uint32_t (&sn)[MCN]) {
+  const uint32_t f = (uint32_t)(tid_here() + j * NT);
+  wn[j] = buf_ld128(n.wb, f * 16u);
+  sn[j] = buf_ld32(n.sb, (f >> 2) * 4u);
+}
+
+// rs[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load; x staged in xs. After each
+// of this phase's chunks, about MCN / MC of the next phase's chunks are requested.
+template <int MC, int MCN>
 __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
                                              int rows, int K, const uint16_t* xs, float* part,
-                                             float* rs) {
+                                             float* rs, const NextW& nx, uint4 (&wn)[MCN],
+                                             uint32_t (&sn)[MCN]) {
   const int tid = tid_here();
   const int cpr = K >> 5;
   const int total = rows * cpr;
@@ -274,7 +297,9 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
       part[f] = chunk_dot(wr[i], sr[i], reinterpret_cast<const uint4*>(xs + c * 32), 0.0f);
     c += step;
     if (c >= cpr) c -= cpr;
-    __builtin_amdgcn_sched_barrier(0);  // keep one chunk's temporaries live at a time
+#pragma unroll
+    for (int j = i * MCN / MC; j < (i + 1) * MCN / MC; ++j) next_load(nx, j, wn, sn);
+    __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time; loads stay spread
   }
   lds_barrier();
   int L = 64;
@@ -591,10 +616,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     const uint32_t rope_cs = buf_ld32(buf_rsrc(p.w.rope + (size_t)pos * 64, 128u),
                                       (uint32_t)(((r0 + 2 * tid) & 63) >> 1) * 4u);
     row_range(D, wg, grid_here(), r0n, rowsn);
-    gemv_load(p.w.wo_q + (size_t)l * D * (D >> 3), p.w.wo_sz + (size_t)l * D * (D >> 7), r0n,
-              rowsn, D, w_o, s_o);
+    const NextW nx_o = next_w(p.w.wo_q + (size_t)l * D * (D >> 3),
+                              p.w.wo_sz + (size_t)l * D * (D >> 7), r0n, rowsn, D, true);
+    gemv_compute(w_qkv, s_qkv, rows, D, xs, ws, rs, nx_o, w_o, s_o);  // (no rows: loads only)
     if (rows > 0) {
-      gemv_compute(w_qkv, s_qkv, rows, D, xs, ws, rs);
       if (tid < (rows >> 1)) {
         const int srow = r0 + 2 * tid;
         const int hh = srow >> 6, j = (srow & 63) >> 1;
@@ -627,10 +652,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     if (rows > 0) stage_tagged(p, p.attn, D, t_attn, xs);
     stamp(p, slot);
     row_range(2 * F, wg, grid_here(), r0n, rowsn);
-    gemv_load(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3), p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7),
-              r0n, rowsn, D, w_gu, s_gu);
+    const NextW nx_gu = next_w(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3),
+                               p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7), r0n, rowsn, D, true);
+    gemv_compute(w_o, s_o, rows, D, xs, ws, rs, nx_gu, w_gu, s_gu);
     if (rows > 0) {
-      gemv_compute(w_o, s_o, rows, D, xs, ws, rs);
       residual_epilogue(p, r0, rows, rs, t_h1, ha, hb);  // engine/model.py:162
     }
     stamp(p, slot);
@@ -640,10 +665,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     if (rows > 0) norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red);
     stamp(p, slot);
     row_range(D, wg, grid_here(), r0n, rowsn);
-    gemv_load(p.w.wd_q + (size_t)l * D * (F >> 3), p.w.wd_sz + (size_t)l * D * (F >> 7), r0n,
-              rowsn, F, w_d, s_d);
+    const NextW nx_d = next_w(p.w.wd_q + (size_t)l * D * (F >> 3),
+                              p.w.wd_sz + (size_t)l * D * (F >> 7), r0n, rowsn, F, true);
+    gemv_compute(w_gu, s_gu, rows, D, xs, ws, rs, nx_d, w_d, s_d);
     if (rows > 0) {
-      gemv_compute(w_gu, s_gu, rows, D, xs, ws, rs);
       if (tid < (rows >> 1)) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
         const float g = rbf(rs[2 * tid]), u = rbf(rs[2 * tid + 1]);
         st_coh_u32(p.act + (r0 >> 1) + tid, f2bf(rbf(silu_f(g)) * u) | (t_act << 16));
@@ -655,13 +680,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     row_range(D, wg, grid_here(), r0, rows);
     if (rows > 0) stage_tagged(p, p.act, F, t_act, xs);
     stamp(p, slot);
-    if (l + 1 < p.NL) {
-      row_range(NQKV, wg, grid_here(), r0n, rowsn);
-      gemv_load(p.w.wqkv_q + (size_t)(l + 1) * NQKV * (D >> 3),
-                p.w.wqkv_sz + (size_t)(l + 1) * NQKV * (D >> 7), r0n, rowsn, D, w_qkv, s_qkv);
-    }
+    row_range(NQKV, wg, grid_here(), r0n, rowsn);
+    const int ln = l + 1 < p.NL ? l + 1 : l;  // the last layer requests nothing
+    const NextW nx_qkv = next_w(p.w.wqkv_q + (size_t)ln * NQKV * (D >> 3),
+                                p.w.wqkv_sz + (size_t)ln * NQKV * (D >> 7), r0n, rowsn, D,
+                                l + 1 < p.NL);
+    gemv_compute(w_d, s_d, rows, F, xs, ws, rs, nx_qkv, w_qkv, s_qkv);
     if (rows > 0) {
-      gemv_compute(w_d, s_d, rows, F, xs, ws, rs);
       residual_epilogue(p, r0, rows, rs, t_h2, ha, hb);  // engine/model.py:163
     }
     stamp(p, slot);
