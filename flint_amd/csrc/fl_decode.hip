@@ -278,9 +278,17 @@ __device__ __forceinline__ void next_load(const NextW& n, int j, uint4 (&wn)[MCN
   sn[j] = buf_ld32(n.sb, (f >> 2) * 4u);
 }
 
+// the next phase's chunks [J0, MCN), requested in one go (at the start of that phase)
+template <int J0, int MCN>
+__device__ __forceinline__ void next_load_from(const NextW& n, uint4 (&wn)[MCN],
+                                               uint32_t (&sn)[MCN]) {
+#pragma unroll
+  for (int j = J0; j < MCN; ++j) next_load(n, j, wn, sn);
+}
+
 // rs[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load; x staged in xs. After each
-// of this phase's chunks, about MCN / MC of the next phase's chunks are requested.
-template <int MC, int MCN>
+// of this phase's chunks, about NPRE / MC of the next phase's first NPRE chunks are requested.
+template <int MC, int MCN, int NPRE = MCN>
 __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
                                              int rows, int K, const uint16_t* xs, float* part,
                                              float* rs, const NextW& nx, uint4 (&wn)[MCN],
@@ -298,7 +306,7 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
     c += step;
     if (c >= cpr) c -= cpr;
 #pragma unroll
-    for (int j = i * MCN / MC; j < (i + 1) * MCN / MC; ++j) next_load(nx, j, wn, sn);
+    for (int j = i * NPRE / MC; j < (i + 1) * NPRE / MC; ++j) next_load(nx, j, wn, sn);
     __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time; loads stay spread
   }
   lds_barrier();
@@ -654,7 +662,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     row_range(2 * F, wg, grid_here(), r0n, rowsn);
     const NextW nx_gu = next_w(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3),
                                p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7), r0n, rowsn, D, true);
-    gemv_compute(w_o, s_o, rows, D, xs, ws, rs, nx_gu, w_gu, s_gu);
+    // half of the gate/up chunks stream in during this short phase, the rest once P4's input
+    // has arrived (their transfer would otherwise delay P4's poll, which returns in order)
+    gemv_compute<MC_O, MC_GU, MC_GU / 2>(w_o, s_o, rows, D, xs, ws, rs, nx_gu, w_gu, s_gu);
     if (rows > 0) {
       residual_epilogue(p, r0, rows, rs, t_h1, ha, hb);  // engine/model.py:162
     }
@@ -663,6 +673,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
     row_range(2 * F, wg, grid_here(), r0, rows);
     if (rows > 0) norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red);
+    next_load_from<MC_GU / 2>(nx_gu, w_gu, s_gu);
     stamp(p, slot);
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_d = next_w(p.w.wd_q + (size_t)l * D * (F >> 3),
