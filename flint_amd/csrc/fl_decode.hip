@@ -662,9 +662,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     row_range(2 * F, wg, grid_here(), r0n, rowsn);
     const NextW nx_gu = next_w(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3),
                                p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7), r0n, rowsn, D, true);
-    // half of the gate/up chunks stream in during this short phase, the rest once P4's input
+    // a third of the gate/up chunks stream in during this short phase, the rest once P4's input
     // has arrived (their transfer would otherwise delay P4's poll, which returns in order)
-    gemv_compute<MC_O, MC_GU, MC_GU / 2>(w_o, s_o, rows, D, xs, ws, rs, nx_gu, w_gu, s_gu);
+    gemv_compute<MC_O, MC_GU, MC_GU / 3>(w_o, s_o, rows, D, xs, ws, rs, nx_gu, w_gu, s_gu);
     if (rows > 0) {
       residual_epilogue(p, r0, rows, rs, t_h1, ha, hb);  // engine/model.py:162
     }
@@ -673,7 +673,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
     row_range(2 * F, wg, grid_here(), r0, rows);
     if (rows > 0) norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red);
-    next_load_from<MC_GU / 2>(nx_gu, w_gu, s_gu);
+    next_load_from<MC_GU / 3>(nx_gu, w_gu, s_gu);
     stamp(p, slot);
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_d = next_w(p.w.wd_q + (size_t)l * D * (F >> 3),
