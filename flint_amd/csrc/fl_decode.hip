@@ -15,16 +15,19 @@
 //    replaces store-completion wait + flag + poll + reload. Every exchange is all-to-all (each
 //    phase needs every producer of the previous one), so no workgroup runs more than one phase
 //    ahead and buffers need no double-buffering;
-//  * the next phase's weight chunks are loaded into registers right after a phase's epilogue,
-//    so the HBM stream overlaps the wait for the next phase's inputs;
+//  * the next phase's weight chunks are requested into registers a few at a time between the
+//    current phase's chunk computations, after the poll for this phase's inputs (vector loads
+//    return in order, so loads issued before a poll would delay it), so the HBM stream overlaps
+//    both the compute and the next hand-off;
 //  * RMSNorm is recomputed by every workgroup from the residual; RoPE + KV append are fused
 //    into the QKV epilogue (NEOX pairs live in adjacent packed rows); SwiGLU into the gate/up
 //    epilogue (gate/up rows interleaved); residual adds into the O / down epilogues; greedy
 //    argmax into the LM head;
-//  * attention: one workgroup per (kv group, key slice); its 8 waves split the slice into
-//    64-key chunks with an online softmax, all query heads of the GQA group sharing each K/V
-//    load; waves merge through LDS; slices (long contexts only) merge through an arrival
-//    counter, the last slice merging.
+//  * attention: one workgroup per (query head, key slice), the heads of a GQA group on one XCD;
+//    its 8 waves take interleaved 8-key steps with an online softmax and merge through LDS;
+//    slices (long contexts only) publish tagged partials that slice 0 merges in order.
+// The speculative-verify kernel (k_verify, below) runs M tokens through the same protocol with
+// the GEMMs on the matrix cores.
 #include "fl_common.h"
 #include <stdlib.h>
 #include <string.h>
