@@ -41,6 +41,10 @@ constexpr int NWAVE = NT / FL_WAVE;  // waves per workgroup
 // max 16-byte weight chunks per thread in each GEMV phase (registers holding one phase's
 // prefetched weights; a small O-phase array keeps attention free of spills)
 constexpr int MC_QKV = 4, MC_O = 4, MC_GU = 12, MC_D = 8;
+// chunks per thread dequantised while the phase's input is exchanged (QKV keeps them in
+// registers, 16 per chunk; O, gate/up and down in LDS: registers are short in those phases)
+constexpr int PD_QKV = 3, PD_O = 2, PD_GU = 3, PD_D = 3;
+constexpr int PD_MAX = 3;            // LDS slots: PD_MAX * 64 B per thread
 constexpr int MAXC = MC_GU;
 constexpr int XS_MAX = 8192;         // max staged activation length (bf16 elements)
 constexpr int ROWS_MAX = 256;        // max rows per workgroup in one GEMV phase
@@ -144,6 +148,13 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The staged activation vector xs keeps one spare 16-byte slot after every four (logical slot
+// s at xslot(s)): a GEMV thread reads the 64 bytes of its chunk's x, and consecutive threads'
+// chunks then start 80 bytes apart instead of 64, which spreads a wave's reads over all LDS
+// banks instead of a quarter of them.
+constexpr int XS_SLOTS = XS_MAX / 8 + XS_MAX / 32;
+__device__ __forceinline__ int xslot(int s) { return s + (s >> 2); }
+
 // Second half of RMSNorm (engine/model.py:237-242): xs holds x (bf16), ss the partial sums of
 // x^2 of this thread; xs <- bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w).
 __device__ void norm_finish(float ss, const uint16_t* __restrict__ nw, int D, float eps,
@@ -157,7 +168,7 @@ __device__ void norm_finish(float ss, const uint16_t* __restrict__ nw, int D, fl
   for (int w = 0; w < NWAVE; ++w) tot += red[w];
   const float r = 1.0f / sqrtf(tot / (float)D + eps);
   for (int i = tid; i < (D >> 3); i += NT) {
-    const uint4 v = reinterpret_cast<const uint4*>(xs)[i];
+    const uint4 v = reinterpret_cast<const uint4*>(xs)[xslot(i)];
     const uint4 g = reinterpret_cast<const uint4*>(nw)[i];
     const uint32_t in[4] = {v.x, v.y, v.z, v.w};
     const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
@@ -167,7 +178,7 @@ __device__ void norm_finish(float ss, const uint16_t* __restrict__ nw, int D, fl
       const float na = rbf(bflo(in[j]) * r), nb = rbf(bfhi(in[j]) * r);
       o[j] = pack_bf16x2(na * bflo(gw[j]), nb * bfhi(gw[j]));
     }
-    reinterpret_cast<uint4*>(xs)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    reinterpret_cast<uint4*>(xs)[xslot(i)] = make_uint4(o[0], o[1], o[2], o[3]);
   }
   lds_barrier();
 }
@@ -188,30 +199,37 @@ __device__ void norm_embed(const uint16_t* __restrict__ erow, float mult,
       ss += b * b;
       o[j] = pack_bf16x2(a, b);
     }
-    reinterpret_cast<uint4*>(xs)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    reinterpret_cast<uint4*>(xs)[xslot(i)] = make_uint4(o[0], o[1], o[2], o[3]);
   }
   norm_finish(ss, nw, D, eps, xs, red);
 }
 
 // Stage the tagged vector src[0..n) (n % 4 == 0, n <= XS_MAX) into xs as bf16 once every word
 // carries `tag`, and return this thread's sum of squares of its values. Each thread requests
-// all of its 16-byte groups at once (coherent range-checked loads) and checks them afterwards,
-// so a vector that is already complete costs one round trip, not one per group.
-constexpr int POLL_MAX = XS_MAX / 4 / NT;
-__device__ __forceinline__ float poll_stage(const DecodeParams& p, const uint32_t* src, int n,
-                                            uint32_t tag, uint16_t* xs) {
+// all of its 16-byte groups at once (coherent range-checked loads, poll_issue) and checks them
+// afterwards (poll_finish), so a vector that is already complete costs one round trip, not one
+// per group. Work that does not depend on the vector runs between the two while the requests
+// are in flight.
+constexpr int POLL_MAX = XS_MAX / 4 / NT;     // 16-byte requests per thread for XS_MAX words
+constexpr int POLL_D = (64 * 8 * LM_MAXC / 4 + NT - 1) / NT;  // ... for a [D] vector (D <= 64*8*LM_MAXC)
+template <int NP>
+__device__ __forceinline__ void poll_issue(const uint32_t* src, int n, uint4 (&v)[NP]) {
   const int tid = tid_here();
   const auto rsrc = buf_rsrc(src, (uint32_t)n * 4u);
   asm volatile("" ::: "memory");  // keep the requests after this workgroup's earlier stores
-  uint4 v[POLL_MAX];
 #pragma unroll
-  for (int i = 0; i < POLL_MAX; ++i) v[i] = buf_ld128_coh(rsrc, (uint32_t)(tid + i * NT) * 16u);
+  for (int i = 0; i < NP; ++i) v[i] = buf_ld128_coh(rsrc, (uint32_t)(tid + i * NT) * 16u);
+}
+template <int NP>
+__device__ __forceinline__ float poll_finish(const DecodeParams& p, const uint32_t* src, int n,
+                                             uint32_t tag, uint16_t* xs, const uint4 (&v)[NP]) {
+  const int tid = tid_here();
   auto ok = [tag](uint4 w) {
     return ((w.x >> 16) == tag) & ((w.y >> 16) == tag) & ((w.z >> 16) == tag) & ((w.w >> 16) == tag);
   };
   float ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < POLL_MAX; ++i) {
+  for (int i = 0; i < NP; ++i) {
     const int g = tid + i * NT;
     if (g < (n >> 2)) {
       uint4 w = v[i];
@@ -224,25 +242,41 @@ __device__ __forceinline__ float poll_stage(const DecodeParams& p, const uint32_
       ss += a1 * a1;
       ss += a2 * a2;
       ss += a3 * a3;
-      reinterpret_cast<uint2*>(xs)[g] =
+      reinterpret_cast<uint2*>(xs)[2 * xslot(g >> 1) + (g & 1)] =
           make_uint2((w.x & 0xFFFFu) | (w.y << 16), (w.z & 0xFFFFu) | (w.w << 16));
     }
   }
   return ss;
 }
 
-// xs = RMSNorm(h) once every word of the tagged residual h carries `tag`
+// xs = RMSNorm(h) once every word of the tagged residual h carries `tag`; work() runs while the
+// first requests for h are in flight
+template <typename Work>
 __device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t tag,
-                            const uint16_t* __restrict__ nw, uint16_t* xs, float* red) {
-  const float ss = poll_stage(p, h, p.D, tag, xs);
+                            const uint16_t* __restrict__ nw, uint16_t* xs, float* red, Work work) {
+  uint4 v[POLL_D];
+  poll_issue(h, p.D, v);
+  work();
+  __builtin_amdgcn_sched_barrier(0);
+  const float ss = poll_finish(p, h, p.D, tag, xs, v);
   lds_barrier();
   norm_finish(ss, nw, p.D, p.eps, xs, red);
 }
+__device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t tag,
+                            const uint16_t* __restrict__ nw, uint16_t* xs, float* red) {
+  norm_tagged(p, h, tag, nw, xs, red, [] {});
+}
 
-// xs = values of the tagged vector src[0..n) once all carry `tag`
+// xs = values of the tagged vector src[0..n) once all carry `tag` (n <= NP * 4 * NT); work() as
+// above
+template <int NP, typename Work>
 __device__ void stage_tagged(const DecodeParams& p, const uint32_t* src, int n, uint32_t tag,
-                             uint16_t* xs) {
-  poll_stage(p, src, n, tag, xs);
+                             uint16_t* xs, Work work) {
+  uint4 v[NP];
+  poll_issue(src, n, v);
+  work();
+  __builtin_amdgcn_sched_barrier(0);
+  poll_finish(p, src, n, tag, xs, v);
   lds_barrier();
 }
 
@@ -291,12 +325,86 @@ __device__ __forceinline__ void next_load_from(const NextW& n, uint4 (&wn)[MCN],
   for (int j = J0; j < MCN; ++j) next_load(n, j, wn, sn);
 }
 
-// rs[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load; x staged in xs. After each
-// of this phase's chunks, about NPRE / MC of the next phase's first NPRE chunks are requested.
-template <int MC, int MCN, int NPRE = MCN>
+// Dequantise this thread's first PD weight chunks ahead of the x-dots: the dequantisation does
+// not depend on the activation vector, so it runs while that vector is still being exchanged
+// (the weights arrived during the previous phase). The bf16 results go to this thread's slots
+// of dql (uint4 plane k of chunk i at dql[(4i + k) * NT + tid]: conflict-free, and each thread
+// reads back only its own slots, so no barrier is needed). Chunks past this workgroup's rows
+// read as zero words and scales and dequantise to zeros.
+template <int MC, int PD>
+__device__ __forceinline__ void gemv_predq(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
+                                           uint4* dql) {
+  static_assert(PD >= 1 && PD <= MC && PD <= PD_MAX, "pre-dequantised chunks");
+  const int tid = tid_here();
+#pragma unroll
+  for (int i = 0; i < PD; ++i) {
+    uint32_t d[4][4];
+    dq32(wr[i], dq_const(sr[i]), d);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dql[(4 * i + k) * NT + tid] = make_uint4(d[k][0], d[k][1], d[k][2], d[k][3]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Register variant for phases with few chunks per thread: d[i] holds chunk i dequantised.
+template <int MC, int PD>
+__device__ __forceinline__ void gemv_predq_reg(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
+                                               uint32_t (&d)[PD][4][4]) {
+  static_assert(PD >= 1 && PD <= MC, "pre-dequantised chunks");
+#pragma unroll
+  for (int i = 0; i < PD; ++i) {
+    dq32(wr[i], dq_const(sr[i]), d[i]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+__device__ __forceinline__ float dq_dot(const uint32_t (&d)[4][4], const uint4* x4) {
+  const uint4 x[4] = {x4[0], x4[1], x4[2], x4[3]};
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc = dot2_bf16(d[0][i], x[i].x, acc);
+    acc = dot2_bf16(d[1][i], x[i].y, acc);
+    acc = dot2_bf16(d[2][i], x[i].z, acc);
+    acc = dot2_bf16(d[3][i], x[i].w, acc);
+  }
+  return acc;
+}
+
+// dot of a dequantised chunk held in dql with 32 bf16 x values (summed in chunk_dot's order)
+__device__ __forceinline__ float dql_dot(const uint4* dql, int i, const uint4* x4) {
+  const int tid = tid_here();
+  const uint4 x[4] = {x4[0], x4[1], x4[2], x4[3]};
+  uint4 d[4];  // plane k: pair k of words 0..3
+#pragma unroll
+  for (int k = 0; k < 4; ++k) d[k] = dql[(4 * i + k) * NT + tid];
+  float acc = 0.0f;
+  acc = dot2_bf16(d[0].x, x[0].x, acc);
+  acc = dot2_bf16(d[1].x, x[0].y, acc);
+  acc = dot2_bf16(d[2].x, x[0].z, acc);
+  acc = dot2_bf16(d[3].x, x[0].w, acc);
+  acc = dot2_bf16(d[0].y, x[1].x, acc);
+  acc = dot2_bf16(d[1].y, x[1].y, acc);
+  acc = dot2_bf16(d[2].y, x[1].z, acc);
+  acc = dot2_bf16(d[3].y, x[1].w, acc);
+  acc = dot2_bf16(d[0].z, x[2].x, acc);
+  acc = dot2_bf16(d[1].z, x[2].y, acc);
+  acc = dot2_bf16(d[2].z, x[2].z, acc);
+  acc = dot2_bf16(d[3].z, x[2].w, acc);
+  acc = dot2_bf16(d[0].w, x[3].x, acc);
+  acc = dot2_bf16(d[1].w, x[3].y, acc);
+  acc = dot2_bf16(d[2].w, x[3].z, acc);
+  acc = dot2_bf16(d[3].w, x[3].w, acc);
+  return acc;
+}
+
+// rs[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load; x staged in xs; chunks
+// i < PD come dequantised ahead: pre_dot(i, x4) is their dot with x. After each of this phase's
+// chunks, about NPRE / MC of the next phase's first NPRE chunks are requested.
+template <int MC, int MCN, int NPRE, int PD, typename PreDot>
 __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
-                                             int rows, int K, const uint16_t* xs, float* part,
-                                             float* rs, const NextW& nx, uint4 (&wn)[MCN],
+                                             PreDot pre_dot, int rows, int K,
+                                             const uint16_t* xs, float* part, float* rs,
+                                             const NextW& nx, uint4 (&wn)[MCN],
                                              uint32_t (&sn)[MCN]) {
   const int tid = tid_here();
   const int cpr = K >> 5;
@@ -306,8 +414,8 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
 #pragma unroll
   for (int i = 0; i < MC; ++i) {
     const int f = tid + i * NT;
-    if (f < total)
-      part[f] = chunk_dot(wr[i], sr[i], reinterpret_cast<const uint4*>(xs + c * 32), 0.0f);
+    const uint4* x4 = reinterpret_cast<const uint4*>(xs) + xslot(4 * c);
+    if (f < total) part[f] = (i < PD) ? pre_dot(i, x4) : chunk_dot(wr[i], sr[i], x4, 0.0f);
     c += step;
     if (c >= cpr) c -= cpr;
 #pragma unroll
@@ -571,8 +679,9 @@ __device__ __forceinline__ void residual_epilogue(const DecodeParams& p, int r0,
 }
 
 __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
-  __shared__ __align__(16) uint16_t xs[XS_MAX];
+  __shared__ __align__(16) uint16_t xs[XS_SLOTS * 8];  // staged activations (slots: xslot)
   __shared__ __align__(16) float ws[WS_FLOATS];
+  __shared__ __align__(16) uint4 dql[PD_MAX * 4 * NT];  // dequantised chunks (gemv_predq)
   __shared__ float rs[ROWS_MAX];
   __shared__ float red[64];
   __shared__ unsigned long long kred[NWAVE];
@@ -618,20 +727,32 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     int r0n, rowsn;
     // ---------------- P1: RMSNorm + QKV + RoPE + KV append ----------------
     row_range(NQKV, wg, grid_here(), r0, rows);
+    // this thread's RoPE (cos, sin) pair, requested right after the residual poll's first
+    // requests (in-order returns: before them it would delay the poll, after the poll's finish
+    // its latency would show in the epilogue)
+    const auto rope_r = buf_rsrc(p.w.rope + (size_t)pos * 64, 128u);
+    const uint32_t rope_off = (uint32_t)(((r0 + 2 * tid) & 63) >> 1) * 4u;
+    uint32_t rope_cs = 0;
+    uint32_t dq_qkv[PD_QKV][4][4];
     if (rows > 0) {
-      if (l == 0)
+      if (l == 0) {
+        rope_cs = buf_ld32(rope_r, rope_off);
         norm_embed(erow, p.emb_mult, p.w.attn_norm, D, p.eps, xs, red);
-      else
-        norm_tagged(p, p.h, t_prev, p.w.attn_norm + (size_t)l * D, xs, red);
+        gemv_predq_reg(w_qkv, s_qkv, dq_qkv);
+      } else {
+        norm_tagged(p, p.h, t_prev, p.w.attn_norm + (size_t)l * D, xs, red, [&] {
+          rope_cs = buf_ld32(rope_r, rope_off);
+          gemv_predq_reg(w_qkv, s_qkv, dq_qkv);
+        });
+      }
     }
     stamp(p, slot);
-    // this thread's RoPE (cos, sin) pair, requested before the O weights (in-order returns)
-    const uint32_t rope_cs = buf_ld32(buf_rsrc(p.w.rope + (size_t)pos * 64, 128u),
-                                      (uint32_t)(((r0 + 2 * tid) & 63) >> 1) * 4u);
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_o = next_w(p.w.wo_q + (size_t)l * D * (D >> 3),
                               p.w.wo_sz + (size_t)l * D * (D >> 7), r0n, rowsn, D, true);
-    gemv_compute(w_qkv, s_qkv, rows, D, xs, ws, rs, nx_o, w_o, s_o);  // (no rows: loads only)
+    gemv_compute<MC_QKV, MC_O, MC_O, PD_QKV>(
+        w_qkv, s_qkv, [&](int i, const uint4* x4) { return dq_dot(dq_qkv[i], x4); }, rows, D, xs, ws, rs, nx_o, w_o,
+                                     s_o);  // (no rows: loads only)
     if (rows > 0) {
       if (tid < (rows >> 1)) {
         const int srow = r0 + 2 * tid;
@@ -662,14 +783,16 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 
     // ---------------- P3: O projection + residual ----------------
     row_range(D, wg, grid_here(), r0, rows);
-    if (rows > 0) stage_tagged(p, p.attn, D, t_attn, xs);
+    if (rows > 0)
+      stage_tagged<POLL_D>(p, p.attn, D, t_attn, xs, [&] { gemv_predq<MC_O, PD_O>(w_o, s_o, dql); });
     stamp(p, slot);
     row_range(2 * F, wg, grid_here(), r0n, rowsn);
     const NextW nx_gu = next_w(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3),
                                p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7), r0n, rowsn, D, true);
     // a third of the gate/up chunks stream in during this short phase, the rest once P4's input
     // has arrived (their transfer would otherwise delay P4's poll, which returns in order)
-    gemv_compute<MC_O, MC_GU, MC_GU / 3>(w_o, s_o, rows, D, xs, ws, rs, nx_gu, w_gu, s_gu);
+    gemv_compute<MC_O, MC_GU, MC_GU / 3, PD_O>(
+        w_o, s_o, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); }, rows, D, xs, ws, rs, nx_gu, w_gu, s_gu);
     if (rows > 0) {
       residual_epilogue(p, r0, rows, rs, t_h1, ha, hb);  // engine/model.py:162
     }
@@ -677,13 +800,16 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 
     // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
     row_range(2 * F, wg, grid_here(), r0, rows);
-    if (rows > 0) norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red);
+    if (rows > 0)
+      norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red,
+                  [&] { gemv_predq<MC_GU, PD_GU>(w_gu, s_gu, dql); });
     next_load_from<MC_GU / 3>(nx_gu, w_gu, s_gu);
     stamp(p, slot);
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_d = next_w(p.w.wd_q + (size_t)l * D * (F >> 3),
                               p.w.wd_sz + (size_t)l * D * (F >> 7), r0n, rowsn, F, true);
-    gemv_compute(w_gu, s_gu, rows, D, xs, ws, rs, nx_d, w_d, s_d);
+    gemv_compute<MC_GU, MC_D, MC_D, PD_GU>(
+        w_gu, s_gu, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); }, rows, D, xs, ws, rs, nx_d, w_d, s_d);
     if (rows > 0) {
       if (tid < (rows >> 1)) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
         const float g = rbf(rs[2 * tid]), u = rbf(rs[2 * tid + 1]);
@@ -694,14 +820,16 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 
     // ---------------- P5: down projection + residual ----------------
     row_range(D, wg, grid_here(), r0, rows);
-    if (rows > 0) stage_tagged(p, p.act, F, t_act, xs);
+    if (rows > 0)
+      stage_tagged<POLL_MAX>(p, p.act, F, t_act, xs, [&] { gemv_predq<MC_D, PD_D>(w_d, s_d, dql); });
     stamp(p, slot);
     row_range(NQKV, wg, grid_here(), r0n, rowsn);
     const int ln = l + 1 < p.NL ? l + 1 : l;  // the last layer requests nothing
     const NextW nx_qkv = next_w(p.w.wqkv_q + (size_t)ln * NQKV * (D >> 3),
                                 p.w.wqkv_sz + (size_t)ln * NQKV * (D >> 7), r0n, rowsn, D,
                                 l + 1 < p.NL);
-    gemv_compute(w_d, s_d, rows, F, xs, ws, rs, nx_qkv, w_qkv, s_qkv);
+    gemv_compute<MC_D, MC_QKV, MC_QKV, PD_D>(
+        w_d, s_d, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); }, rows, F, xs, ws, rs, nx_qkv, w_qkv, s_qkv);
     if (rows > 0) {
       residual_epilogue(p, r0, rows, rs, t_h2, ha, hb);  // engine/model.py:163
     }
@@ -735,7 +863,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
       for (int i = 0; i < LM_MAXC; ++i) {
         const int c = lane + 64 * i;
         if (c < nck) {
-          const uint4 xv = reinterpret_cast<const uint4*>(xs)[c];
+          const uint4 xv = reinterpret_cast<const uint4*>(xs)[xslot(c)];
           acc = dot2_bf16(ev[rr][i].x, xv.x, acc);
           acc = dot2_bf16(ev[rr][i].y, xv.y, acc);
           acc = dot2_bf16(ev[rr][i].z, xv.z, acc);
@@ -757,7 +885,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
   norm_tagged(p, p.h, tag_of(p.epoch + 5u * (uint32_t)p.NL - 1u), p.w.final_norm, xs, red);
   stamp(p, slot);
   if (p.feat && wg == 0)
-    for (int i = tid; i < D; i += NT) p.feat[i] = xs[i];
+    for (int i = tid; i < D; i += NT) p.feat[i] = xs[8 * xslot(i >> 3) + (i & 7)];
   for (int rb = rb0; rb < rows; rb += 2 * STEP) {
     if (rb + STEP < rows) lm_load(eb, rb + STEP);
     lm_compute(ea, rb);
