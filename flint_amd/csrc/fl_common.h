@@ -58,10 +58,11 @@ __device__ __forceinline__ DqConst dq_const(uint32_t szw) {
 // Step j (nibbles j and j+4) of four words w0..w3 of one 128-group: o[i] = packed bf16
 // dequantised pair (element 2j, 2j+1) of word i. One asm block so the instruction order is
 // fixed: the three-address (VOP3P) v_dot2_f32_bf16 needs no copy of its shared accumulator, and
-// every value is consumed at least three instructions after it is written (a VOP3P dot reading
-// a VGPR written just before it must be separated from the write; the compiler does not track
-// that across inline asm). The block ends with two wait states, so the outputs may feed an
-// MFMA or a VOP3P instruction right away (the compiler sees no VALU write inside the asm).
+// the order puts at least three instructions between every write and its first read (a dot
+// reading a VGPR written just before it, and any read of a dot's result right after the dot,
+// need wait states that the compiler does not insert across inline asm), so the block needs no
+// s_nop of its own. It ends with two wait states, so the outputs may feed an MFMA or a VOP3P
+// instruction right away (the compiler sees no VALU write inside the asm).
 template <int J>
 __device__ __forceinline__ void dq_step4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
                                          const DqConst& k, uint32_t magic, uint32_t one_lo,
@@ -75,18 +76,16 @@ __device__ __forceinline__ void dq_step4(uint32_t w0, uint32_t w1, uint32_t w2, 
         "v_lshrrev_b32 %3, %4, %3"
         : "+v"(w0), "+v"(w1), "+v"(w2), "+v"(w3) : "I"(4 * J));
   }
-  asm("s_nop 2\n\t"
-      "v_and_or_b32 %[m0], %[w0], %[mask], %[magic]\n\t"
+  asm("v_and_or_b32 %[m0], %[w0], %[mask], %[magic]\n\t"
       "v_and_or_b32 %[m1], %[w1], %[mask], %[magic]\n\t"
       "v_and_or_b32 %[m2], %[w2], %[mask], %[magic]\n\t"
       "v_and_or_b32 %[m3], %[w3], %[mask], %[magic]\n\t"
-      "s_nop 2\n\t"
       "v_dot2_f32_bf16 %[p00], %[m0], %[slo], %[c]\n\t"
       "v_dot2_f32_bf16 %[p10], %[m1], %[slo], %[c]\n\t"
-      "v_dot2_f32_bf16 %[p20], %[m2], %[slo], %[c]\n\t"
-      "v_dot2_f32_bf16 %[p30], %[m3], %[slo], %[c]\n\t"
       "v_dot2_f32_bf16 %[p01], %[m0], %[shi], %[c]\n\t"
       "v_dot2_f32_bf16 %[p11], %[m1], %[shi], %[c]\n\t"
+      "v_dot2_f32_bf16 %[p20], %[m2], %[slo], %[c]\n\t"
+      "v_dot2_f32_bf16 %[p30], %[m3], %[slo], %[c]\n\t"
       "v_dot2_f32_bf16 %[p21], %[m2], %[shi], %[c]\n\t"
       "v_dot2_f32_bf16 %[p31], %[m3], %[shi], %[c]\n\t"
       "v_cvt_pk_bf16_f32 %[p0], %[p00], %[p01]\n\t"
@@ -95,10 +94,10 @@ __device__ __forceinline__ void dq_step4(uint32_t w0, uint32_t w1, uint32_t w2, 
       "v_cvt_pk_bf16_f32 %[p3], %[p30], %[p31]\n\t"
       "v_dot2_f32_bf16 %[d00], %[p0], %[olo], %[z]\n\t"
       "v_dot2_f32_bf16 %[d10], %[p1], %[olo], %[z]\n\t"
-      "v_dot2_f32_bf16 %[d20], %[p2], %[olo], %[z]\n\t"
-      "v_dot2_f32_bf16 %[d30], %[p3], %[olo], %[z]\n\t"
       "v_dot2_f32_bf16 %[d01], %[p0], %[ohi], %[z]\n\t"
       "v_dot2_f32_bf16 %[d11], %[p1], %[ohi], %[z]\n\t"
+      "v_dot2_f32_bf16 %[d20], %[p2], %[olo], %[z]\n\t"
+      "v_dot2_f32_bf16 %[d30], %[p3], %[olo], %[z]\n\t"
       "v_dot2_f32_bf16 %[d21], %[p2], %[ohi], %[z]\n\t"
       "v_dot2_f32_bf16 %[d31], %[p3], %[ohi], %[z]\n\t"
       "v_cvt_pk_bf16_f32 %[o0], %[d00], %[d01]\n\t"
@@ -132,9 +131,9 @@ __device__ __forceinline__ void dq32(const uint4 w, const DqConst& k, uint32_t (
 // dot of one 16-byte chunk (32 int4 elements of one 128-group) with 32 bf16 x values
 // (16 packed pairs), accumulated into acc.
 __device__ __forceinline__ float chunk_dot(const uint4 w, uint32_t szw, const uint4* x4, float acc) {
+  const uint4 x[4] = {x4[0], x4[1], x4[2], x4[3]};  // requested first: the dequantisation hides them
   uint32_t d[4][4];
   dq32(w, dq_const(szw), d);
-  const uint4 x[4] = {x4[0], x4[1], x4[2], x4[3]};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     acc = dot2_bf16(d[0][i], x[i].x, acc);
