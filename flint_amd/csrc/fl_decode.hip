@@ -423,12 +423,23 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
     __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time; loads stay spread
   }
   lds_barrier();
-  int L = 64;
-  while (L * rows > NT) L >>= 1;
-  const int row = tid / L, li = tid % L;
+  // per row, L = 2^lg lanes (L * rows <= NT) each sum every L-th partial, four requests at a
+  // time (one LDS round trip per four partials), in the same order as a sequential loop
+  int lg = 6;
+  while ((rows << lg) > NT) --lg;
+  const int L = 1 << lg;
+  const int row = tid >> lg, li = tid & (L - 1);
   float acc = 0.0f;
-  if (row < rows)
-    for (int j = li; j < cpr; j += L) acc += part[row * cpr + j];
+  if (row < rows) {
+    const float* pr = part + row * cpr;
+    for (int j0 = li; j0 < cpr; j0 += 4 * L) {
+      float v[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) v[m] = pr[min(j0 + m * L, cpr - 1)];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc += (j0 + m * L < cpr) ? v[m] : 0.0f;
+    }
+  }
   acc = group_sum(acc, L);
   if (row < rows && li == 0) rs[row] = acc;
   lds_barrier();
