@@ -155,10 +155,17 @@ __device__ __forceinline__ void wave_sync() {
 constexpr int XS_SLOTS = XS_MAX / 8 + XS_MAX / 32;
 __device__ __forceinline__ int xslot(int s) { return s + (s >> 2); }
 
+// This thread's 16 bytes of a [D] norm weight vector (D <= 8 * NT: one group per thread),
+// requested ahead of the norm so its latency overlaps the wait for the vector being normed.
+static_assert(64 * LM_MAXC <= NT, "a norm vector has at most one 16-byte group per thread");
+__device__ __forceinline__ uint4 norm_w_load(const uint16_t* __restrict__ nw, int D) {
+  return buf_ld128(buf_rsrc(nw, (uint32_t)D * 2u), (uint32_t)tid_here() * 16u);
+}
+
 // Second half of RMSNorm (engine/model.py:237-242): xs holds x (bf16), ss the partial sums of
-// x^2 of this thread; xs <- bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w).
-__device__ void norm_finish(float ss, const uint16_t* __restrict__ nw, int D, float eps,
-                            uint16_t* xs, float* red) {
+// x^2 of this thread, g this thread's group of the weight (norm_w_load);
+// xs <- bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w).
+__device__ void norm_finish(float ss, uint4 g, int D, float eps, uint16_t* xs, float* red) {
   const int tid = tid_here();
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -167,9 +174,9 @@ __device__ void norm_finish(float ss, const uint16_t* __restrict__ nw, int D, fl
 #pragma unroll
   for (int w = 0; w < NWAVE; ++w) tot += red[w];
   const float r = 1.0f / sqrtf(tot / (float)D + eps);
-  for (int i = tid; i < (D >> 3); i += NT) {
+  const int i = tid;
+  if (i < (D >> 3)) {
     const uint4 v = reinterpret_cast<const uint4*>(xs)[xslot(i)];
-    const uint4 g = reinterpret_cast<const uint4*>(nw)[i];
     const uint32_t in[4] = {v.x, v.y, v.z, v.w};
     const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
     uint32_t o[4];
@@ -187,6 +194,7 @@ __device__ void norm_finish(float ss, const uint16_t* __restrict__ nw, int D, fl
 __device__ void norm_embed(const uint16_t* __restrict__ erow, float mult,
                            const uint16_t* __restrict__ nw, int D, float eps, uint16_t* xs,
                            float* red) {
+  const uint4 g = norm_w_load(nw, D);
   float ss = 0.0f;
   for (int i = tid_here(); i < (D >> 3); i += NT) {
     const uint4 v = reinterpret_cast<const uint4*>(erow)[i];
@@ -201,7 +209,7 @@ __device__ void norm_embed(const uint16_t* __restrict__ erow, float mult,
     }
     reinterpret_cast<uint4*>(xs)[xslot(i)] = make_uint4(o[0], o[1], o[2], o[3]);
   }
-  norm_finish(ss, nw, D, eps, xs, red);
+  norm_finish(ss, g, D, eps, xs, red);
 }
 
 // Stage the tagged vector src[0..n) (n % 4 == 0, n <= XS_MAX) into xs as bf16 once every word
@@ -256,11 +264,12 @@ __device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t t
                             const uint16_t* __restrict__ nw, uint16_t* xs, float* red, Work work) {
   uint4 v[POLL_D];
   poll_issue(h, p.D, v);
+  const uint4 g = norm_w_load(nw, p.D);
   work();
   __builtin_amdgcn_sched_barrier(0);
   const float ss = poll_finish(p, h, p.D, tag, xs, v);
   lds_barrier();
-  norm_finish(ss, nw, p.D, p.eps, xs, red);
+  norm_finish(ss, g, p.D, p.eps, xs, red);
 }
 __device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t tag,
                             const uint16_t* __restrict__ nw, uint16_t* xs, float* red) {
