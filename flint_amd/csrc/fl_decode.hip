@@ -1463,6 +1463,7 @@ struct fl_state {
   unsigned long long* qkv;
   unsigned long long* part;
   int att_spw;
+  int coop;       // launch with hipLaunchCooperativeKernel (else a plain launch, the default)
   int verify_ok;  // k_verify's dynamic LDS fits and a grid of it is co-resident
   unsigned long long* amax;
   uint32_t* done;
@@ -1627,6 +1628,13 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   st->vc = v_cache;
   st->epoch = 1;
   st->att_spw = 12;
+  // Plain launches by default: one workgroup per CU is all that fits (LDS), the grid is one per
+  // CU, and on a device not shared with concurrent work every workgroup is resident at once. A
+  // plain launch starts right after the previous one on the stream; a cooperative launch, which
+  // guarantees residency, starts about 20 us later. Should a workgroup ever not be resident,
+  // the bounded waits end the launch with FL_E_TIMEOUT instead of hanging.
+  st->coop = 0;
+  if (const char* e = getenv("FLINT_AMD_COOPERATIVE")) st->coop = atoi(e) != 0;
   if (const char* e = getenv("FLINT_AMD_ATT_STEPS")) {  // tuning knob: steps per wave per slice
     const int v = atoi(e);
     if (v >= 1 && v <= 64) st->att_spw = v;
@@ -1720,7 +1728,9 @@ int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, i
   p.prof_slots = st->prof_slots;
   void* args[] = {&p};
   const hipError_t e =
-      hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode), dim3(st->grid),
+      st->coop ? hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode),
+                                            dim3(st->grid), dim3(NT), args, 0, as_stream(stream))
+               : hipLaunchKernel(reinterpret_cast<const void*>(k_decode), dim3(st->grid),
                                  dim3(NT), args, 0, as_stream(stream));
   if (e != hipSuccess) return FL_E_LAUNCH;
   st->epoch += 5u * (uint32_t)st->d.n_layer;
@@ -1743,9 +1753,12 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
   p.logits = logits;
   p.feat = feat;
   void* args[] = {&p};
-  const hipError_t e = hipLaunchCooperativeKernel(
-      reinterpret_cast<const void*>(k_verify), dim3(st->vgrid), dim3(NT), args,
-      (unsigned)verify_lds_bytes(m, st->d.dim), as_stream(stream));
+  const unsigned lds = (unsigned)verify_lds_bytes(m, st->d.dim);
+  const hipError_t e =
+      st->coop ? hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_verify),
+                                            dim3(st->vgrid), dim3(NT), args, lds, as_stream(stream))
+               : hipLaunchKernel(reinterpret_cast<const void*>(k_verify), dim3(st->vgrid),
+                                 dim3(NT), args, lds, as_stream(stream));
   if (e != hipSuccess) return FL_E_LAUNCH;
   st->epoch += 5u * (uint32_t)st->d.n_layer;
   return FL_OK;

@@ -30,9 +30,10 @@ enum {
   FL_E_ARG = -1,        /* null pointer / bad size / unsupported shape                         */
   FL_E_POS = -2,        /* pos (+ M) beyond the state's max_seq or the rope table              */
   FL_E_M = -3,          /* verify width M outside 1..FL_MAX_VERIFY                             */
-  FL_E_LAUNCH = -4,     /* HIP launch failed (e.g. cooperative grid cannot be co-resident)     */
+  FL_E_LAUNCH = -4,     /* HIP launch failed (e.g. a cooperative grid cannot be co-resident)   */
   FL_E_HIP = -5,        /* other HIP runtime error (allocation, copy)                          */
-  FL_E_TIMEOUT = -6     /* an inter-workgroup wait hit its 2 s limit in an earlier launch       */
+  FL_E_TIMEOUT = -6     /* an inter-workgroup wait hit its 2 s limit in an earlier launch (e.g.
+                           a workgroup was not resident because other work held its CU)        */
 };
 
 #define FL_MAX_VERIFY 16
