@@ -38,14 +38,23 @@ namespace {
 
 constexpr int NT = 512;              // threads per workgroup
 constexpr int NWAVE = NT / FL_WAVE;  // waves per workgroup
-// max 16-byte weight chunks per thread in each GEMV phase (registers holding one phase's
-// prefetched weights; a small O-phase array keeps attention free of spills)
-constexpr int MC_QKV = 4, MC_O = 4, MC_GU = 12, MC_D = 8;
-// chunks per thread dequantised while the phase's input is exchanged (QKV keeps them in
-// registers, 16 per chunk; O, gate/up and down in LDS: registers are short in those phases)
+// Chunk budget of one decode-kernel instantiation: the max 16-byte weight chunks per thread in
+// each GEMV phase (registers holding one phase's prefetched weights), the gate/up chunks
+// requested during the O phase, and PR_GU / PR_D chunks of gate/up and down dequantised into
+// registers while the phase's input is exchanged, on top of the PD_* chunks below. A model that
+// fits the small budget gets its instantiation: the registers its tighter arrays free hold the
+// extra dequantised chunks.
+struct ChunksLarge {  // dim <= 3072, inter <= 8192 (any shape the state accepts)
+  static constexpr int QKV = 4, O = 4, GU = 12, D = 8, NPRE_GU = 4, PR_GU = 0, PR_D = 0;
+};
+struct ChunksSmall {  // e.g. flint-3b on 256 CUs: 3 / 2 / 10 / 5 chunks per thread
+  static constexpr int QKV = 3, O = 2, GU = 10, D = 5, NPRE_GU = 4, PR_GU = 1, PR_D = 2;
+};
+// chunks per thread dequantised while the phase's input is exchanged: QKV in registers (16 per
+// chunk), O, gate/up and down in LDS
 constexpr int PD_QKV = 3, PD_O = 2, PD_GU = 3, PD_D = 3;
 constexpr int PD_MAX = 3;            // LDS slots: PD_MAX * 64 B per thread
-constexpr int MAXC = MC_GU;
+constexpr int MAXC = ChunksLarge::GU;
 constexpr int XS_MAX = 8192;         // max staged activation length (bf16 elements)
 constexpr int ROWS_MAX = 256;        // max rows per workgroup in one GEMV phase
 constexpr int LM_MAXC = 6;           // max 16-byte chunks per lane of one LM-head row (D <= 3072)
@@ -355,14 +364,14 @@ __device__ __forceinline__ void gemv_predq(const uint4 (&wr)[MC], const uint32_t
   }
 }
 
-// Register variant for phases with few chunks per thread: d[i] holds chunk i dequantised.
-template <int MC, int PD>
+// Register variant for phases with few chunks per thread: d[i] holds chunk OFF + i dequantised.
+template <int MC, int PR, int OFF = 0>
 __device__ __forceinline__ void gemv_predq_reg(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
-                                               uint32_t (&d)[PD][4][4]) {
-  static_assert(PD >= 1 && PD <= MC, "pre-dequantised chunks");
+                                               uint32_t (&d)[PR][4][4]) {
+  static_assert(PR >= 1 && OFF + PR <= MC, "pre-dequantised chunks");
 #pragma unroll
-  for (int i = 0; i < PD; ++i) {
-    dq32(wr[i], dq_const(sr[i]), d[i]);
+  for (int i = 0; i < PR; ++i) {
+    dq32(wr[OFF + i], dq_const(sr[OFF + i]), d[i]);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -485,7 +494,7 @@ __device__ __forceinline__ void attn_slices(int pos, int NH, int G, int spw, int
 // LDS; slices > 0 publish (m, l, o) as tagged 64-bit words and slice 0 merges them in order.
 __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
                                 uint32_t ptag, float* ws, int& slot) {
-  constexpr int RG = 4, NG = 3, RB = RG * NG;  // steps per wave per round, in groups of RG
+  constexpr int RG = 4, NG = 2, RB = RG * NG;  // steps per wave per round, in groups of RG
   const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
   const int kk = lane >> 3, ds = lane & 7;
   const int pos = p.pos;
@@ -698,7 +707,11 @@ __device__ __forceinline__ void residual_epilogue(const DecodeParams& p, int r0,
   }
 }
 
+template <class C>
 __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
+  static_assert(PD_QKV <= C::QKV && PD_O <= C::O && PD_D + C::PR_D <= C::D &&
+                    PD_GU + C::PR_GU <= C::NPRE_GU && C::NPRE_GU <= C::GU,
+                "chunk budget");
   __shared__ __align__(16) uint16_t xs[XS_SLOTS * 8];  // staged activations (slots: xslot)
   __shared__ __align__(16) float ws[WS_FLOATS];
   __shared__ __align__(16) uint4 dql[PD_MAX * 4 * NT];  // dequantised chunks (gemv_predq)
@@ -730,8 +743,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     hb = rbf(bfhi(e2) * p.emb_mult);
   }
 
-  uint4 w_qkv[MC_QKV], w_o[MC_O], w_gu[MC_GU], w_d[MC_D];
-  uint32_t s_qkv[MC_QKV], s_o[MC_O], s_gu[MC_GU], s_d[MC_D];
+  uint4 w_qkv[C::QKV], w_o[C::O], w_gu[C::GU], w_d[C::D];
+  uint32_t s_qkv[C::QKV], s_o[C::O], s_gu[C::GU], s_d[C::D];
   int r0, rows;
   row_range(NQKV, wg, G, r0, rows);
   gemv_load(p.w.wqkv_q, p.w.wqkv_sz, r0, rows, D, w_qkv, s_qkv);
@@ -770,7 +783,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_o = next_w(p.w.wo_q + (size_t)l * D * (D >> 3),
                               p.w.wo_sz + (size_t)l * D * (D >> 7), r0n, rowsn, D, true);
-    gemv_compute<MC_QKV, MC_O, MC_O, PD_QKV>(
+    gemv_compute<C::QKV, C::O, C::O, PD_QKV>(
         w_qkv, s_qkv, [&](int i, const uint4* x4) { return dq_dot(dq_qkv[i], x4); }, rows, D, xs, ws, rs, nx_o, w_o,
                                      s_o);  // (no rows: loads only)
     if (rows > 0) {
@@ -804,14 +817,14 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     // ---------------- P3: O projection + residual ----------------
     row_range(D, wg, grid_here(), r0, rows);
     if (rows > 0)
-      stage_tagged<POLL_D>(p, p.attn, D, t_attn, xs, [&] { gemv_predq<MC_O, PD_O>(w_o, s_o, dql); });
+      stage_tagged<POLL_D>(p, p.attn, D, t_attn, xs, [&] { gemv_predq<C::O, PD_O>(w_o, s_o, dql); });
     stamp(p, slot);
     row_range(2 * F, wg, grid_here(), r0n, rowsn);
     const NextW nx_gu = next_w(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3),
                                p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7), r0n, rowsn, D, true);
-    // a third of the gate/up chunks stream in during this short phase, the rest once P4's input
-    // has arrived (their transfer would otherwise delay P4's poll, which returns in order)
-    gemv_compute<MC_O, MC_GU, MC_GU / 3, PD_O>(
+    // about a third of the gate/up chunks stream in during this short phase, the rest once P4's
+    // input has arrived (their transfer would otherwise delay P4's poll, which returns in order)
+    gemv_compute<C::O, C::GU, C::NPRE_GU, PD_O>(
         w_o, s_o, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); }, rows, D, xs, ws, rs, nx_gu, w_gu, s_gu);
     if (rows > 0) {
       residual_epilogue(p, r0, rows, rs, t_h1, ha, hb);  // engine/model.py:162
@@ -820,16 +833,24 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 
     // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
     row_range(2 * F, wg, grid_here(), r0, rows);
+    constexpr int PR_GU = C::PR_GU > 0 ? C::PR_GU : 1;
+    uint32_t dqr_gu[PR_GU][4][4];
     if (rows > 0)
-      norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red,
-                  [&] { gemv_predq<MC_GU, PD_GU>(w_gu, s_gu, dql); });
-    next_load_from<MC_GU / 3>(nx_gu, w_gu, s_gu);
+      norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red, [&] {
+        gemv_predq<C::GU, PD_GU>(w_gu, s_gu, dql);
+        if constexpr (C::PR_GU > 0) gemv_predq_reg<C::GU, PR_GU, PD_GU>(w_gu, s_gu, dqr_gu);
+      });
+    next_load_from<C::NPRE_GU>(nx_gu, w_gu, s_gu);
     stamp(p, slot);
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_d = next_w(p.w.wd_q + (size_t)l * D * (F >> 3),
                               p.w.wd_sz + (size_t)l * D * (F >> 7), r0n, rowsn, F, true);
-    gemv_compute<MC_GU, MC_D, MC_D, PD_GU>(
-        w_gu, s_gu, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); }, rows, D, xs, ws, rs, nx_d, w_d, s_d);
+    gemv_compute<C::GU, C::D, C::D, PD_GU + C::PR_GU>(
+        w_gu, s_gu,
+        [&](int i, const uint4* x4) {
+          return i < PD_GU ? dql_dot(dql, i, x4) : dq_dot(dqr_gu[i >= PD_GU ? i - PD_GU : 0], x4);
+        },
+        rows, D, xs, ws, rs, nx_d, w_d, s_d);
     if (rows > 0) {
       if (tid < (rows >> 1)) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
         const float g = rbf(rs[2 * tid]), u = rbf(rs[2 * tid + 1]);
@@ -840,16 +861,25 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 
     // ---------------- P5: down projection + residual ----------------
     row_range(D, wg, grid_here(), r0, rows);
+    constexpr int PR_D = C::PR_D > 0 ? C::PR_D : 1;
+    uint32_t dqr_d[PR_D][4][4];
     if (rows > 0)
-      stage_tagged<POLL_MAX>(p, p.act, F, t_act, xs, [&] { gemv_predq<MC_D, PD_D>(w_d, s_d, dql); });
+      stage_tagged<POLL_MAX>(p, p.act, F, t_act, xs, [&] {
+        gemv_predq<C::D, PD_D>(w_d, s_d, dql);
+        if constexpr (C::PR_D > 0) gemv_predq_reg<C::D, PR_D, PD_D>(w_d, s_d, dqr_d);
+      });
     stamp(p, slot);
     row_range(NQKV, wg, grid_here(), r0n, rowsn);
     const int ln = l + 1 < p.NL ? l + 1 : l;  // the last layer requests nothing
     const NextW nx_qkv = next_w(p.w.wqkv_q + (size_t)ln * NQKV * (D >> 3),
                                 p.w.wqkv_sz + (size_t)ln * NQKV * (D >> 7), r0n, rowsn, D,
                                 l + 1 < p.NL);
-    gemv_compute<MC_D, MC_QKV, MC_QKV, PD_D>(
-        w_d, s_d, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); }, rows, F, xs, ws, rs, nx_qkv, w_qkv, s_qkv);
+    gemv_compute<C::D, C::QKV, C::QKV, PD_D + C::PR_D>(
+        w_d, s_d,
+        [&](int i, const uint4* x4) {
+          return i < PD_D ? dql_dot(dql, i, x4) : dq_dot(dqr_d[i >= PD_D ? i - PD_D : 0], x4);
+        },
+        rows, F, xs, ws, rs, nx_qkv, w_qkv, s_qkv);
     if (rows > 0) {
       residual_epilogue(p, r0, rows, rs, t_h2, ha, hb);  // engine/model.py:163
     }
@@ -1464,6 +1494,7 @@ struct fl_state {
   unsigned long long* part;
   int att_spw;
   int coop;       // launch with hipLaunchCooperativeKernel (else a plain launch, the default)
+  const void* kdec;  // the k_decode instantiation whose chunk budget fits the model
   int verify_ok;  // k_verify's dynamic LDS fits and a grid of it is co-resident
   unsigned long long* amax;
   uint32_t* done;
@@ -1587,7 +1618,7 @@ int fl_device_info(int32_t* num_cu, int32_t* decode_grid) {
   if (hipGetDevice(&dev) != hipSuccess) return FL_E_HIP;
   if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return FL_E_HIP;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_decode),
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_decode<ChunksLarge>),
                                                    NT, 0) != hipSuccess)
     return FL_E_HIP;
   if (num_cu) *num_cu = cu;
@@ -1609,25 +1640,33 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   if (hipGetDevice(&dev) != hipSuccess) return FL_E_HIP;
   if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return FL_E_HIP;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &occ, reinterpret_cast<const void*>(k_decode), NT, 0) != hipSuccess)
-    return FL_E_HIP;
-  if (occ < 1 || cu < 1) return FL_E_LAUNCH;
   const int G = cu;
   const int D = d->dim, F = d->inter, NQKV = (d->n_head + 2 * d->n_kv_head) * FL_HEAD_DIM;
-  if (!phase_fits(NQKV, D, G, MC_QKV) || !phase_fits(D, D, G, MC_O) ||
-      !phase_fits(2 * F, D, G, MC_GU) || !phase_fits(D, F, G, MC_D))
-    return FL_E_ARG;
+  auto fits = [&](auto c) {
+    using C = decltype(c);
+    return phase_fits(NQKV, D, G, C::QKV) && phase_fits(D, D, G, C::O) &&
+           phase_fits(2 * F, D, G, C::GU) && phase_fits(D, F, G, C::D);
+  };
+  // FLINT_AMD_DECODE_BUDGET=large selects the large-budget instantiation for any model (tests)
+  const char* budget = getenv("FLINT_AMD_DECODE_BUDGET");
+  const bool small = fits(ChunksSmall{}) && !(budget && strcmp(budget, "large") == 0);
+  if (!small && !fits(ChunksLarge{})) return FL_E_ARG;
+  const void* kdec = small ? reinterpret_cast<const void*>(k_decode<ChunksSmall>)
+                           : reinterpret_cast<const void*>(k_decode<ChunksLarge>);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kdec, NT, 0) != hipSuccess)
+    return FL_E_HIP;
+  if (occ < 1 || cu < 1) return FL_E_LAUNCH;
   fl_state* st = (fl_state*)calloc(1, sizeof(fl_state));
   if (!st) return FL_E_HIP;
   st->d = *d;
   st->max_seq = max_seq;
   st->grid = G;
+  st->kdec = kdec;
   st->vgrid = cu;
   st->kc = k_cache;
   st->vc = v_cache;
   st->epoch = 1;
-  st->att_spw = 12;
+  st->att_spw = 8;
   // Plain launches by default: one workgroup per CU is all that fits (LDS), the grid is one per
   // CU, and on a device not shared with concurrent work every workgroup is resident at once. A
   // plain launch starts right after the previous one on the stream; a cooperative launch, which
@@ -1728,10 +1767,9 @@ int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, i
   p.prof_slots = st->prof_slots;
   void* args[] = {&p};
   const hipError_t e =
-      st->coop ? hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode),
-                                            dim3(st->grid), dim3(NT), args, 0, as_stream(stream))
-               : hipLaunchKernel(reinterpret_cast<const void*>(k_decode), dim3(st->grid),
-                                 dim3(NT), args, 0, as_stream(stream));
+      st->coop ? hipLaunchCooperativeKernel(st->kdec, dim3(st->grid), dim3(NT), args, 0,
+                                            as_stream(stream))
+               : hipLaunchKernel(st->kdec, dim3(st->grid), dim3(NT), args, 0, as_stream(stream));
   if (e != hipSuccess) return FL_E_LAUNCH;
   st->epoch += 5u * (uint32_t)st->d.n_layer;
   return FL_OK;

@@ -60,6 +60,10 @@ CONFIGS = {
                  intermediate_size=1024, vocab_size=1024, rope_base=10000),
     "small": dict(block_size=2048, n_layer=4, n_head=20, n_local_heads=4, dim=1280,
                   intermediate_size=3072, vocab_size=4096, rope_base=10000),
+    # the widest shape the decode kernel accepts (dim 3072, inter 8192): more weight chunks per
+    # thread than the kernel's small chunk budget holds, so it runs the large-budget kernel
+    "wide": dict(block_size=2048, n_layer=2, n_head=48, n_local_heads=8, dim=3072,
+                 intermediate_size=8192, vocab_size=2048, rope_base=10000),
 }
 
 

@@ -133,6 +133,26 @@ def test_decode_multi_slice_attention(dev, monkeypatch, steps_per_wave):
         assert am_e == am_o or near_tie(lo)
 
 
+@pytest.mark.parametrize("name,budget", [("small", "large"), ("wide", None)])
+def test_decode_large_chunk_budget(dev, monkeypatch, name, budget):
+    """The decode kernel is built for two per-thread chunk budgets; models that fit the small one
+    (every other test model) run its instantiation. This covers the large one: forced on the
+    small model, and chosen by itself for the widest accepted shape (dim 3072, inter 8192)."""
+    if budget:
+        monkeypatch.setenv("FLINT_AMD_DECODE_BUDGET", budget)
+    args, sd, eng, orc = make_pair(name, seed=8)
+    eng.setup_caches(1, 512)
+    orc.setup_caches(eng.max_seq_length)
+    for pos in (0, 65, 300):
+        fill_kv_random(eng, orc, pos, seed=pos + 4)
+        tok = (11 * pos + 5) % args.vocab_size
+        am_e, am_o, (ok, d, within, same), lg, lo, fe, fo = _step_compare(eng, orc, tok, pos)
+        log(f"{name} budget={budget}: pos={pos} max|dlogit|={d:.3e} ({within:.1%} within 2e-2) "
+            f"argmax eng={am_e} oracle={am_o}")
+        assert ok
+        assert am_e == am_o or near_tie(lo)
+
+
 @pytest.mark.parametrize("pos", [4095, 8191])
 def test_decode_long_context(dev, pos):
     """BASELINE config 3 shape (one layer of the 3B model, 40 Q / 8 KV heads) at context 4096 and
