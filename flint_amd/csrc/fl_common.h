@@ -347,5 +347,9 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
   return v;
 }
 
-// SiLU as torch computes it for a bf16 tensor: x / (1 + exp(-x)) in fp32.
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+// SiLU of a bf16 tensor's element (torch: x / (1 + exp(-x)) in fp32), as x * sigmoid(x) with the
+// hardware exp2 and reciprocal: within a few fp32 ulp of that (callers round the result to bf16),
+// and the same -0 / x at the extremes
+__device__ __forceinline__ float silu_f(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}

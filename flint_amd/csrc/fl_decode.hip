@@ -298,17 +298,31 @@ __device__ void stage_tagged(const DecodeParams& p, const uint32_t* src, int n, 
   lds_barrier();
 }
 
+// Chunk mapping of a GEMV phase. A workgroup's rows [r0, r0+rows) of a [N, K] int4 matrix are
+// rows * (K / 32) 16-byte chunks in row-major order; thread tid takes chunks f = tid + i * S,
+// i = 0..MC-1, for a chunk stride S <= NT (threads tid >= S take none). S = NT deals the chunks
+// evenly; S = the largest multiple of K / 32 that is <= NT (cs_stride) keeps each thread in
+// one column of chunks, so it reads its 32 activation values once per phase.
+__device__ __forceinline__ int cs_stride(int K) {
+  const int cpr = K >> 5;
+  return (NT / cpr) * cpr;
+}
+// chunk index of thread tid's i-th chunk; past every buffer's end for tid >= S (reads 0)
+__device__ __forceinline__ uint32_t chunk_f(int tid, int i, int S) {
+  return tid < S ? (uint32_t)(tid + i * S) : 0x0FFFFFFFu;
+}
+
 // Issue this workgroup's weight chunks for rows [r0, r0+rows) of a [N, K] int4 matrix.
 template <int MC>
 __device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ q,
                                           const uint32_t* __restrict__ sz, int r0, int rows, int K,
-                                          uint4 (&wr)[MC], uint32_t (&sr)[MC]) {
+                                          int S, uint4 (&wr)[MC], uint32_t (&sr)[MC]) {
   const auto wb = buf_rsrc(q + (size_t)r0 * (K >> 3), (uint32_t)rows * (K >> 1));
   const auto sb = buf_rsrc(sz + (size_t)r0 * (K >> 7), (uint32_t)rows * (K >> 5));
   const int tid = tid_here();
 #pragma unroll
   for (int i = 0; i < MC; ++i) {  // chunks past this workgroup's rows read as 0
-    const uint32_t f = (uint32_t)(tid + i * NT);
+    const uint32_t f = chunk_f(tid, i, S);
     wr[i] = buf_ld128(wb, f * 16u);
     sr[i] = buf_ld32(sb, (f >> 2) * 4u);
   }
@@ -319,18 +333,20 @@ __device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ q,
 // stalls on issue until the memory pipeline drains). on = false requests nothing (empty ranges).
 struct NextW {
   __amdgpu_buffer_rsrc_t wb, sb;
+  int S;  // the next phase's chunk stride
 };
 __device__ __forceinline__ NextW next_w(const uint32_t* q, const uint32_t* sz, int r0, int rows,
-                                        int K, bool on) {
+                                        int K, int S, bool on) {
   NextW n;
   n.wb = buf_rsrc(q + (size_t)r0 * (K >> 3), on ? (uint32_t)rows * (K >> 1) : 0u);
   n.sb = buf_rsrc(sz + (size_t)r0 * (K >> 7), on ? (uint32_t)rows * (K >> 5) : 0u);
+  n.S = S;
   return n;
 }
 template <int MCN>
 __device__ __forceinline__ void next_load(const NextW& n, int j, uint4 (&wn)[MCN],
                                           uint32_t (&sn)[MCN]) {
-  const uint32_t f = (uint32_t)(tid_here() + j * NT);
+  const uint32_t f = chunk_f(tid_here(), j, n.S);
   wn[j] = buf_ld128(n.wb, f * 16u);
   sn[j] = buf_ld32(n.sb, (f >> 2) * 4u);
 }
@@ -415,36 +431,62 @@ __device__ __forceinline__ float dql_dot(const uint4* dql, int i, const uint4* x
   return acc;
 }
 
-// rs[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load; x staged in xs; chunks
-// i < PD come dequantised ahead: pre_dot(i, x4) is their dot with x. After each of this phase's
-// chunks, about NPRE / MC of the next phase's first NPRE chunks are requested.
-template <int MC, int MCN, int NPRE, int PD, typename PreDot>
+// Lanes per row of the GEMV partial-sum reduction: L = 2^lg with L * rows <= NT and L <= 32, so
+// that the groups of rows 2j and 2j+1 share a wave. The lead lane of pair j (the first lane of
+// row 2j's group) is lane (2j) << lg. (rows <= ROWS_MAX = NT / 2, so L >= 2.)
+__device__ __forceinline__ int row_lanes_lg(int rows) {
+  int lg = 5;
+  while ((rows << lg) > NT) --lg;
+  return lg;
+}
+
+// y[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load with chunk stride S; x staged
+// in xs; chunks i < PD come dequantised ahead: pre_dot(i, x4) is their dot with x. XR: S is a
+// multiple of K / 32 (cs_stride), so the thread's 32 x values are read once, into registers.
+// After each of this phase's chunks, about NPRE / MC of the next phase's first NPRE chunks are
+// requested. Ends with epi(j, y[2j], y[2j+1]) on the lead lane of every row pair j.
+template <int MC, int MCN, int NPRE, int PD, bool XR, typename PreDot, typename Epi>
 __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
-                                             PreDot pre_dot, int rows, int K,
-                                             const uint16_t* xs, float* part, float* rs,
+                                             PreDot pre_dot, int rows, int K, int S,
+                                             const uint16_t* xs, float* part,
                                              const NextW& nx, uint4 (&wn)[MCN],
-                                             uint32_t (&sn)[MCN]) {
+                                             uint32_t (&sn)[MCN], Epi epi) {
   const int tid = tid_here();
   const int cpr = K >> 5;
   const int total = rows * cpr;
-  int c = tid % cpr;
-  const int step = NT % cpr;
+  const bool active = tid < S;
+  if constexpr (XR) {
+    const uint4* xp = reinterpret_cast<const uint4*>(xs) + xslot(4 * (tid % cpr));
+    const uint4 xr[4] = {xp[0], xp[1], xp[2], xp[3]};
 #pragma unroll
-  for (int i = 0; i < MC; ++i) {
-    const int f = tid + i * NT;
-    const uint4* x4 = reinterpret_cast<const uint4*>(xs) + xslot(4 * c);
-    if (f < total) part[f] = (i < PD) ? pre_dot(i, x4) : chunk_dot(wr[i], sr[i], x4, 0.0f);
-    c += step;
-    if (c >= cpr) c -= cpr;
+    for (int i = 0; i < MC; ++i) {
+      const int f = tid + i * S;
+      if (active && f < total)
+        part[f] = (i < PD) ? pre_dot(i, xr) : chunk_dot(wr[i], sr[i], xr, 0.0f);
 #pragma unroll
-    for (int j = i * NPRE / MC; j < (i + 1) * NPRE / MC; ++j) next_load(nx, j, wn, sn);
-    __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time; loads stay spread
+      for (int j = i * NPRE / MC; j < (i + 1) * NPRE / MC; ++j) next_load(nx, j, wn, sn);
+      __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time
+    }
+  } else {
+    int c = tid % cpr;
+    const int step = S % cpr;
+#pragma unroll
+    for (int i = 0; i < MC; ++i) {
+      const int f = tid + i * S;
+      const uint4* x4 = reinterpret_cast<const uint4*>(xs) + xslot(4 * c);
+      if (active && f < total)
+        part[f] = (i < PD) ? pre_dot(i, x4) : chunk_dot(wr[i], sr[i], x4, 0.0f);
+      c += step;
+      if (c >= cpr) c -= cpr;
+#pragma unroll
+      for (int j = i * NPRE / MC; j < (i + 1) * NPRE / MC; ++j) next_load(nx, j, wn, sn);
+      __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time; loads spread
+    }
   }
   lds_barrier();
-  // per row, L = 2^lg lanes (L * rows <= NT) each sum every L-th partial, four requests at a
-  // time (one LDS round trip per four partials), in the same order as a sequential loop
-  int lg = 6;
-  while ((rows << lg) > NT) --lg;
+  // per row, L = 2^lg lanes each sum every L-th partial, four requests at a time (one LDS round
+  // trip per four partials), in the same order as a sequential loop
+  const int lg = row_lanes_lg(rows);
   const int L = 1 << lg;
   const int row = tid >> lg, li = tid & (L - 1);
   float acc = 0.0f;
@@ -458,8 +500,12 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
       for (int m = 0; m < 4; ++m) acc += (j0 + m * L < cpr) ? v[m] : 0.0f;
     }
   }
-  acc = group_sum(acc, L);
-  if (row < rows && li == 0) rs[row] = acc;
+  acc = group_sum(acc, L);  // every lane of the row's group holds the row's sum
+  // rows 2j and 2j+1 are neighbouring groups of one wave (L <= 32): the first lane of row 2j
+  // runs the pair's epilogue from registers, before the barrier that frees `part`. (ds_bpermute
+  // measured faster here than the DPP / permlane exchanges of the same lanes.)
+  const float other = __shfl_xor(acc, L);
+  if (row < rows && !(row & 1) && li == 0) epi(row >> 1, acc, other);
   lds_barrier();
 }
 
@@ -689,22 +735,18 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
   stamp(p, slot);
 }
 
-// h[r0 .. r0+rows) = bf16(h + bf16(bf16(acc) * rm)), two rows per thread (r0, rows even). The
+// h[r0+2j], h[r0+2j+1] += bf16(bf16(acc) * rm) (bf16), run by the lead lane of row pair j. The
 // workgroup owns these rows for the whole step (O and down share the row split), so their
-// current values live in registers (ha, hb) and only the tagged result is stored.
-__device__ __forceinline__ void residual_epilogue(const DecodeParams& p, int r0, int rows,
-                                                  const float* rs, uint32_t tag, float& ha,
-                                                  float& hb) {
-  const int t = tid_here();
-  if (2 * t < rows) {
-    const float o0 = rbf(rbf(rs[2 * t]) * p.resid_mult);
-    const float o1 = rbf(rbf(rs[2 * t + 1]) * p.resid_mult);
-    ha = rbf(ha + o0);
-    hb = rbf(hb + o1);
-    const uint32_t n0 = f2bf(ha) | (tag << 16), n1 = f2bf(hb) | (tag << 16);
-    st_coh_u64(reinterpret_cast<unsigned long long*>(p.h + r0) + t,
-               (unsigned long long)n0 | ((unsigned long long)n1 << 32));
-  }
+// current values live in registers (ha, hb) of that lane and only the tagged result is stored.
+__device__ __forceinline__ void residual_pair(const DecodeParams& p, int r0, int j, float y0,
+                                              float y1, uint32_t tag, float& ha, float& hb) {
+  const float o0 = rbf(rbf(y0) * p.resid_mult);
+  const float o1 = rbf(rbf(y1) * p.resid_mult);
+  ha = rbf(ha + o0);
+  hb = rbf(hb + o1);
+  const uint32_t n0 = f2bf(ha) | (tag << 16), n1 = f2bf(hb) | (tag << 16);
+  st_coh_u64(reinterpret_cast<unsigned long long*>(p.h + r0) + j,
+             (unsigned long long)n0 | ((unsigned long long)n1 << 32));
 }
 
 template <class C>
@@ -715,7 +757,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
   __shared__ __align__(16) uint16_t xs[XS_SLOTS * 8];  // staged activations (slots: xslot)
   __shared__ __align__(16) float ws[WS_FLOATS];
   __shared__ __align__(16) uint4 dql[PD_MAX * 4 * NT];  // dequantised chunks (gemv_predq)
-  __shared__ float rs[ROWS_MAX];
   __shared__ float red[64];
   __shared__ unsigned long long kred[NWAVE];
 
@@ -735,19 +776,27 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 
   int r0d, rowsd;  // this workgroup's rows of every [D]-output GEMV (O, down): it owns h there
   row_range(D, wg, G, r0d, rowsd);
-  // h = bf16(embed[token] * emb_mult) on the owned rows (engine/model.py:138), held in registers
+  // h = bf16(embed[token] * emb_mult) on the owned rows (engine/model.py:138), held in the
+  // registers of the lane that leads their row pair in the O and down epilogues
   float ha = 0.0f, hb = 0.0f;
-  if (2 * tid < rowsd) {
-    const uint32_t e2 = reinterpret_cast<const uint32_t*>(erow + r0d)[tid];
-    ha = rbf(bflo(e2) * p.emb_mult);
-    hb = rbf(bfhi(e2) * p.emb_mult);
+  {
+    const int lgd = row_lanes_lg(rowsd);
+    const int jd = tid >> (lgd + 1);
+    if ((tid & ((2 << lgd) - 1)) == 0 && 2 * jd < rowsd) {
+      const uint32_t e2 = reinterpret_cast<const uint32_t*>(erow + r0d)[jd];
+      ha = rbf(bflo(e2) * p.emb_mult);
+      hb = rbf(bfhi(e2) * p.emb_mult);
+    }
   }
 
   uint4 w_qkv[C::QKV], w_o[C::O], w_gu[C::GU], w_d[C::D];
   uint32_t s_qkv[C::QKV], s_o[C::O], s_gu[C::GU], s_d[C::D];
+  // chunk strides: QKV, O (K = D) and down (K = F) keep each thread in one column of chunks;
+  // gate/up deals its chunks evenly over all threads
+  const int sD = cs_stride(D), sF = cs_stride(F);
   int r0, rows;
   row_range(NQKV, wg, G, r0, rows);
-  gemv_load(p.w.wqkv_q, p.w.wqkv_sz, r0, rows, D, w_qkv, s_qkv);
+  gemv_load(p.w.wqkv_q, p.w.wqkv_sz, r0, rows, D, sD, w_qkv, s_qkv);
 
   for (int l = 0; l < p.NL; ++l) {
     const uint32_t e0 = p.epoch + 5u * (uint32_t)l;
@@ -760,11 +809,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     int r0n, rowsn;
     // ---------------- P1: RMSNorm + QKV + RoPE + KV append ----------------
     row_range(NQKV, wg, grid_here(), r0, rows);
-    // this thread's RoPE (cos, sin) pair, requested right after the residual poll's first
-    // requests (in-order returns: before them it would delay the poll, after the poll's finish
-    // its latency would show in the epilogue)
+    // the RoPE (cos, sin) pair of the row pair this lane leads in the epilogue, requested right
+    // after the residual poll's first requests (in-order returns: before them it would delay the
+    // poll, after the poll's finish its latency would show in the epilogue)
     const auto rope_r = buf_rsrc(p.w.rope + (size_t)pos * 64, 128u);
-    const uint32_t rope_off = (uint32_t)(((r0 + 2 * tid) & 63) >> 1) * 4u;
+    const uint32_t rope_off =
+        (uint32_t)(((r0 + 2 * (tid >> (row_lanes_lg(rows) + 1))) & 63) >> 1) * 4u;
     uint32_t rope_cs = 0;
     uint32_t dq_qkv[PD_QKV][4][4];
     if (rows > 0) {
@@ -782,32 +832,31 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     stamp(p, slot);
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_o = next_w(p.w.wo_q + (size_t)l * D * (D >> 3),
-                              p.w.wo_sz + (size_t)l * D * (D >> 7), r0n, rowsn, D, true);
-    gemv_compute<C::QKV, C::O, C::O, PD_QKV>(
-        w_qkv, s_qkv, [&](int i, const uint4* x4) { return dq_dot(dq_qkv[i], x4); }, rows, D, xs, ws, rs, nx_o, w_o,
-                                     s_o);  // (no rows: loads only)
-    if (rows > 0) {
-      if (tid < (rows >> 1)) {
-        const int srow = r0 + 2 * tid;
-        const int hh = srow >> 6, j = (srow & 63) >> 1;
-        const float a = rbf(rs[2 * tid]), b = rbf(rs[2 * tid + 1]);
-        float oa = a, ob = b;
-        if (hh < NH + NKV) {  // RoPE (engine/model.py:257-269 on NEOX pairs j, j+32)
-          const uint32_t cs = rope_cs;
-          const float c = bflo(cs), sn = bfhi(cs);
-          oa = rbf(a * c - b * sn);
-          ob = rbf(b * c + a * sn);
-        }
-        st_coh_u64(p.qkv + hh * 32 + j,
-                   (unsigned long long)pack_bf16x2(oa, ob) | ((unsigned long long)t_qkv << 32));
-        if (hh >= NH) {  // KV append for later launches (engine/model.py:89-98)
-          const int g = (hh < NH + NKV) ? hh - NH : hh - NH - NKV;
-          uint16_t* dst = ((hh < NH + NKV) ? p.kc : p.vc) + ((size_t)(l * NKV + g) * p.S + pos) * 64;
-          dst[j] = (uint16_t)f2bf(oa);
-          dst[j + 32] = (uint16_t)f2bf(ob);
-        }
-      }
-    }
+                              p.w.wo_sz + (size_t)l * D * (D >> 7), r0n, rowsn, D, sD, true);
+    // (a workgroup without rows only requests the O chunks)
+    gemv_compute<C::QKV, C::O, C::O, PD_QKV, true>(
+        w_qkv, s_qkv, [&](int i, const uint4* x4) { return dq_dot(dq_qkv[i], x4); }, rows, D,
+        sD, xs, ws, nx_o, w_o, s_o, [&](int pr, float ya, float yb) {
+          const int srow = r0 + 2 * pr;
+          const int hh = srow >> 6, j = (srow & 63) >> 1;
+          const float a = rbf(ya), b = rbf(yb);
+          float oa = a, ob = b;
+          if (hh < NH + NKV) {  // RoPE (engine/model.py:257-269 on NEOX pairs j, j+32)
+            const uint32_t cs = rope_cs;
+            const float c = bflo(cs), sn = bfhi(cs);
+            oa = rbf(a * c - b * sn);
+            ob = rbf(b * c + a * sn);
+          }
+          st_coh_u64(p.qkv + hh * 32 + j,
+                     (unsigned long long)pack_bf16x2(oa, ob) | ((unsigned long long)t_qkv << 32));
+          if (hh >= NH) {  // KV append for later launches (engine/model.py:89-98)
+            const int g = (hh < NH + NKV) ? hh - NH : hh - NH - NKV;
+            uint16_t* dst =
+                ((hh < NH + NKV) ? p.kc : p.vc) + ((size_t)(l * NKV + g) * p.S + pos) * 64;
+            dst[j] = (uint16_t)f2bf(oa);
+            dst[j + 32] = (uint16_t)f2bf(ob);
+          }
+        });
     stamp(p, slot);
 
     // ---------------- P2: GQA flash-decode attention ----------------
@@ -821,14 +870,14 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     stamp(p, slot);
     row_range(2 * F, wg, grid_here(), r0n, rowsn);
     const NextW nx_gu = next_w(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3),
-                               p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7), r0n, rowsn, D, true);
+                               p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7), r0n, rowsn, D, NT, true);
     // about a third of the gate/up chunks stream in during this short phase, the rest once P4's
     // input has arrived (their transfer would otherwise delay P4's poll, which returns in order)
-    gemv_compute<C::O, C::GU, C::NPRE_GU, PD_O>(
-        w_o, s_o, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); }, rows, D, xs, ws, rs, nx_gu, w_gu, s_gu);
-    if (rows > 0) {
-      residual_epilogue(p, r0, rows, rs, t_h1, ha, hb);  // engine/model.py:162
-    }
+    gemv_compute<C::O, C::GU, C::NPRE_GU, PD_O, true>(
+        w_o, s_o, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); }, rows, D, sD, xs,
+        ws, nx_gu, w_gu, s_gu, [&](int pr, float ya, float yb) {
+          residual_pair(p, r0, pr, ya, yb, t_h1, ha, hb);  // engine/model.py:162
+        });
     stamp(p, slot);
 
     // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
@@ -844,19 +893,17 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     stamp(p, slot);
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_d = next_w(p.w.wd_q + (size_t)l * D * (F >> 3),
-                              p.w.wd_sz + (size_t)l * D * (F >> 7), r0n, rowsn, F, true);
-    gemv_compute<C::GU, C::D, C::D, PD_GU + C::PR_GU>(
+                              p.w.wd_sz + (size_t)l * D * (F >> 7), r0n, rowsn, F, sF, true);
+    gemv_compute<C::GU, C::D, C::D, PD_GU + C::PR_GU, false>(
         w_gu, s_gu,
         [&](int i, const uint4* x4) {
           return i < PD_GU ? dql_dot(dql, i, x4) : dq_dot(dqr_gu[i >= PD_GU ? i - PD_GU : 0], x4);
         },
-        rows, D, xs, ws, rs, nx_d, w_d, s_d);
-    if (rows > 0) {
-      if (tid < (rows >> 1)) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
-        const float g = rbf(rs[2 * tid]), u = rbf(rs[2 * tid + 1]);
-        st_coh_u32(p.act + (r0 >> 1) + tid, f2bf(rbf(silu_f(g)) * u) | (t_act << 16));
-      }
-    }
+        rows, D, NT, xs, ws, nx_d, w_d, s_d, [&](int pr, float yg, float yu) {
+          // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
+          const float g = rbf(yg), u = rbf(yu);
+          st_coh_u32(p.act + (r0 >> 1) + pr, f2bf(rbf(silu_f(g)) * u) | (t_act << 16));
+        });
     stamp(p, slot);
 
     // ---------------- P5: down projection + residual ----------------
@@ -873,16 +920,15 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     const int ln = l + 1 < p.NL ? l + 1 : l;  // the last layer requests nothing
     const NextW nx_qkv = next_w(p.w.wqkv_q + (size_t)ln * NQKV * (D >> 3),
                                 p.w.wqkv_sz + (size_t)ln * NQKV * (D >> 7), r0n, rowsn, D,
-                                l + 1 < p.NL);
-    gemv_compute<C::D, C::QKV, C::QKV, PD_D + C::PR_D>(
+                                sD, l + 1 < p.NL);
+    gemv_compute<C::D, C::QKV, C::QKV, PD_D + C::PR_D, true>(
         w_d, s_d,
         [&](int i, const uint4* x4) {
           return i < PD_D ? dql_dot(dql, i, x4) : dq_dot(dqr_d[i >= PD_D ? i - PD_D : 0], x4);
         },
-        rows, F, xs, ws, rs, nx_qkv, w_qkv, s_qkv);
-    if (rows > 0) {
-      residual_epilogue(p, r0, rows, rs, t_h2, ha, hb);  // engine/model.py:163
-    }
+        rows, F, sF, xs, ws, nx_qkv, w_qkv, s_qkv, [&](int pr, float ya, float yb) {
+          residual_pair(p, r0, pr, ya, yb, t_h2, ha, hb);  // engine/model.py:163
+        });
     stamp(p, slot);
   }
 
@@ -1475,10 +1521,14 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-int phase_fits(int n, int k, int G, int cap) {
+// A GEMV phase's rows per workgroup fit its chunk budget: cap chunks per thread with chunk
+// stride NT (cs = false) or cs_stride(k) (cs = true: NT / (k / 32) rows of chunks per round).
+int phase_fits(int n, int k, int G, int cap, bool cs) {
   int R = (n + G - 1) / G;
   R += (R & 1);
-  return R <= ROWS_MAX && (long)R * (k >> 5) <= (long)cap * NT;
+  const int cpr = k >> 5;
+  if (R > ROWS_MAX || cpr > NT) return 0;
+  return cs ? R <= (NT / cpr) * cap : (long)R * cpr <= (long)cap * NT;
 }
 
 }  // namespace
@@ -1644,8 +1694,8 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   const int D = d->dim, F = d->inter, NQKV = (d->n_head + 2 * d->n_kv_head) * FL_HEAD_DIM;
   auto fits = [&](auto c) {
     using C = decltype(c);
-    return phase_fits(NQKV, D, G, C::QKV) && phase_fits(D, D, G, C::O) &&
-           phase_fits(2 * F, D, G, C::GU) && phase_fits(D, F, G, C::D);
+    return phase_fits(NQKV, D, G, C::QKV, true) && phase_fits(D, D, G, C::O, true) &&
+           phase_fits(2 * F, D, G, C::GU, false) && phase_fits(D, F, G, C::D, true);
   };
   // FLINT_AMD_DECODE_BUDGET=large selects the large-budget instantiation for any model (tests)
   const char* budget = getenv("FLINT_AMD_DECODE_BUDGET");
