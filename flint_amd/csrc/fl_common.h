@@ -216,6 +216,9 @@ __device__ __forceinline__ uint4 buf_ld128(__amdgpu_buffer_rsrc_t r, uint32_t of
 __device__ __forceinline__ uint32_t buf_ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
+__device__ __forceinline__ uint2 buf_ld64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
 // device-coherent variant (sc1: served past the non-coherent per-XCD L2s, like an agent-scope
 // relaxed atomic load); each aligned dword of the result is read atomically
 __device__ __forceinline__ uint4 buf_ld128_coh(__amdgpu_buffer_rsrc_t r, uint32_t off) {

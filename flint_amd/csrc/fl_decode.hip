@@ -237,9 +237,46 @@ __device__ __forceinline__ void poll_issue(const uint32_t* src, int n, uint4 (&v
 #pragma unroll
   for (int i = 0; i < NP; ++i) v[i] = buf_ld128_coh(rsrc, (uint32_t)(tid + i * NT) * 16u);
 }
+// A second look at a tagged vector while the wait's work is still running: groups that are
+// not yet complete in v are requested again into t (a complete group gets an out-of-range
+// request, which touches no memory, so the requests need no branch); poll_merge takes the
+// answers in before the wait. By the end of the work the vector has then usually arrived, and
+// the wait costs no further round trip.
 template <int NP>
-__device__ __forceinline__ float poll_finish(const DecodeParams& p, const uint32_t* src, int n,
-                                             uint32_t tag, uint16_t* xs, const uint4 (&v)[NP]) {
+struct PollRefresh {
+  uint4 t[NP];
+  bool need[NP];
+  bool issued = false;
+};
+template <int NP>
+__device__ __forceinline__ void poll_refresh(const uint32_t* src, int n, uint32_t tag,
+                                             const uint4 (&v)[NP], PollRefresh<NP>& r) {
+  const int tid = tid_here();
+  const auto rsrc = buf_rsrc(src, (uint32_t)n * 4u);
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int g = tid + i * NT;
+    const uint4 w = v[i];
+    const bool ok = ((w.x >> 16) == tag) & ((w.y >> 16) == tag) & ((w.z >> 16) == tag) &
+                    ((w.w >> 16) == tag);
+    r.need[i] = !ok && g < (n >> 2);
+    r.t[i] = buf_ld128_coh(rsrc, r.need[i] ? (uint32_t)g * 16u : 0xFFFFFFF0u);
+  }
+  r.issued = true;
+}
+template <int NP>
+__device__ __forceinline__ void poll_merge(uint4 (&v)[NP], const PollRefresh<NP>& r) {
+  if (!r.issued) return;
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+    if (r.need[i]) v[i] = r.t[i];
+}
+
+// Wait until this thread's groups of the tagged vector src[0..n) all carry `tag` (v: the
+// requests of poll_issue, refreshed in place); returns the sum of squares of their values
+template <int NP>
+__device__ __forceinline__ float poll_wait(const DecodeParams& p, const uint32_t* src, int n,
+                                           uint32_t tag, uint4 (&v)[NP]) {
   const int tid = tid_here();
   auto ok = [tag](uint4 w) {
     return ((w.x >> 16) == tag) & ((w.y >> 16) == tag) & ((w.z >> 16) == tag) & ((w.w >> 16) == tag);
@@ -254,35 +291,86 @@ __device__ __forceinline__ float poll_finish(const DecodeParams& p, const uint32
         const uint32_t* a = src + 4 * g;
         w = spin_until(p, w, ok, [a]() { return ld_coh_u128(a); });
       }
+      v[i] = w;
       const float a0 = bflo(w.x), a1 = bflo(w.y), a2 = bflo(w.z), a3 = bflo(w.w);
       ss += a0 * a0;
       ss += a1 * a1;
       ss += a2 * a2;
       ss += a3 * a3;
-      reinterpret_cast<uint2*>(xs)[2 * xslot(g >> 1) + (g & 1)] =
-          make_uint2((w.x & 0xFFFFu) | (w.y << 16), (w.z & 0xFFFFu) | (w.w << 16));
     }
   }
   return ss;
 }
+// xs slots of group g (4 bf16 values: elements 4g .. 4g+3)
+__device__ __forceinline__ void xs_put4(uint16_t* xs, int g, uint2 val) {
+  reinterpret_cast<uint2*>(xs)[2 * xslot(g >> 1) + (g & 1)] = val;
+}
+template <int NP>
+__device__ __forceinline__ float poll_finish(const DecodeParams& p, const uint32_t* src, int n,
+                                             uint32_t tag, uint16_t* xs, uint4 (&v)[NP]) {
+  const float ss = poll_wait(p, src, n, tag, v);
+  const int tid = tid_here();
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int g = tid + i * NT;
+    const uint4 w = v[i];
+    if (g < (n >> 2))
+      xs_put4(xs, g, make_uint2((w.x & 0xFFFFu) | (w.y << 16), (w.z & 0xFFFFu) | (w.w << 16)));
+  }
+  return ss;
+}
+
+// The norm weights of this thread's poll groups (group g = tid + i * NT: 4 bf16 weights for
+// elements 4g .. 4g+3; groups past D read 0), requested ahead of the norm so their latency
+// overlaps the wait for the vector being normed
+template <int NP>
+__device__ __forceinline__ void norm_w_load4(const uint16_t* __restrict__ nw, int D,
+                                             uint2 (&g)[NP]) {
+  const auto r = buf_rsrc(nw, (uint32_t)D * 2u);
+#pragma unroll
+  for (int i = 0; i < NP; ++i) g[i] = buf_ld64(r, (uint32_t)(tid_here() + i * NT) * 8u);
+}
 
 // xs = RMSNorm(h) once every word of the tagged residual h carries `tag`; work() runs while the
 // first requests for h are in flight
+// (engine/model.py:237-242: xs <- bf16(bf16(h * rsqrt(mean(h^2) + eps)) * w)). Each thread
+// normalises the groups it polled, from registers: one barrier for the sum of squares, one for xs.
 template <typename Work>
 __device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t tag,
                             const uint16_t* __restrict__ nw, uint16_t* xs, float* red, Work work) {
+  const int tid = tid_here();
   uint4 v[POLL_D];
   poll_issue(h, p.D, v);
-  const uint4 g = norm_w_load(nw, p.D);
-  work();
+  uint2 g[POLL_D];
+  norm_w_load4(nw, p.D, g);
+  PollRefresh<POLL_D> rf;
+  work([&] { poll_refresh(h, p.D, tag, v, rf); });
   __builtin_amdgcn_sched_barrier(0);
-  const float ss = poll_finish(p, h, p.D, tag, xs, v);
+  poll_merge(v, rf);
+  float ss = poll_wait(p, h, p.D, tag, v);
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
   lds_barrier();
-  norm_finish(ss, g, p.D, p.eps, xs, red);
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) tot += red[w];
+  const float r = 1.0f / sqrtf(tot / (float)p.D + p.eps);
+#pragma unroll
+  for (int i = 0; i < POLL_D; ++i) {
+    const int gi = tid + i * NT;
+    if (gi < (p.D >> 2)) {
+      const uint4 w = v[i];
+      const float a = rbf(bflo(w.x) * r), b = rbf(bflo(w.y) * r);
+      const float c = rbf(bflo(w.z) * r), d = rbf(bflo(w.w) * r);
+      xs_put4(xs, gi, make_uint2(pack_bf16x2(a * bflo(g[i].x), b * bfhi(g[i].x)),
+                                 pack_bf16x2(c * bflo(g[i].y), d * bfhi(g[i].y))));
+    }
+  }
+  lds_barrier();
 }
 __device__ void norm_tagged(const DecodeParams& p, const uint32_t* h, uint32_t tag,
                             const uint16_t* __restrict__ nw, uint16_t* xs, float* red) {
-  norm_tagged(p, h, tag, nw, xs, red, [] {});
+  norm_tagged(p, h, tag, nw, xs, red, [](auto&&) {});
 }
 
 // xs = values of the tagged vector src[0..n) once all carry `tag` (n <= NP * 4 * NT); work() as
@@ -292,8 +380,10 @@ __device__ void stage_tagged(const DecodeParams& p, const uint32_t* src, int n, 
                              uint16_t* xs, Work work) {
   uint4 v[NP];
   poll_issue(src, n, v);
-  work();
+  PollRefresh<NP> rf;
+  work([&] { poll_refresh(src, n, tag, v, rf); });
   __builtin_amdgcn_sched_barrier(0);
+  poll_merge(v, rf);
   poll_finish(p, src, n, tag, xs, v);
   lds_barrier();
 }
@@ -365,9 +455,9 @@ __device__ __forceinline__ void next_load_from(const NextW& n, uint4 (&wn)[MCN],
 // of dql (uint4 plane k of chunk i at dql[(4i + k) * NT + tid]: conflict-free, and each thread
 // reads back only its own slots, so no barrier is needed). Chunks past this workgroup's rows
 // read as zero words and scales and dequantise to zeros.
-template <int MC, int PD>
+template <int MC, int PD, typename Between>
 __device__ __forceinline__ void gemv_predq(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
-                                           uint4* dql) {
+                                           uint4* dql, Between between) {
   static_assert(PD >= 1 && PD <= MC && PD <= PD_MAX, "pre-dequantised chunks");
   const int tid = tid_here();
 #pragma unroll
@@ -377,18 +467,20 @@ __device__ __forceinline__ void gemv_predq(const uint4 (&wr)[MC], const uint32_t
 #pragma unroll
     for (int k = 0; k < 4; ++k) dql[(4 * i + k) * NT + tid] = make_uint4(d[k][0], d[k][1], d[k][2], d[k][3]);
     __builtin_amdgcn_sched_barrier(0);
+    between(i);
   }
 }
 
 // Register variant for phases with few chunks per thread: d[i] holds chunk OFF + i dequantised.
-template <int MC, int PR, int OFF = 0>
+template <int MC, int PR, int OFF = 0, typename Between>
 __device__ __forceinline__ void gemv_predq_reg(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
-                                               uint32_t (&d)[PR][4][4]) {
+                                               uint32_t (&d)[PR][4][4], Between between) {
   static_assert(PR >= 1 && OFF + PR <= MC, "pre-dequantised chunks");
 #pragma unroll
   for (int i = 0; i < PR; ++i) {
     dq32(wr[OFF + i], dq_const(sr[OFF + i]), d[i]);
     __builtin_amdgcn_sched_barrier(0);
+    between(i);
   }
 }
 __device__ __forceinline__ float dq_dot(const uint32_t (&d)[4][4], const uint4* x4) {
@@ -821,11 +913,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
       if (l == 0) {
         rope_cs = buf_ld32(rope_r, rope_off);
         norm_embed(erow, p.emb_mult, p.w.attn_norm, D, p.eps, xs, red);
-        gemv_predq_reg(w_qkv, s_qkv, dq_qkv);
+        gemv_predq_reg(w_qkv, s_qkv, dq_qkv, [](int) {});
       } else {
-        norm_tagged(p, p.h, t_prev, p.w.attn_norm + (size_t)l * D, xs, red, [&] {
+        norm_tagged(p, p.h, t_prev, p.w.attn_norm + (size_t)l * D, xs, red, [&](auto refresh) {
           rope_cs = buf_ld32(rope_r, rope_off);
-          gemv_predq_reg(w_qkv, s_qkv, dq_qkv);
+          gemv_predq_reg(w_qkv, s_qkv, dq_qkv, [&](int i) {  // a second look before the last
+            if (i == PD_QKV - 2) refresh();
+          });
         });
       }
     }
@@ -866,7 +960,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     // ---------------- P3: O projection + residual ----------------
     row_range(D, wg, grid_here(), r0, rows);
     if (rows > 0)
-      stage_tagged<POLL_D>(p, p.attn, D, t_attn, xs, [&] { gemv_predq<C::O, PD_O>(w_o, s_o, dql); });
+      stage_tagged<POLL_D>(p, p.attn, D, t_attn, xs, [&](auto refresh) {
+        gemv_predq<C::O, PD_O>(w_o, s_o, dql, [&](int i) {
+          if (i == PD_O - 2) refresh();
+        });
+      });
     stamp(p, slot);
     row_range(2 * F, wg, grid_here(), r0n, rowsn);
     const NextW nx_gu = next_w(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3),
@@ -885,9 +983,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     constexpr int PR_GU = C::PR_GU > 0 ? C::PR_GU : 1;
     uint32_t dqr_gu[PR_GU][4][4];
     if (rows > 0)
-      norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red, [&] {
-        gemv_predq<C::GU, PD_GU>(w_gu, s_gu, dql);
-        if constexpr (C::PR_GU > 0) gemv_predq_reg<C::GU, PR_GU, PD_GU>(w_gu, s_gu, dqr_gu);
+      norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red, [&](auto refresh) {
+        static_assert(C::PR_GU <= 1, "the second look sits in the LDS pre-dequantisation");
+        gemv_predq<C::GU, PD_GU>(w_gu, s_gu, dql, [&](int i) {  // a second look before the last
+          if (i == PD_GU + C::PR_GU - 2) refresh();
+        });
+        if constexpr (C::PR_GU > 0)
+          gemv_predq_reg<C::GU, PR_GU, PD_GU>(w_gu, s_gu, dqr_gu, [](int) {});
       });
     next_load_from<C::NPRE_GU>(nx_gu, w_gu, s_gu);
     stamp(p, slot);
@@ -911,9 +1013,15 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     constexpr int PR_D = C::PR_D > 0 ? C::PR_D : 1;
     uint32_t dqr_d[PR_D][4][4];
     if (rows > 0)
-      stage_tagged<POLL_MAX>(p, p.act, F, t_act, xs, [&] {
-        gemv_predq<C::D, PD_D>(w_d, s_d, dql);
-        if constexpr (C::PR_D > 0) gemv_predq_reg<C::D, PR_D, PD_D>(w_d, s_d, dqr_d);
+      stage_tagged<POLL_MAX>(p, p.act, F, t_act, xs, [&](auto refresh) {
+        // a second look at act before the last pre-dequantised chunk
+        gemv_predq<C::D, PD_D>(w_d, s_d, dql, [&](int i) {
+          if (i == PD_D + C::PR_D - 2) refresh();
+        });
+        if constexpr (C::PR_D > 0)
+          gemv_predq_reg<C::D, PR_D, PD_D>(w_d, s_d, dqr_d, [&](int i) {
+            if (i == C::PR_D - 2) refresh();
+          });
       });
     stamp(p, slot);
     row_range(NQKV, wg, grid_here(), r0n, rowsn);
