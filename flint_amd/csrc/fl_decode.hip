@@ -39,16 +39,18 @@ namespace {
 constexpr int NT = 512;              // threads per workgroup
 constexpr int NWAVE = NT / FL_WAVE;  // waves per workgroup
 // Chunk budget of one decode-kernel instantiation: the max 16-byte weight chunks per thread in
-// each GEMV phase (registers holding one phase's prefetched weights), the gate/up chunks
-// requested during the O phase, and PR_GU / PR_D chunks of gate/up and down dequantised into
+// each GEMV phase (registers holding one phase's prefetched weights); G3 gate/up chunks
+// requested at the start of the O phase's wait and dequantised into registers during it (that
+// wait lasts as long as the attention chain); the gate/up chunks requested by then and during
+// the O phase (NPRE_GU in all); and PR_GU / PR_D chunks of gate/up and down dequantised into
 // registers while the phase's input is exchanged, on top of the PD_* chunks below. A model that
 // fits the small budget gets its instantiation: the registers its tighter arrays free hold the
 // extra dequantised chunks.
 struct ChunksLarge {  // dim <= 3072, inter <= 8192 (any shape the state accepts)
-  static constexpr int QKV = 4, O = 4, GU = 12, D = 8, NPRE_GU = 4, PR_GU = 0, PR_D = 0;
+  static constexpr int QKV = 4, O = 4, GU = 12, D = 8, G3 = 0, NPRE_GU = 4, PR_GU = 0, PR_D = 0;
 };
 struct ChunksSmall {  // e.g. flint-3b on 256 CUs: 3 / 2 / 10 / 5 chunks per thread
-  static constexpr int QKV = 3, O = 2, GU = 10, D = 5, NPRE_GU = 4, PR_GU = 1, PR_D = 2;
+  static constexpr int QKV = 3, O = 2, GU = 10, D = 5, G3 = 2, NPRE_GU = 6, PR_GU = 1, PR_D = 2;
 };
 // chunks per thread dequantised while the phase's input is exchanged: QKV in registers (16 per
 // chunk), O, gate/up and down in LDS
@@ -448,6 +450,13 @@ __device__ __forceinline__ void next_load_from(const NextW& n, uint4 (&wn)[MCN],
 #pragma unroll
   for (int j = J0; j < MCN; ++j) next_load(n, j, wn, sn);
 }
+// ... chunks [J0, J1)
+template <int J0, int J1, int MCN>
+__device__ __forceinline__ void next_load_range(const NextW& n, uint4 (&wn)[MCN],
+                                                uint32_t (&sn)[MCN]) {
+#pragma unroll
+  for (int j = J0; j < J1; ++j) next_load(n, j, wn, sn);
+}
 
 // Dequantise this thread's first PD weight chunks ahead of the x-dots: the dequantisation does
 // not depend on the activation vector, so it runs while that vector is still being exchanged
@@ -455,15 +464,15 @@ __device__ __forceinline__ void next_load_from(const NextW& n, uint4 (&wn)[MCN],
 // of dql (uint4 plane k of chunk i at dql[(4i + k) * NT + tid]: conflict-free, and each thread
 // reads back only its own slots, so no barrier is needed). Chunks past this workgroup's rows
 // read as zero words and scales and dequantise to zeros.
-template <int MC, int PD, typename Between>
+template <int MC, int PD, int OFF = 0, typename Between>
 __device__ __forceinline__ void gemv_predq(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
                                            uint4* dql, Between between) {
-  static_assert(PD >= 1 && PD <= MC && PD <= PD_MAX, "pre-dequantised chunks");
+  static_assert(PD >= 1 && OFF + PD <= MC && PD <= PD_MAX, "pre-dequantised chunks");
   const int tid = tid_here();
 #pragma unroll
-  for (int i = 0; i < PD; ++i) {
+  for (int i = 0; i < PD; ++i) {  // chunk OFF + i into slot i
     uint32_t d[4][4];
-    dq32(wr[i], dq_const(sr[i]), d);
+    dq32(wr[OFF + i], dq_const(sr[OFF + i]), d);
 #pragma unroll
     for (int k = 0; k < 4; ++k) dql[(4 * i + k) * NT + tid] = make_uint4(d[k][0], d[k][1], d[k][2], d[k][3]);
     __builtin_amdgcn_sched_barrier(0);
@@ -535,9 +544,9 @@ __device__ __forceinline__ int row_lanes_lg(int rows) {
 // y[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load with chunk stride S; x staged
 // in xs; chunks i < PD come dequantised ahead: pre_dot(i, x4) is their dot with x. XR: S is a
 // multiple of K / 32 (cs_stride), so the thread's 32 x values are read once, into registers.
-// After each of this phase's chunks, about NPRE / MC of the next phase's first NPRE chunks are
+// After each of this phase's chunks, about 1 / MC of the next phase's chunks [J0, NPRE) are
 // requested. Ends with epi(j, y[2j], y[2j+1]) on the lead lane of every row pair j.
-template <int MC, int MCN, int NPRE, int PD, bool XR, typename PreDot, typename Epi>
+template <int MC, int MCN, int NPRE, int PD, bool XR, int J0 = 0, typename PreDot, typename Epi>
 __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
                                              PreDot pre_dot, int rows, int K, int S,
                                              const uint16_t* xs, float* part,
@@ -556,7 +565,8 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
       if (active && f < total)
         part[f] = (i < PD) ? pre_dot(i, xr) : chunk_dot(wr[i], sr[i], xr, 0.0f);
 #pragma unroll
-      for (int j = i * NPRE / MC; j < (i + 1) * NPRE / MC; ++j) next_load(nx, j, wn, sn);
+      for (int j = J0 + i * (NPRE - J0) / MC; j < J0 + (i + 1) * (NPRE - J0) / MC; ++j)
+        next_load(nx, j, wn, sn);
       __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time
     }
   } else {
@@ -571,7 +581,8 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
       c += step;
       if (c >= cpr) c -= cpr;
 #pragma unroll
-      for (int j = i * NPRE / MC; j < (i + 1) * NPRE / MC; ++j) next_load(nx, j, wn, sn);
+      for (int j = J0 + i * (NPRE - J0) / MC; j < J0 + (i + 1) * (NPRE - J0) / MC; ++j)
+        next_load(nx, j, wn, sn);
       __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time; loads spread
     }
   }
@@ -844,7 +855,7 @@ __device__ __forceinline__ void residual_pair(const DecodeParams& p, int r0, int
 template <class C>
 __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
   static_assert(PD_QKV <= C::QKV && PD_O <= C::O && PD_D + C::PR_D <= C::D &&
-                    PD_GU + C::PR_GU <= C::NPRE_GU && C::NPRE_GU <= C::GU,
+                    C::G3 + PD_GU + C::PR_GU <= C::NPRE_GU && C::NPRE_GU <= C::GU,
                 "chunk budget");
   __shared__ __align__(16) uint16_t xs[XS_SLOTS * 8];  // staged activations (slots: xslot)
   __shared__ __align__(16) float ws[WS_FLOATS];
@@ -908,7 +919,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     const uint32_t rope_off =
         (uint32_t)(((r0 + 2 * (tid >> (row_lanes_lg(rows) + 1))) & 63) >> 1) * 4u;
     uint32_t rope_cs = 0;
-    uint32_t dq_qkv[PD_QKV][4][4];
+    uint32_t dq_qkv[PD_QKV][4][4] = {};  // (defined on every path: see dqe below)
     if (rows > 0) {
       if (l == 0) {
         rope_cs = buf_ld32(rope_r, rope_off);
@@ -959,19 +970,36 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 
     // ---------------- P3: O projection + residual ----------------
     row_range(D, wg, grid_here(), r0, rows);
-    if (rows > 0)
-      stage_tagged<POLL_D>(p, p.attn, D, t_attn, xs, [&](auto refresh) {
-        gemv_predq<C::O, PD_O>(w_o, s_o, dql, [&](int i) {
-          if (i == PD_O - 2) refresh();
-        });
-      });
-    stamp(p, slot);
     row_range(2 * F, wg, grid_here(), r0n, rowsn);
     const NextW nx_gu = next_w(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3),
                                p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7), r0n, rowsn, D, NT, true);
-    // about a third of the gate/up chunks stream in during this short phase, the rest once P4's
-    // input has arrived (their transfer would otherwise delay P4's poll, which returns in order)
-    gemv_compute<C::O, C::GU, C::NPRE_GU, PD_O, true>(
+    // The wait for the attention output lasts as long as the attention chain: besides O's chunks,
+    // the first G3 gate/up chunks are requested and dequantised into registers meanwhile. (The
+    // arrays are defined on every path: a conditionally written array keeps its registers live
+    // across the whole layer loop.)
+    constexpr int G3 = C::G3 > 0 ? C::G3 : 1;
+    uint32_t dqe[G3][4][4] = {};
+    auto early_gu = [&] {
+      if constexpr (C::G3 > 0) {
+        next_load_range<0, C::G3>(nx_gu, w_gu, s_gu);
+        gemv_predq_reg<C::GU, C::G3, 0>(w_gu, s_gu, dqe, [](int) {});
+      }
+    };
+    if (rows > 0) {
+      stage_tagged<POLL_D>(p, p.attn, D, t_attn, xs, [&](auto refresh) {
+        if constexpr (C::G3 > 0) next_load_range<0, C::G3>(nx_gu, w_gu, s_gu);
+        gemv_predq<C::O, PD_O>(w_o, s_o, dql, [&](int i) {
+          if (i == PD_O - 1) refresh();
+        });
+        if constexpr (C::G3 > 0) gemv_predq_reg<C::GU, C::G3, 0>(w_gu, s_gu, dqe, [](int) {});
+      });
+    } else {
+      early_gu();
+    }
+    stamp(p, slot);
+    // more gate/up chunks stream in during this short phase, the rest once P4's input has
+    // arrived (their transfer would otherwise delay P4's poll, which returns in order)
+    gemv_compute<C::O, C::GU, C::NPRE_GU, PD_O, true, C::G3>(
         w_o, s_o, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); }, rows, D, sD, xs,
         ws, nx_gu, w_gu, s_gu, [&](int pr, float ya, float yb) {
           residual_pair(p, r0, pr, ya, yb, t_h1, ha, hb);  // engine/model.py:162
@@ -981,25 +1009,27 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
     row_range(2 * F, wg, grid_here(), r0, rows);
     constexpr int PR_GU = C::PR_GU > 0 ? C::PR_GU : 1;
-    uint32_t dqr_gu[PR_GU][4][4];
+    uint32_t dqr_gu[PR_GU][4][4] = {};
     if (rows > 0)
       norm_tagged(p, p.h, t_h1, p.w.ffn_norm + (size_t)l * D, xs, red, [&](auto refresh) {
         static_assert(C::PR_GU <= 1, "the second look sits in the LDS pre-dequantisation");
-        gemv_predq<C::GU, PD_GU>(w_gu, s_gu, dql, [&](int i) {  // a second look before the last
+        gemv_predq<C::GU, PD_GU, C::G3>(w_gu, s_gu, dql, [&](int i) {  // a second look before the last
           if (i == PD_GU + C::PR_GU - 2) refresh();
         });
         if constexpr (C::PR_GU > 0)
-          gemv_predq_reg<C::GU, PR_GU, PD_GU>(w_gu, s_gu, dqr_gu, [](int) {});
+          gemv_predq_reg<C::GU, PR_GU, C::G3 + PD_GU>(w_gu, s_gu, dqr_gu, [](int) {});
       });
     next_load_from<C::NPRE_GU>(nx_gu, w_gu, s_gu);
     stamp(p, slot);
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_d = next_w(p.w.wd_q + (size_t)l * D * (F >> 3),
                               p.w.wd_sz + (size_t)l * D * (F >> 7), r0n, rowsn, F, sF, true);
-    gemv_compute<C::GU, C::D, C::D, PD_GU + C::PR_GU, false>(
+    gemv_compute<C::GU, C::D, C::D, C::G3 + PD_GU + C::PR_GU, false>(
         w_gu, s_gu,
-        [&](int i, const uint4* x4) {
-          return i < PD_GU ? dql_dot(dql, i, x4) : dq_dot(dqr_gu[i >= PD_GU ? i - PD_GU : 0], x4);
+        [&](int i, const uint4* x4) {  // chunks [0, G3) in dqe, then PD_GU in dql, then dqr_gu
+          if (i < C::G3) return dq_dot(dqe[i < C::G3 ? i : 0], x4);
+          const int k = i - C::G3;
+          return k < PD_GU ? dql_dot(dql, k, x4) : dq_dot(dqr_gu[k >= PD_GU ? k - PD_GU : 0], x4);
         },
         rows, D, NT, xs, ws, nx_d, w_d, s_d, [&](int pr, float yg, float yu) {
           // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
@@ -1011,7 +1041,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     // ---------------- P5: down projection + residual ----------------
     row_range(D, wg, grid_here(), r0, rows);
     constexpr int PR_D = C::PR_D > 0 ? C::PR_D : 1;
-    uint32_t dqr_d[PR_D][4][4];
+    uint32_t dqr_d[PR_D][4][4] = {};
     if (rows > 0)
       stage_tagged<POLL_MAX>(p, p.act, F, t_act, xs, [&](auto refresh) {
         // a second look at act before the last pre-dequantised chunk
