@@ -48,9 +48,11 @@ constexpr int NWAVE = NT / FL_WAVE;  // waves per workgroup
 // extra dequantised chunks.
 struct ChunksLarge {  // dim <= 3072, inter <= 8192 (any shape the state accepts)
   static constexpr int QKV = 4, O = 4, GU = 12, D = 8, G3 = 0, NPRE_GU = 4, PR_GU = 0, PR_D = 0;
+  static constexpr bool ROWS = false;
 };
 struct ChunksSmall {  // e.g. flint-3b on 256 CUs: 3 / 2 / 10 / 5 chunks per thread
   static constexpr int QKV = 3, O = 2, GU = 10, D = 5, G3 = 2, NPRE_GU = 6, PR_GU = 1, PR_D = 2;
+  static constexpr bool ROWS = true;  // QKV and gate/up by rows
 };
 // chunks per thread dequantised while the phase's input is exchanged: QKV in registers (16 per
 // chunk), O, gate/up and down in LDS
@@ -226,7 +228,7 @@ __device__ void norm_embed(const uint16_t* __restrict__ erow, float mult,
 // Stage the tagged vector src[0..n) (n % 4 == 0, n <= XS_MAX) into xs as bf16 once every word
 // carries `tag`, and return this thread's sum of squares of its values. Each thread requests
 // all of its 16-byte groups at once (coherent range-checked loads, poll_issue) and checks them
-// afterwards (poll_finish), so a vector that is already complete costs one round trip, not one
+// afterwards (poll_wait), so a vector that is already complete costs one round trip, not one
 // per group. Work that does not depend on the vector runs between the two while the requests
 // are in flight.
 constexpr int POLL_MAX = XS_MAX / 4 / NT;     // 16-byte requests per thread for XS_MAX words
@@ -307,10 +309,9 @@ __device__ __forceinline__ float poll_wait(const DecodeParams& p, const uint32_t
 __device__ __forceinline__ void xs_put4(uint16_t* xs, int g, uint2 val) {
   reinterpret_cast<uint2*>(xs)[2 * xslot(g >> 1) + (g & 1)] = val;
 }
+// the values of this thread's groups (v, as poll_wait left them) into xs
 template <int NP>
-__device__ __forceinline__ float poll_finish(const DecodeParams& p, const uint32_t* src, int n,
-                                             uint32_t tag, uint16_t* xs, uint4 (&v)[NP]) {
-  const float ss = poll_wait(p, src, n, tag, v);
+__device__ __forceinline__ void poll_put(int n, uint16_t* xs, const uint4 (&v)[NP]) {
   const int tid = tid_here();
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
@@ -319,7 +320,6 @@ __device__ __forceinline__ float poll_finish(const DecodeParams& p, const uint32
     if (g < (n >> 2))
       xs_put4(xs, g, make_uint2((w.x & 0xFFFFu) | (w.y << 16), (w.z & 0xFFFFu) | (w.w << 16)));
   }
-  return ss;
 }
 
 // The norm weights of this thread's poll groups (group g = tid + i * NT: 4 bf16 weights for
@@ -386,35 +386,64 @@ __device__ void stage_tagged(const DecodeParams& p, const uint32_t* src, int n, 
   work([&] { poll_refresh(src, n, tag, v, rf); });
   __builtin_amdgcn_sched_barrier(0);
   poll_merge(v, rf);
-  poll_finish(p, src, n, tag, xs, v);
+  poll_wait(p, src, n, tag, v);
+  lds_barrier();  // every wave is done reading the previous phase's xs
+  poll_put(n, xs, v);
   lds_barrier();
 }
 
 // Chunk mapping of a GEMV phase. A workgroup's rows [r0, r0+rows) of a [N, K] int4 matrix are
-// rows * (K / 32) 16-byte chunks in row-major order; thread tid takes chunks f = tid + i * S,
-// i = 0..MC-1, for a chunk stride S <= NT (threads tid >= S take none). S = NT deals the chunks
-// evenly; S = the largest multiple of K / 32 that is <= NT (cs_stride) keeps each thread in
-// one column of chunks, so it reads its 32 activation values once per phase.
+// rows * (K / 32) 16-byte chunks in row-major order (cpr = K / 32 per row), dealt to threads in
+// one of two ways:
+//  - by stride: thread tid takes chunks f = tid + i * S, i = 0..MC-1, for a stride S <= NT
+//    (threads tid >= S take none). S = NT deals them evenly; S = the largest multiple of cpr
+//    that is <= NT (cs_stride) keeps each thread in one column of chunks, so it reads its 32
+//    activation values once per phase. Partial sums meet in LDS.
+//  - by rows: 2^lg lanes per row (rs_lg), lane j of row r takes chunks j + i * 2^lg of row r,
+//    so a thread's partial sums add up in a register and a row's sum is a DPP reduction.
+struct ChunkMap {
+  bool by_rows;
+  int S;    // by stride
+  int lg;   // by rows
+  int cpr, rows;
+};
 __device__ __forceinline__ int cs_stride(int K) {
   const int cpr = K >> 5;
   return (NT / cpr) * cpr;
 }
-// chunk index of thread tid's i-th chunk; past every buffer's end for tid >= S (reads 0)
-__device__ __forceinline__ uint32_t chunk_f(int tid, int i, int S) {
-  return tid < S ? (uint32_t)(tid + i * S) : 0x0FFFFFFFu;
+// lanes per row of the by-rows mapping: a power of two <= 32 (the groups of rows 2j and 2j+1
+// share a wave), rows * lanes <= NT, and no more lanes than chunks in a row
+__device__ __forceinline__ int rs_lg(int rows, int cpr) {
+  int lg = 5;
+  while (lg > 0 && ((rows << lg) > NT || (1 << (lg - 1)) >= cpr)) --lg;
+  return lg;
+}
+__device__ __forceinline__ ChunkMap map_stride(int K, int rows, int S) {
+  return ChunkMap{false, S, 0, K >> 5, rows};
+}
+__device__ __forceinline__ ChunkMap map_rows(int K, int rows) {
+  return ChunkMap{true, NT, rs_lg(rows, K >> 5), K >> 5, rows};
+}
+// chunk index of thread tid's i-th chunk; past every buffer's end where it has none (reads 0)
+__device__ __forceinline__ uint32_t chunk_f(const ChunkMap& m, int tid, int i) {
+  if (m.by_rows) {
+    const int row = tid >> m.lg, c = (tid & ((1 << m.lg) - 1)) + (i << m.lg);
+    return (row < m.rows && c < m.cpr) ? (uint32_t)(row * m.cpr + c) : 0x0FFFFFFFu;
+  }
+  return tid < m.S ? (uint32_t)(tid + i * m.S) : 0x0FFFFFFFu;
 }
 
 // Issue this workgroup's weight chunks for rows [r0, r0+rows) of a [N, K] int4 matrix.
 template <int MC>
 __device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ q,
                                           const uint32_t* __restrict__ sz, int r0, int rows, int K,
-                                          int S, uint4 (&wr)[MC], uint32_t (&sr)[MC]) {
+                                          const ChunkMap& m, uint4 (&wr)[MC], uint32_t (&sr)[MC]) {
   const auto wb = buf_rsrc(q + (size_t)r0 * (K >> 3), (uint32_t)rows * (K >> 1));
   const auto sb = buf_rsrc(sz + (size_t)r0 * (K >> 7), (uint32_t)rows * (K >> 5));
   const int tid = tid_here();
 #pragma unroll
   for (int i = 0; i < MC; ++i) {  // chunks past this workgroup's rows read as 0
-    const uint32_t f = chunk_f(tid, i, S);
+    const uint32_t f = chunk_f(m, tid, i);
     wr[i] = buf_ld128(wb, f * 16u);
     sr[i] = buf_ld32(sb, (f >> 2) * 4u);
   }
@@ -425,20 +454,20 @@ __device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ q,
 // stalls on issue until the memory pipeline drains). on = false requests nothing (empty ranges).
 struct NextW {
   __amdgpu_buffer_rsrc_t wb, sb;
-  int S;  // the next phase's chunk stride
+  ChunkMap m;  // the next phase's chunk mapping
 };
 __device__ __forceinline__ NextW next_w(const uint32_t* q, const uint32_t* sz, int r0, int rows,
-                                        int K, int S, bool on) {
+                                        int K, const ChunkMap& m, bool on) {
   NextW n;
   n.wb = buf_rsrc(q + (size_t)r0 * (K >> 3), on ? (uint32_t)rows * (K >> 1) : 0u);
   n.sb = buf_rsrc(sz + (size_t)r0 * (K >> 7), on ? (uint32_t)rows * (K >> 5) : 0u);
-  n.S = S;
+  n.m = m;
   return n;
 }
 template <int MCN>
 __device__ __forceinline__ void next_load(const NextW& n, int j, uint4 (&wn)[MCN],
                                           uint32_t (&sn)[MCN]) {
-  const uint32_t f = chunk_f(tid_here(), j, n.S);
+  const uint32_t f = chunk_f(n.m, tid_here(), j);
   wn[j] = buf_ld128(n.wb, f * 16u);
   sn[j] = buf_ld32(n.sb, (f >> 2) * 4u);
 }
@@ -541,22 +570,58 @@ __device__ __forceinline__ int row_lanes_lg(int rows) {
   return lg;
 }
 
-// y[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load with chunk stride S; x staged
-// in xs; chunks i < PD come dequantised ahead: pre_dot(i, x4) is their dot with x. XR: S is a
-// multiple of K / 32 (cs_stride), so the thread's 32 x values are read once, into registers.
+// GEMV modes: chunks by stride with partial sums in LDS (GM_STRIDE), the same with each thread
+// in one column of chunks (GM_COLUMN: its 32 x values read once, into registers), or by rows
+// (GM_ROWS: partial sums in registers, rows summed by DPP; no LDS partials, no barrier).
+enum { GM_STRIDE = 0, GM_COLUMN = 1, GM_ROWS = 2 };
+
+// y[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load with mapping m (mode MODE);
+// x staged in xs; chunks i < PD come dequantised ahead: pre_dot(i, x4) is their dot with x.
 // After each of this phase's chunks, about 1 / MC of the next phase's chunks [J0, NPRE) are
-// requested. Ends with epi(j, y[2j], y[2j+1]) on the lead lane of every row pair j.
-template <int MC, int MCN, int NPRE, int PD, bool XR, int J0 = 0, typename PreDot, typename Epi>
+// requested. Ends with epi(j, y[2j], y[2j+1]) on the lead lane of every row pair j. The stride
+// modes end with a barrier (part is free again); GM_ROWS writes no LDS, and the next writer of
+// xs waits at a barrier of its own.
+template <int MC, int MCN, int NPRE, int PD, int MODE, int J0 = 0, typename PreDot, typename Epi>
 __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
-                                             PreDot pre_dot, int rows, int K, int S,
+                                             PreDot pre_dot, const ChunkMap& m,
                                              const uint16_t* xs, float* part,
                                              const NextW& nx, uint4 (&wn)[MCN],
                                              uint32_t (&sn)[MCN], Epi epi) {
   const int tid = tid_here();
-  const int cpr = K >> 5;
+  const int cpr = m.cpr, rows = m.rows;
+  auto next = [&](int i) {
+#pragma unroll
+    for (int j = J0 + i * (NPRE - J0) / MC; j < J0 + (i + 1) * (NPRE - J0) / MC; ++j)
+      next_load(nx, j, wn, sn);
+  };
+  if constexpr (MODE == GM_ROWS) {
+    const int lg = m.lg, L = 1 << lg;
+    const int row = tid >> lg, lj = tid & (L - 1);
+    const bool on = row < rows;
+    // Waves still in this phase issue first: a wave that has finished its rows goes on to the
+    // next phase's dequantisation, which would otherwise take the shared SIMD from the waves
+    // whose rows everyone waits for (s_setprio: the wave's own issue priority).
+    __builtin_amdgcn_s_setprio(1);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MC; ++i) {
+      const int c = lj + (i << lg);
+      const uint4* x4 = reinterpret_cast<const uint4*>(xs) + xslot(4 * min(c, cpr - 1));
+      const float y = (i < PD) ? pre_dot(i, x4) : chunk_dot(wr[i], sr[i], x4, 0.0f);
+      acc += (on && c < cpr) ? y : 0.0f;
+      next(i);
+      __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time; loads spread
+    }
+    acc = group_sum(acc, L);  // every lane of the row's group holds the row's sum
+    const float other = __shfl_xor(acc, L);
+    if (on && !(row & 1) && lj == 0) epi(row >> 1, acc, other);
+    __builtin_amdgcn_s_setprio(0);
+    return;
+  }
+  const int S = m.S;
   const int total = rows * cpr;
   const bool active = tid < S;
-  if constexpr (XR) {
+  if constexpr (MODE == GM_COLUMN) {
     const uint4* xp = reinterpret_cast<const uint4*>(xs) + xslot(4 * (tid % cpr));
     const uint4 xr[4] = {xp[0], xp[1], xp[2], xp[3]};
 #pragma unroll
@@ -564,9 +629,7 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
       const int f = tid + i * S;
       if (active && f < total)
         part[f] = (i < PD) ? pre_dot(i, xr) : chunk_dot(wr[i], sr[i], xr, 0.0f);
-#pragma unroll
-      for (int j = J0 + i * (NPRE - J0) / MC; j < J0 + (i + 1) * (NPRE - J0) / MC; ++j)
-        next_load(nx, j, wn, sn);
+      next(i);
       __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time
     }
   } else {
@@ -580,9 +643,7 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
         part[f] = (i < PD) ? pre_dot(i, x4) : chunk_dot(wr[i], sr[i], x4, 0.0f);
       c += step;
       if (c >= cpr) c -= cpr;
-#pragma unroll
-      for (int j = J0 + i * (NPRE - J0) / MC; j < J0 + (i + 1) * (NPRE - J0) / MC; ++j)
-        next_load(nx, j, wn, sn);
+      next(i);
       __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time; loads spread
     }
   }
@@ -598,9 +659,9 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
     for (int j0 = li; j0 < cpr; j0 += 4 * L) {
       float v[4];
 #pragma unroll
-      for (int m = 0; m < 4; ++m) v[m] = pr[min(j0 + m * L, cpr - 1)];
+      for (int m4 = 0; m4 < 4; ++m4) v[m4] = pr[min(j0 + m4 * L, cpr - 1)];
 #pragma unroll
-      for (int m = 0; m < 4; ++m) acc += (j0 + m * L < cpr) ? v[m] : 0.0f;
+      for (int m4 = 0; m4 < 4; ++m4) acc += (j0 + m4 * L < cpr) ? v[m4] : 0.0f;
     }
   }
   acc = group_sum(acc, L);  // every lane of the row's group holds the row's sum
@@ -894,12 +955,15 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 
   uint4 w_qkv[C::QKV], w_o[C::O], w_gu[C::GU], w_d[C::D];
   uint32_t s_qkv[C::QKV], s_o[C::O], s_gu[C::GU], s_d[C::D];
-  // chunk strides: QKV, O (K = D) and down (K = F) keep each thread in one column of chunks;
-  // gate/up deals its chunks evenly over all threads
+  // chunk mappings: O and down keep each thread in one column of chunks; QKV and gate/up go by
+  // rows in the instantiations that have them (C::ROWS), else by column / by stride
   const int sD = cs_stride(D), sF = cs_stride(F);
+  constexpr int M_QKV = C::ROWS ? GM_ROWS : GM_COLUMN, M_GU = C::ROWS ? GM_ROWS : GM_STRIDE;
+  auto map_qkv = [&](int n) { return C::ROWS ? map_rows(D, n) : map_stride(D, n, sD); };
+  auto map_gu = [&](int n) { return C::ROWS ? map_rows(D, n) : map_stride(D, n, NT); };
   int r0, rows;
   row_range(NQKV, wg, G, r0, rows);
-  gemv_load(p.w.wqkv_q, p.w.wqkv_sz, r0, rows, D, sD, w_qkv, s_qkv);
+  gemv_load(p.w.wqkv_q, p.w.wqkv_sz, r0, rows, D, map_qkv(rows), w_qkv, s_qkv);
 
   for (int l = 0; l < p.NL; ++l) {
     const uint32_t e0 = p.epoch + 5u * (uint32_t)l;
@@ -917,7 +981,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     // poll, after the poll's finish its latency would show in the epilogue)
     const auto rope_r = buf_rsrc(p.w.rope + (size_t)pos * 64, 128u);
     const uint32_t rope_off =
-        (uint32_t)(((r0 + 2 * (tid >> (row_lanes_lg(rows) + 1))) & 63) >> 1) * 4u;
+        (uint32_t)(((r0 + 2 * (tid >> ((C::ROWS ? rs_lg(rows, D >> 5) : row_lanes_lg(rows)) + 1))) &
+                    63) >> 1) * 4u;
     uint32_t rope_cs = 0;
     uint32_t dq_qkv[PD_QKV][4][4] = {};  // (defined on every path: see dqe below)
     if (rows > 0) {
@@ -937,11 +1002,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     stamp(p, slot);
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_o = next_w(p.w.wo_q + (size_t)l * D * (D >> 3),
-                              p.w.wo_sz + (size_t)l * D * (D >> 7), r0n, rowsn, D, sD, true);
+                              p.w.wo_sz + (size_t)l * D * (D >> 7), r0n, rowsn, D,
+                              map_stride(D, rowsn, sD), true);
     // (a workgroup without rows only requests the O chunks)
-    gemv_compute<C::QKV, C::O, C::O, PD_QKV, true>(
-        w_qkv, s_qkv, [&](int i, const uint4* x4) { return dq_dot(dq_qkv[i], x4); }, rows, D,
-        sD, xs, ws, nx_o, w_o, s_o, [&](int pr, float ya, float yb) {
+    gemv_compute<C::QKV, C::O, C::O, PD_QKV, M_QKV>(
+        w_qkv, s_qkv, [&](int i, const uint4* x4) { return dq_dot(dq_qkv[i], x4); },
+        map_qkv(rows), xs, ws, nx_o, w_o, s_o, [&](int pr, float ya, float yb) {
           const int srow = r0 + 2 * pr;
           const int hh = srow >> 6, j = (srow & 63) >> 1;
           const float a = rbf(ya), b = rbf(yb);
@@ -972,7 +1038,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     row_range(D, wg, grid_here(), r0, rows);
     row_range(2 * F, wg, grid_here(), r0n, rowsn);
     const NextW nx_gu = next_w(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3),
-                               p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7), r0n, rowsn, D, NT, true);
+                               p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7), r0n, rowsn, D,
+                               map_gu(rowsn), true);
     // The wait for the attention output lasts as long as the attention chain: besides O's chunks,
     // the first G3 gate/up chunks are requested and dequantised into registers meanwhile. (The
     // arrays are defined on every path: a conditionally written array keeps its registers live
@@ -999,8 +1066,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     stamp(p, slot);
     // more gate/up chunks stream in during this short phase, the rest once P4's input has
     // arrived (their transfer would otherwise delay P4's poll, which returns in order)
-    gemv_compute<C::O, C::GU, C::NPRE_GU, PD_O, true, C::G3>(
-        w_o, s_o, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); }, rows, D, sD, xs,
+    gemv_compute<C::O, C::GU, C::NPRE_GU, PD_O, GM_COLUMN, C::G3>(
+        w_o, s_o, [&](int i, const uint4* x4) { return dql_dot(dql, i, x4); },
+        map_stride(D, rows, sD), xs,
         ws, nx_gu, w_gu, s_gu, [&](int pr, float ya, float yb) {
           residual_pair(p, r0, pr, ya, yb, t_h1, ha, hb);  // engine/model.py:162
         });
@@ -1023,15 +1091,16 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     stamp(p, slot);
     row_range(D, wg, grid_here(), r0n, rowsn);
     const NextW nx_d = next_w(p.w.wd_q + (size_t)l * D * (F >> 3),
-                              p.w.wd_sz + (size_t)l * D * (F >> 7), r0n, rowsn, F, sF, true);
-    gemv_compute<C::GU, C::D, C::D, C::G3 + PD_GU + C::PR_GU, false>(
+                              p.w.wd_sz + (size_t)l * D * (F >> 7), r0n, rowsn, F,
+                              map_stride(F, rowsn, sF), true);
+    gemv_compute<C::GU, C::D, C::D, C::G3 + PD_GU + C::PR_GU, M_GU>(
         w_gu, s_gu,
         [&](int i, const uint4* x4) {  // chunks [0, G3) in dqe, then PD_GU in dql, then dqr_gu
           if (i < C::G3) return dq_dot(dqe[i < C::G3 ? i : 0], x4);
           const int k = i - C::G3;
           return k < PD_GU ? dql_dot(dql, k, x4) : dq_dot(dqr_gu[k >= PD_GU ? k - PD_GU : 0], x4);
         },
-        rows, D, NT, xs, ws, nx_d, w_d, s_d, [&](int pr, float yg, float yu) {
+        map_gu(rows), xs, ws, nx_d, w_d, s_d, [&](int pr, float yg, float yu) {
           // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
           const float g = rbf(yg), u = rbf(yu);
           st_coh_u32(p.act + (r0 >> 1) + pr, f2bf(rbf(silu_f(g)) * u) | (t_act << 16));
@@ -1058,13 +1127,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     const int ln = l + 1 < p.NL ? l + 1 : l;  // the last layer requests nothing
     const NextW nx_qkv = next_w(p.w.wqkv_q + (size_t)ln * NQKV * (D >> 3),
                                 p.w.wqkv_sz + (size_t)ln * NQKV * (D >> 7), r0n, rowsn, D,
-                                sD, l + 1 < p.NL);
-    gemv_compute<C::D, C::QKV, C::QKV, PD_D + C::PR_D, true>(
+                                map_qkv(rowsn), l + 1 < p.NL);
+    gemv_compute<C::D, C::QKV, C::QKV, PD_D + C::PR_D, GM_COLUMN>(
         w_d, s_d,
         [&](int i, const uint4* x4) {
           return i < PD_D ? dql_dot(dql, i, x4) : dq_dot(dqr_d[i >= PD_D ? i - PD_D : 0], x4);
         },
-        rows, F, sF, xs, ws, nx_qkv, w_qkv, s_qkv, [&](int pr, float ya, float yb) {
+        map_stride(F, rows, sF), xs, ws, nx_qkv, w_qkv, s_qkv, [&](int pr, float ya, float yb) {
           residual_pair(p, r0, pr, ya, yb, t_h2, ha, hb);  // engine/model.py:163
         });
     stamp(p, slot);
@@ -1659,14 +1728,20 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-// A GEMV phase's rows per workgroup fit its chunk budget: cap chunks per thread with chunk
-// stride NT (cs = false) or cs_stride(k) (cs = true: NT / (k / 32) rows of chunks per round).
-int phase_fits(int n, int k, int G, int cap, bool cs) {
+// A GEMV phase's rows per workgroup fit its chunk budget: cap chunks per thread, dealt with
+// mode GM_STRIDE (stride NT), GM_COLUMN (stride cs_stride(k): NT / (k / 32) rows of chunks per
+// round) or GM_ROWS (2^rs_lg lanes per row: ceil((k / 32) / lanes) chunks each).
+int phase_fits(int n, int k, int G, int cap, int mode) {
   int R = (n + G - 1) / G;
   R += (R & 1);
   const int cpr = k >> 5;
   if (R > ROWS_MAX || cpr > NT) return 0;
-  return cs ? R <= (NT / cpr) * cap : (long)R * cpr <= (long)cap * NT;
+  if (mode == GM_ROWS) {
+    int lg = 5;  // rs_lg
+    while (lg > 0 && ((R << lg) > NT || (1 << (lg - 1)) >= cpr)) --lg;
+    return R <= NT && (cpr + (1 << lg) - 1) >> lg <= cap;
+  }
+  return mode == GM_COLUMN ? R <= (NT / cpr) * cap : (long)R * cpr <= (long)cap * NT;
 }
 
 }  // namespace
@@ -1832,8 +1907,10 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   const int D = d->dim, F = d->inter, NQKV = (d->n_head + 2 * d->n_kv_head) * FL_HEAD_DIM;
   auto fits = [&](auto c) {
     using C = decltype(c);
-    return phase_fits(NQKV, D, G, C::QKV, true) && phase_fits(D, D, G, C::O, true) &&
-           phase_fits(2 * F, D, G, C::GU, false) && phase_fits(D, F, G, C::D, true);
+    return phase_fits(NQKV, D, G, C::QKV, C::ROWS ? GM_ROWS : GM_COLUMN) &&
+           phase_fits(D, D, G, C::O, GM_COLUMN) &&
+           phase_fits(2 * F, D, G, C::GU, C::ROWS ? GM_ROWS : GM_STRIDE) &&
+           phase_fits(D, F, G, C::D, GM_COLUMN);
   };
   // FLINT_AMD_DECODE_BUDGET=large selects the large-budget instantiation for any model (tests)
   const char* budget = getenv("FLINT_AMD_DECODE_BUDGET");
