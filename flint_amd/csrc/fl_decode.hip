@@ -621,6 +621,7 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
   const int S = m.S;
   const int total = rows * cpr;
   const bool active = tid < S;
+  __builtin_amdgcn_s_setprio(1);  // as in GM_ROWS, until this phase's sums are out
   if constexpr (MODE == GM_COLUMN) {
     const uint4* xp = reinterpret_cast<const uint4*>(xs) + xslot(4 * (tid % cpr));
     const uint4 xr[4] = {xp[0], xp[1], xp[2], xp[3]};
@@ -670,7 +671,7 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
   // measured faster here than the DPP / permlane exchanges of the same lanes.)
   const float other = __shfl_xor(acc, L);
   if (row < rows && !(row & 1) && li == 0) epi(row >> 1, acc, other);
-  lds_barrier();
+  lds_barrier();  __builtin_amdgcn_s_setprio(0);
 }
 
 // Key slices of one query head over the cached keys 0..pos-1. Keys are processed in 8-key steps
