@@ -671,7 +671,8 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
   // measured faster here than the DPP / permlane exchanges of the same lanes.)
   const float other = __shfl_xor(acc, L);
   if (row < rows && !(row & 1) && li == 0) epi(row >> 1, acc, other);
-  lds_barrier();  __builtin_amdgcn_s_setprio(0);
+  lds_barrier();
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // Key slices of one query head over the cached keys 0..pos-1. Keys are processed in 8-key steps
