@@ -578,9 +578,9 @@ enum { GM_STRIDE = 0, GM_COLUMN = 1, GM_ROWS = 2 };
 // y[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load with mapping m (mode MODE);
 // x staged in xs; chunks i < PD come dequantised ahead: pre_dot(i, x4) is their dot with x.
 // After each of this phase's chunks, about 1 / MC of the next phase's chunks [J0, NPRE) are
-// requested. Ends with epi(j, y[2j], y[2j+1]) on the lead lane of every row pair j. The stride
-// modes end with a barrier (part is free again); GM_ROWS writes no LDS, and the next writer of
-// xs waits at a barrier of its own.
+// requested. Ends with epi(j, y[2j], y[2j+1]) on the lead lane of every row pair j. GM_ROWS
+// writes no LDS, and the next writer of xs waits at a barrier of its own; the stride modes end
+// with a barrier (part is free again; measured faster than letting the early waves go on).
 template <int MC, int MCN, int NPRE, int PD, int MODE, int J0 = 0, typename PreDot, typename Epi>
 __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32_t (&sr)[MC],
                                              PreDot pre_dot, const ChunkMap& m,
@@ -846,6 +846,10 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
     mywp[1] = lsum;
   }
   lds_barrier();
+  // The merge runs in wave 0 at raised issue priority; the other waves go on to the next phase's
+  // dequantisation meanwhile (no barrier at the end: that phase touches only each thread's own
+  // dql slots before a barrier of its own, and the LDS used here only after it).
+  if (tid < 64) __builtin_amdgcn_s_setprio(1);
   if (tid < 64) {  // thread d: output dim d, waves merged in a fixed order
     const int d = tid;
     float M = -INFINITY, Ls = 0.0f, O = 0.0f;
@@ -897,7 +901,7 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
       st_coh_u32(p.attn + hq * 64 + d, f2bf(O / Ls) | (otag << 16));
     }
   }
-  lds_barrier();  // LDS is reused by the next phase
+  __builtin_amdgcn_s_setprio(0);
   stamp(p, slot);
 }
 
