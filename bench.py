@@ -127,6 +127,60 @@ def verify_latency(model, args, dev, ctx=1024, reps=20):
             "cost_vs_decode": {k: round(v / dec_us, 3) for k, v in res.items()}}
 
 
+class KnownDraft:
+    """Draft for the speculative-loop timing: proposes a known continuation `ref` of the prompt
+    (chain), or that continuation hidden among two decoy siblings per level (tree: the accepted
+    node is never the first child, so every pass compacts the KV cache). Once the context leaves
+    `ref` it proposes nothing."""
+
+    def __init__(self, ref, vocab, depth=5):
+        self.ref, self.vocab, self.depth = ref, vocab, depth
+
+    def _future(self, context, k):
+        i = len(context)
+        return self.ref[i:i + k] if context == self.ref[:i] else []
+
+    def chain(self, context, feats, k):
+        return self._future(context, k)
+
+    def tree(self, context, feats):
+        toks, pars, par = [], [], -1
+        for t in self._future(context, self.depth):
+            for d in ((t + 1) % self.vocab, (t + 2) % self.vocab, t):
+                toks.append(int(d))
+                pars.append(par)
+            par = len(toks) - 1
+        return toks, pars
+
+
+def spec_loop(model, args, prompt, ref, n, rounds=40):
+    """Speculative greedy decoding through flint_amd.spec (one fl_verify launch per pass, plus
+    fl_kv_move for a tree) at full acceptance: chain k = 4 and 7, a 16-node tree (depth 5, width
+    3), and k = 0 (one verify of M = 1 per token) for the loop's own overhead. The synthetic
+    model's logits are bf16-rounded and often tie at the top, and the verify kernel's fp32 sums
+    depend on M, so a draft built from plain decode loses agreement at the first tie broken the
+    other way; the draft is therefore re-seeded with each run's own output until a run accepts its
+    whole draft (a fixed point, reached within `rounds`), and that run is the one reported.
+    Wall-clock tok/s over the decode loop (prefill excluded), host loop included."""
+    from flint_amd.spec import SpecDecoder
+    res = []
+    for mode, k in (("chain", 0), ("chain", 4), ("chain", 7), ("tree", 0)):
+        cur = ref
+        for r in range(rounds):
+            dec = SpecDecoder(model, KnownDraft(cur, args.vocab_size), k=k)
+            out, st = dec.generate(prompt, n, mode=mode)
+            if out == cur:
+                break
+            cur = out
+        model.check()
+        res.append({"mode": mode, "k": k if mode == "chain" else 15, "tokens": st.tokens,
+                    "passes": st.passes, "tokens_per_pass": round(st.tokens_per_pass, 2),
+                    "tok_s": round(st.tokens / st.seconds, 1),
+                    "ms_per_pass": round(1000 * st.seconds / max(st.passes, 1), 3),
+                    "full_acceptance": out == cur, "reseeds": r})
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -138,6 +192,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true",
                     help="skip the speculative-verify latency of BASELINE config 4")
+    ap.add_argument("--no-spec", action="store_true",
+                    help="skip the speculative-loop timing (chain / tree with a known draft)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="after timing, run one device-to-device copy of this many MiB (the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -200,6 +256,15 @@ def main():
         log(f"verify at ctx {verify['ctx']}: decode {verify['decode_us']} us, "
             f"verify {verify['verify_us']} us")
 
+    spec = None
+    if not a.no_spec:
+        n = min(128, a.warmup + a.steps)
+        spec = spec_loop(model, args, prompt.tolist(), seq[:a.ctx + n].tolist(), n)
+        for r in spec:
+            log(f"spec {r['mode']} k={r['k']}: {r['tok_s']} tok/s, {r['tokens_per_pass']} tokens "
+                f"per pass, {r['ms_per_pass']} ms per pass (full acceptance {r['full_acceptance']} "
+                f"after {r['reseeds']} re-seeds)")
+
     if a.copy_probe_mb > 0:
         n = a.copy_probe_mb * (1 << 20)
         src = torch.ones(n, dtype=torch.uint8, device=dev)
@@ -240,6 +305,7 @@ def main():
                      "traffic": measured_traffic(a.config, a.ctx)},
         "cpu_baseline": cpu,
         "verify": verify,
+        "spec": spec,
     }
     print(json.dumps(out), flush=True)
 

@@ -1732,6 +1732,27 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
   }
 }
 
+// KV cache compaction after a tree verify (the reference moves the accepted path's rows one
+// index copy at a time, spec_tree.py:124-127). One workgroup per (layer, KV group): thread t of
+// the first 16 n moves 16 bytes of K (t / 8 even) or V of row t / 16, and every row is read
+// before any is written, so a destination that is also a later move's source is read first.
+struct KvMove {
+  int32_t src[FL_MAX_VERIFY], dst[FL_MAX_VERIFY];
+  int32_t n;
+};
+__global__ __launch_bounds__(256) void k_kv_move(uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                 int S, KvMove mv) {
+  const int t = threadIdx.x;
+  const size_t base = (size_t)blockIdx.x * S * 64;  // (layer, group) span: S rows of 64 bf16
+  const int i = t >> 4, half = (t >> 3) & 1, part = t & 7;
+  uint16_t* c = half ? vc : kc;
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  const bool on = i < mv.n;
+  if (on) v = reinterpret_cast<const uint4*>(c + base + (size_t)mv.src[i] * 64)[part];
+  __syncthreads();
+  if (on) reinterpret_cast<uint4*>(c + base + (size_t)mv.dst[i] * 64)[part] = v;
+}
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // A GEMV phase's rows per workgroup fit its chunk budget: cap chunks per thread, dealt with
@@ -2023,6 +2044,21 @@ int fl_state_check(fl_state* st, void* stream) {
   if (hipStreamSynchronize(as_stream(stream)) != hipSuccess) return FL_E_HIP;
   if (hipMemcpy(&e, st->err, sizeof(e), hipMemcpyDeviceToHost) != hipSuccess) return FL_E_HIP;
   return e;
+}
+
+int fl_kv_move(fl_state* st, const int32_t* src, const int32_t* dst, int32_t n, void* stream) {
+  if (!st || n < 0 || n > FL_MAX_VERIFY || (n > 0 && (!src || !dst))) return FL_E_ARG;
+  KvMove mv{};
+  mv.n = n;
+  for (int i = 0; i < n; ++i) {
+    if (src[i] < 0 || src[i] >= st->max_seq || dst[i] < 0 || dst[i] >= st->max_seq) return FL_E_POS;
+    mv.src[i] = src[i];
+    mv.dst[i] = dst[i];
+  }
+  if (n == 0) return FL_OK;
+  hipLaunchKernelGGL(k_kv_move, dim3(st->d.n_layer * st->d.n_kv_head), dim3(256), 0,
+                     as_stream(stream), st->kc, st->vc, st->max_seq, mv);
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
 
 int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, int32_t pos,

@@ -163,7 +163,8 @@ class Transformer:
     def verify(self, tokens, pos, depth=None, amask=None, logits=None, feat=None, tokens_out=None):
         """Speculative verify of M tokens at cache slots pos..pos+M-1 (reference verify_mega_launch).
         depth (int32 [M], default arange) gives RoPE positions pos+depth; amask (uint8 [M,M], default
-        causal) the tree mask. Returns (argmax tokens [M], logits [M,V] fp32, feat [M,D] bf16)."""
+        causal) the tree mask. Returns (argmax tokens [M], logits [M,V] fp32, feat [M,D] bf16);
+        logits=False / feat=False skip writing that output (None is returned in its place)."""
         if self._state is None:
             raise RuntimeError("call setup_caches first")
         m = tokens.numel()
@@ -174,14 +175,30 @@ class Transformer:
             amask = torch.tril(torch.ones(m, m, dtype=torch.uint8, device=dev))
         if logits is None:
             logits = torch.empty(m, self.config.vocab_size, dtype=torch.float32, device=dev)
+        elif logits is False:
+            logits = None
         if feat is None:
             feat = torch.empty(m, self.config.dim, dtype=torch.bfloat16, device=dev)
+        elif feat is False:
+            feat = None
         if tokens_out is None:
             tokens_out = torch.empty(m, dtype=torch.int32, device=dev)
         _lib.call("fl_verify", _lib.ctypes.byref(self._cw), self._state, _lib.ptr(tokens.int().contiguous()),
                   m, _lib.ptr(depth.int().contiguous()), _lib.ptr(amask.to(torch.uint8).contiguous()), int(pos),
                   _lib.ptr(tokens_out), _lib.ptr(logits), _lib.ptr(feat), _lib.stream_ptr())
         return tokens_out, logits, feat
+
+    def kv_move(self, src, dst):
+        """Move the K/V rows of cache slots src[i] to dst[i] in every layer (host int lists, at most
+        16): the KV compaction after a tree verify (reference spec_tree.py:124-127). All rows are
+        read before any is written."""
+        if self._state is None:
+            raise RuntimeError("call setup_caches first")
+        n = len(src)
+        if n != len(dst):
+            raise ValueError("src and dst must have the same length")
+        arr = _lib.ctypes.c_int32 * max(n, 1)
+        _lib.call("fl_kv_move", self._state, arr(*src), arr(*dst), n, _lib.stream_ptr())
 
     # reference engine/model.py:134-145 (decode: one token per call)
     def forward(self, idx, input_pos, return_hidden=False):

@@ -138,6 +138,14 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
               const int32_t* depth, const uint8_t* amask, int32_t pos,
               int32_t* tokens_out, float* logits, uint16_t* feat, void* stream);
 
+/* KV cache compaction after a tree verify: for i = 0..n-1 (n <= FL_MAX_VERIFY) the K and V rows
+ * of cache slot src[i] move to slot dst[i], in every layer and KV group. All n rows are read
+ * before any is written, which equals moving them one at a time in order i whenever no source is
+ * an earlier move's destination (true of an accepted tree path: src[i] = pos + path[i+1] >=
+ * pos + i + 1 = dst[i], path increasing). src / dst are host arrays; n = 0 is a no-op.
+ * Replaces the reference's per-step index copies spec_tree.py:124-127. */
+int fl_kv_move(fl_state* st, const int32_t* src, const int32_t* dst, int32_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

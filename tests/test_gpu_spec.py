@@ -1,0 +1,155 @@
+"""GPU parity of the speculative loops (flint_amd/spec.py over fl_verify and fl_kv_move).
+
+fl_kv_move must leave the cache exactly as the reference's one-at-a-time row copies do
+(spec_tree.py:126-128). The chain and tree loops (spec_mega.py:89-117, spec_tree.py:85-133) must
+emit the tokens of sequential greedy decoding with fl_decode_step (reference result.md:111-113).
+The verify and decode kernels sum in different fp32 orders and may break a near-tie the other
+way, so the check is teacher-forced: every emitted token must be fl_decode_step's argmax given
+the emitted prefix, except where the decode logits' top-2 margin is below the noise floor
+(counted and logged).
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import log, make_pair, near_tie
+
+pytestmark = pytest.mark.gpu
+
+
+def test_kv_move_equals_in_order_copies(dev):
+    from flint_amd import _lib
+    args, _, eng, _ = make_pair("tiny", seed=3)
+    eng.setup_caches(1, 128)
+    g = torch.Generator().manual_seed(4)
+    eng.k_cache.copy_(torch.randn(eng.k_cache.shape, generator=g).to(torch.bfloat16))
+    eng.v_cache.copy_(torch.randn(eng.v_cache.shape, generator=g).to(torch.bfloat16))
+    for pos, path in ((40, [0, 2, 5, 6, 9]), (0, [0, 1, 3]), (100, list(range(16))),
+                      (7, [0, 15]),
+                      (60, [0, 3, 4, 8, 12, 13, 14, 15])):
+        src = [pos + p for s, p in enumerate(path) if s and p != s]
+        dst = [pos + s for s, p in enumerate(path) if s and p != s]
+        log(f"kv_move pos={pos} path={path} moves={len(src)}")
+        k_ref, v_ref = eng.k_cache.clone(), eng.v_cache.clone()
+        for s, d in zip(src, dst):
+            k_ref[:, :, d] = k_ref[:, :, s]
+            v_ref[:, :, d] = v_ref[:, :, s]
+        eng.kv_move(src, dst)
+        torch.cuda.synchronize()
+        assert torch.equal(eng.k_cache, k_ref) and torch.equal(eng.v_cache, v_ref)
+    # sixteen arbitrary disjoint moves (no source is another move's destination)
+    src, dst = list(range(64, 80)), list(range(16))
+    k_ref, v_ref = eng.k_cache.clone(), eng.v_cache.clone()
+    k_ref[:, :, dst] = k_ref[:, :, src]
+    v_ref[:, :, dst] = v_ref[:, :, src]
+    eng.kv_move(src[::-1], dst[::-1])
+    torch.cuda.synchronize()
+    assert torch.equal(eng.k_cache, k_ref) and torch.equal(eng.v_cache, v_ref)
+    before = eng.k_cache.clone()
+    eng.kv_move([], [])
+    with pytest.raises(_lib.FlError):
+        eng.kv_move(list(range(17)), list(range(17)))
+    with pytest.raises(_lib.FlError):
+        eng.kv_move([eng.max_seq_length], [0])
+    with pytest.raises(_lib.FlError):
+        eng.kv_move([0], [-1])
+    torch.cuda.synchronize()
+    assert torch.equal(eng.k_cache, before)
+    eng.check()
+
+
+def _decode_check(eng, out, t0, label):
+    """Teacher-forced sequential greedy: decode out[:t0+i] with fl_decode_step and require
+    out[t0+i] to be its argmax, except where the decode logits' top-2 margin is below the noise
+    floor. Returns the number of such tie-breaks that went the other way."""
+    from flint_amd.generate import prefill
+    dev = eng.device
+    eng.setup_caches(1, len(out) + 16)
+    if t0 > 1:
+        prefill(eng, torch.tensor(out[:t0 - 1], dtype=torch.int32), 0)
+    logits = torch.empty(eng.config.vocab_size, dtype=torch.float32, device=dev)
+    toks = torch.tensor(out, dtype=torch.int32, device=dev)
+    am = torch.empty(len(out) - t0, dtype=torch.int32, device=dev)
+    lgs = torch.empty(len(out) - t0, eng.config.vocab_size, dtype=torch.float32, device=dev)
+    for i in range(len(out) - t0):
+        eng.decode_step(toks[t0 - 1 + i:t0 + i], t0 - 1 + i, token_out=am[i:i + 1], logits=lgs[i])
+    eng.check()
+    am, lgs = am.tolist(), lgs.cpu()
+    flips = 0
+    for i, a in enumerate(am):
+        if a != out[t0 + i]:
+            assert near_tie(lgs[i]), (label, i, a, out[t0 + i])
+            flips += 1
+    log(f"{label}: {len(am)} tokens = teacher-forced decode argmax ({flips} noise-floor tie-breaks differ)")
+    return flips
+
+
+class FutureDraft:
+    """Proposes a known continuation `ref` of the prompt (the sequence an earlier run emitted),
+    with planted mistakes (chain), or a tree that hides the true branch behind decoy siblings
+    (tree): full, partial and zero acceptance and KV compaction over non-trivial paths, on the
+    real model. Once the context leaves `ref` it proposes nothing."""
+
+    def __init__(self, ref, vocab, seed, err):
+        self.ref, self.vocab = ref, vocab
+        self.rng = np.random.default_rng(seed)
+        self.err = err
+
+    def _future(self, context, k):
+        i = len(context)
+        if context != self.ref[:i]:
+            return []
+        return self.ref[i:i + k]
+
+    def _decoy(self, t):
+        return int((t + 1 + self.rng.integers(0, self.vocab - 1)) % self.vocab)
+
+    def chain(self, context, feats, k):
+        out = list(self._future(context, k))
+        for j in range(len(out)):
+            if self.rng.random() < self.err:
+                out[j] = self._decoy(out[j])
+        return out
+
+    def tree(self, context, feats):
+        fut = self._future(context, 5)
+        toks, pars, par = [], [], -1
+        for t in fut:
+            kids = [self._decoy(t) for _ in range(2)] + [t]
+            self.rng.shuffle(kids)
+            if self.rng.random() < self.err:
+                kids = [k for k in kids if k != t]
+            node = None
+            for kk in kids:
+                toks.append(int(kk))
+                pars.append(par)
+                if kk == t:
+                    node = len(toks) - 1
+            if node is None:
+                break
+            par = node
+        return toks, pars
+
+
+@pytest.mark.parametrize("mode", ["chain", "tree"])
+def test_spec_decode_equals_sequential_greedy(dev, mode):
+    from flint_amd.spec import LookupDraft, SpecDecoder
+    args, _, eng, _ = make_pair("small", seed=21)
+    g = torch.Generator().manual_seed(22)
+    prompt = torch.randint(0, args.vocab_size, (37,), generator=g).tolist()
+    n, t0 = 64, len(prompt)
+    log(f"spec {mode} lookup: prompt {t0} new {n}")
+    first, st = SpecDecoder(eng, LookupDraft(width=3, depth=4), k=4).generate(prompt, n, mode=mode)
+    log(f"  {st}")
+    flips = _decode_check(eng, first, t0, f"{mode} lookup")
+    for label, err, k in (("future err 0", 0.0, 7), ("future err 0.25", 0.25, 4)):
+        log(f"spec {mode} {label}: prompt {t0} new {n}")
+        draft = FutureDraft(first, args.vocab_size, 1 if err == 0 else 2, err)
+        out, st = SpecDecoder(eng, draft, k=k).generate(prompt, n, mode=mode)
+        log(f"  {st}")
+        flips += _decode_check(eng, out, t0, f"{mode} {label}")
+        if out == first and err == 0:
+            assert st.passes <= -(-n // 4)      # at least 4 new tokens per verify pass
+        if out == first and mode == "tree":
+            assert st.tokens_per_pass > 1.5
+    assert flips <= 6
