@@ -1234,37 +1234,44 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 // (bf16) and the unit's mask row [16]
 inline size_t verify_lds_bytes(int M, int D) {
   const size_t xs = ((size_t)(M + 1) * (D + 8) * 2 + 15) & ~(size_t)15;
-  return xs + NWAVE * 256 * 4 + (64 + 2 * FL_MAX_VERIFY * 64) * 2 + FL_MAX_VERIFY;
+  return xs + NWAVE * 256 * 4 + 3 * FL_MAX_VERIFY * 64 * 2 + FL_MAX_VERIFY * FL_MAX_VERIFY;
 }
 
-// xs[m][k - k0] (row stride ld) = values of the tagged rows src[m * stride + k], m < M,
-// k0 <= k < k0 + kn (kn % 4 == 0), once every word carries `tag`; four 16-byte groups per thread
-// are requested before any is checked
+// Token rows [M, kn] of a tagged exchange buffer (row stride `stride` words, columns k0 ..
+// k0+kn-1) -> bf16 rows of xs, once every word carries `tag`. Each thread requests up to SB
+// 16-byte groups at once (all of them for M <= 6 at D = 2560) and then waits for them one by
+// one. A phase requests its first weight tile before this: a poll that fails is re-sent behind
+// every load already issued, so weights requested after a failed poll delay the next look at
+// the inputs.
 __device__ void stage_rows(const DecodeParams& p, const uint32_t* src, int stride, int M, int k0,
                            int kn, uint32_t tag, uint16_t* xs, int ld) {
+  constexpr int SB = 8;
   const int tid = tid_here();
   const int gpr = kn >> 2, total = M * gpr;
   auto ok = [tag](uint4 w) {
     return ((w.x >> 16) == tag) & ((w.y >> 16) == tag) & ((w.z >> 16) == tag) & ((w.w >> 16) == tag);
   };
-  for (int base = 0; base < total; base += 4 * NT) {
-    uint4 v[4];
+  auto addr = [&](int idx) {
+    const int m = idx / gpr, g = idx - m * gpr;
+    return src + (size_t)m * stride + k0 + 4 * g;
+  };
+  for (int base = 0; base < total; base += SB * NT) {
+    uint4 v[SB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = min(base + tid + i * NT, total - 1);
-      const int m = idx / gpr, g = idx - m * gpr;
-      v[i] = ld_coh_u128(src + (size_t)m * stride + k0 + 4 * g);
+    for (int i = 0; i < SB; ++i) {
+      const int idx = base + tid + i * NT;
+      v[i] = idx < total ? ld_coh_u128(addr(idx)) : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < SB; ++i) {
       const int idx = base + tid + i * NT;
       if (idx < total) {
-        const int m = idx / gpr, g = idx - m * gpr;
         uint4 w = v[i];
         if (!ok(w)) {
-          const uint32_t* a = src + (size_t)m * stride + k0 + 4 * g;
+          const uint32_t* a = addr(idx);
           w = spin_until(p, w, ok, [a]() { return ld_coh_u128(a); });
         }
+        const int m = idx / gpr, g = idx - m * gpr;
         reinterpret_cast<uint2*>(xs + m * ld)[g] =
             make_uint2((w.x & 0xFFFFu) | (w.y << 16), (w.z & 0xFFFFu) | (w.w << 16));
       }
@@ -1272,74 +1279,97 @@ __device__ void stage_rows(const DecodeParams& p, const uint32_t* src, int strid
   }
 }
 
-// rows m < M of xs: x <- bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)  (engine/model.py:237-242),
-// one wave per row
+// rows m < M of xs: x <- bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)  (engine/model.py:237-242).
+// A row is shared by NWAVE / M waves (all 8 for one token), whose partial sums of squares meet
+// in red (NWAVE floats of LDS); the row loop has the same trip count in every wave, so the
+// barriers are uniform.
 __device__ void norm_rows(uint16_t* xs, int ld, int M, int D, const uint16_t* __restrict__ nw,
-                          float eps) {
+                          float eps, float* red) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
-  for (int m = wave; m < M; m += NWAVE) {
-    uint4* row = reinterpret_cast<uint4*>(xs + m * ld);
+  int wpr = 1;                                  // waves per row: a power of two, wpr * M <= NWAVE
+  while (wpr * 2 * M <= NWAVE) wpr *= 2;
+  const int rpp = NWAVE / wpr;                  // rows per pass
+  const int sub = wave % wpr, nch = D >> 3;     // this wave's share of a row; 8-value chunks per row
+  for (int m0 = 0; m0 < M; m0 += rpp) {
+    const int m = m0 + wave / wpr;
+    const bool on = m < M;
+    uint4* row = reinterpret_cast<uint4*>(xs + (on ? m : 0) * ld);
     float ss = 0.0f;
-    for (int i = lane; i < (D >> 3); i += 64) {
-      const uint4 v = row[i];
-      const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+    if (on)
+      for (int i = sub * 64 + lane; i < nch; i += wpr * 64) {
+        const uint4 v = row[i];
+        const uint32_t in[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        ss += bflo(in[j]) * bflo(in[j]);
-        ss += bfhi(in[j]) * bfhi(in[j]);
+        for (int j = 0; j < 4; ++j) {
+          ss += bflo(in[j]) * bflo(in[j]);
+          ss += bfhi(in[j]) * bfhi(in[j]);
+        }
       }
-    }
     ss = wave_sum(ss);
-    const float r = 1.0f / sqrtf(ss / (float)D + eps);
-    for (int i = lane; i < (D >> 3); i += 64) {
-      const uint4 v = row[i];
-      const uint4 g = reinterpret_cast<const uint4*>(nw)[i];
-      const uint32_t in[4] = {v.x, v.y, v.z, v.w};
-      const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
-      uint32_t o[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float na = rbf(bflo(in[j]) * r), nb = rbf(bfhi(in[j]) * r);
-        o[j] = pack_bf16x2(na * bflo(gw[j]), nb * bfhi(gw[j]));
-      }
-      row[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    if (wpr > 1) {
+      if (lane == 0) red[wave] = ss;
+      lds_barrier();
+      ss = 0.0f;
+      for (int w = 0; w < wpr; ++w) ss += red[(wave / wpr) * wpr + w];
     }
+    const float r = 1.0f / sqrtf(ss / (float)D + eps);
+    if (on)
+      for (int i = sub * 64 + lane; i < nch; i += wpr * 64) {
+        const uint4 v = row[i];
+        const uint4 g = reinterpret_cast<const uint4*>(nw)[i];
+        const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float na = rbf(bflo(in[j]) * r), nb = rbf(bfhi(in[j]) * r);
+          o[j] = pack_bf16x2(na * bflo(gw[j]), nb * bfhi(gw[j]));
+        }
+        row[i] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    if (wpr > 1) lds_barrier();  // red is reused by the next pass
   }
 }
 
-// acc += X(token rows of xs) . dq(rows n0 .. n0+rows of a [N, K] int4 matrix)^T over the groups
-// g0 .. g0+ng-1 (ng <= 32) of the K block staged in xs (xs column 0 = group g0); this wave takes
-// groups g0 + wave + 8i
-__device__ __forceinline__ void tile_mma_int4(const uint32_t* __restrict__ q,
-                                              const uint32_t* __restrict__ sz, int n0, int rows,
-                                              int K, int g0, int ng, const uint16_t* xs, int ld,
-                                              int M, fl_f32x4& acc) {
-  constexpr int GPW = 4;
+// The weights of one 16-row tile of an [N, K] int4 matrix over the K groups g0 .. g0+ng-1
+// (ng <= 32): this wave's groups g0 + wave + 8i, one 16-byte quarter-group per lane. Loading
+// does not depend on the token rows, so a phase requests its first tile before it waits for its
+// inputs and the next tile before it computes the current one.
+struct TileW {
+  uint4 w[4];
+  uint32_t s[4];
+};
+__device__ __forceinline__ void tile_load(const uint32_t* __restrict__ q, const uint32_t* __restrict__ sz,
+                                          int n0, int rows, int K, int g0, int ng, TileW& tw) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
   const int r = lane & 15, c = lane >> 4;
   const int groups = K >> 7;
   const auto wr = buf_rsrc(q + (size_t)n0 * (K >> 3), (uint32_t)rows * (uint32_t)(K >> 1));
   const auto sr = buf_rsrc(sz + (size_t)n0 * groups, (uint32_t)rows * (uint32_t)groups * 4u);
-  uint4 w[GPW];
-  uint32_t s[GPW];
 #pragma unroll
-  for (int i = 0; i < GPW; ++i) {
+  for (int i = 0; i < 4; ++i) {
     const int u = wave + NWAVE * i;
     const uint32_t gg = (uint32_t)(g0 + u);
     const bool in = u < ng;
-    w[i] = buf_ld128(wr, in ? (uint32_t)r * (uint32_t)(K >> 1) + gg * 64u + (uint32_t)c * 16u : 0xFFFFFFF0u);
-    s[i] = buf_ld32(sr, in ? ((uint32_t)r * (uint32_t)groups + gg) * 4u : 0xFFFFFFF0u);
+    tw.w[i] = buf_ld128(wr, in ? (uint32_t)r * (uint32_t)(K >> 1) + gg * 64u + (uint32_t)c * 16u : 0xFFFFFFF0u);
+    tw.s[i] = buf_ld32(sr, in ? ((uint32_t)r * (uint32_t)groups + gg) * 4u : 0xFFFFFFF0u);
   }
+}
+// acc += X(token rows of xs) . dq(tile)^T; xs column 0 = group g0 of the tile's K range
+__device__ __forceinline__ void tile_mma(const TileW& tw, int ng, const uint16_t* xs, int ld, int M,
+                                         fl_f32x4& acc) {
+  const int lane = tid_here() & 63, wave = tid_here() >> 6;
+  const int r = lane & 15, c = lane >> 4;
   const uint16_t* xrow = xs + (r < M ? r : M) * ld + c * 32;
 #pragma unroll
-  for (int i = 0; i < GPW; ++i) {
+  for (int i = 0; i < 4; ++i) {
     const int u = wave + NWAVE * i;
     if (u < ng) {  // wave-uniform
       uint4 xa[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) xa[e] = *reinterpret_cast<const uint4*>(xrow + u * 128 + e * 8);
       uint32_t d[4][4];
-      dq32(w[i], dq_const(s[i]), d);
+      dq32(tw.w[i], dq_const(tw.s[i]), d);
       mfma_chunk(d, xa, acc);
     }
   }
@@ -1361,7 +1391,12 @@ __device__ __forceinline__ float tile_sum(const float* part, int t) {
   return v;
 }
 
-// attention of every (query head, token) unit (engine/model.py:171-179 over the verify key set)
+// Attention (engine/model.py:171-179 over the verify key set). A unit is one query head and a
+// group of TPU consecutive tokens, TPU the fewest that give every workgroup at most one unit; the
+// unit requests the head's cached keys and values once and runs its tokens one after another.
+// While the cache fits one round of registers (pos <= 8 * NWAVE * RB) the later tokens reuse it.
+// LDS att: q of the unit's tokens [16][64], then the new k and v of the group [16][64] each;
+// amk: the unit's amask rows.
 __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
                                  uint16_t* att, uint8_t* amk, float* wpart) {
   constexpr int RB = 12;
@@ -1371,11 +1406,13 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
   const int HALF = (NH + 2 * NKV) * 32;  // tagged pairs per token
   const int ns = (pos + 7) >> 3;         // 8-key steps over the cached keys [0, pos)
   const int nrounds = (ns + NWAVE * RB - 1) / (NWAVE * RB);
+  const int TPU = (NH * M + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int ngrp = (M + TPU - 1) / TPU;
   const float sc = p.attn_scale * 1.4426950408889634f;
   const uint32_t* att32 = reinterpret_cast<const uint32_t*>(att);
-  for (int u = blockIdx.x; u < NH * M; u += gridDim.x) {
-    const int g = u % NKV, rest = u / NKV, j = rest % QPG, m = rest / QPG;
-    const int hq = g * QPG + j;
+  for (int u = blockIdx.x; u < NH * ngrp; u += gridDim.x) {
+    const int g = u % NKV, rest = u / NKV, j = rest % QPG, grp = rest / QPG;
+    const int hq = g * QPG + j, m0 = grp * TPU, mt = min(M, m0 + TPU) - m0;
     const size_t cbase = (size_t)(l * NKV + g) * p.S * 64;
     const auto kb = buf_rsrc(p.kc + cbase, (uint32_t)pos * 128u);
     const auto vb = buf_rsrc(p.vc + cbase, (uint32_t)pos * 128u);
@@ -1389,116 +1426,120 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
       }
     };
     if (nrounds > 0) issue(0);
-    // LDS: q of (hq, token m), then new k / v of group g for tokens 0..M-1 (bf16 [16][64] each)
-    for (int i = tid; i < 32 + 64 * M; i += NT) {
+    const int nq = 32 * mt;
+    for (int i = tid; i < nq + 64 * M; i += NT) {
       int hh, tok, d, dst;
-      if (i < 32) {
-        hh = hq, tok = m, d = i, dst = 0;
+      if (i < nq) {
+        hh = hq, tok = m0 + (i >> 5), d = i & 31, dst = (i >> 5) * 64;
       } else {
-        const int i2 = i - 32, which = i2 / (32 * M), r2 = i2 - which * 32 * M;
+        const int i2 = i - nq, which = i2 / (32 * M), r2 = i2 - which * 32 * M;
         tok = r2 >> 5, d = r2 & 31;
         hh = which ? NH + NKV + g : NH + g;
-        dst = 64 + which * FL_MAX_VERIFY * 64 + tok * 64;
+        dst = (1 + which) * FL_MAX_VERIFY * 64 + tok * 64;
       }
       const unsigned long long v = wait_pair(p, p.qkv + (size_t)tok * HALF + hh * 32 + d, qtag);
       att[dst + d] = (uint16_t)v;
       att[dst + d + 32] = (uint16_t)(v >> 16);
     }
-    if (tid < M) amk[tid] = p.amask[m * M + tid];
+    for (int i = tid; i < mt * M; i += NT) amk[i] = p.amask[m0 * M + i];
     lds_barrier();
-    uint32_t qv[4];
+    for (int mi = 0; mi < mt; ++mi) {
+      const int m = m0 + mi;
+      uint32_t qv[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) qv[e] = att32[ds * 4 + e];
-    float mx = -INFINITY, lsum = 0.0f, o[8];
+      for (int e = 0; e < 4; ++e) qv[e] = att32[mi * 32 + ds * 4 + e];
+      float mx = -INFINITY, lsum = 0.0f, o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
-    for (int r = 0; r < nrounds; ++r) {
-      if (r > 0) issue(r);
-      float s[RB];
-      float rmax = -INFINITY;
+      for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+      if (mi > 0 && nrounds > 1) issue(0);  // the registers hold the last round
+      for (int r = 0; r < nrounds; ++r) {
+        if (r > 0) issue(r);
+        float s[RB];
+        float rmax = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const int st = r * NWAVE * RB + wave + NWAVE * i;
-        float a = dot2_bf16(kr[i].x, qv[0], 0.0f);
-        a = dot2_bf16(kr[i].y, qv[1], a);
-        a = dot2_bf16(kr[i].z, qv[2], a);
-        a = dot2_bf16(kr[i].w, qv[3], a);
-        a = sum8(a);
-        s[i] = (st * 8 + kk < pos) ? a * sc : -INFINITY;
-        rmax = fmaxf(rmax, s[i]);
-      }
-      const float mn = fmaxf(mx, max_stride8(rmax));
-      const float mu = (mn == -INFINITY) ? 0.0f : mn;
-      const float corr = __builtin_amdgcn_exp2f(mx - mu);
-      lsum *= corr;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] *= corr;
-      mx = mn;
-#pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const float pw = __builtin_amdgcn_exp2f(s[i] - mu);
-        lsum += pw;
-        o[0] = __builtin_fmaf(pw, bflo(vr[i].x), o[0]);
-        o[1] = __builtin_fmaf(pw, bfhi(vr[i].x), o[1]);
-        o[2] = __builtin_fmaf(pw, bflo(vr[i].y), o[2]);
-        o[3] = __builtin_fmaf(pw, bfhi(vr[i].y), o[3]);
-        o[4] = __builtin_fmaf(pw, bflo(vr[i].z), o[4]);
-        o[5] = __builtin_fmaf(pw, bfhi(vr[i].z), o[5]);
-        o[6] = __builtin_fmaf(pw, bflo(vr[i].w), o[6]);
-        o[7] = __builtin_fmaf(pw, bfhi(vr[i].w), o[7]);
-      }
-    }
-    if (wave == 0) {  // the new tokens' keys, 8 per step, masked by amask[m][.]
-      for (int s0 = 0; s0 < M; s0 += 8) {
-        const int jn = s0 + kk;
-        const bool valid = jn < M && amk[min(jn, M - 1)] != 0;
-        const int js = min(jn, M - 1);
-        const uint32_t* kw = att32 + 32 + js * 32 + ds * 4;
-        const uint32_t* vw = att32 + 32 + FL_MAX_VERIFY * 32 + js * 32 + ds * 4;
-        float a = dot2_bf16(kw[0], qv[0], 0.0f);
-        a = dot2_bf16(kw[1], qv[1], a);
-        a = dot2_bf16(kw[2], qv[2], a);
-        a = dot2_bf16(kw[3], qv[3], a);
-        a = sum8(a);
-        const float sn = valid ? a * sc : -INFINITY;
-        const float mn = fmaxf(mx, max_stride8(sn));
+        for (int i = 0; i < RB; ++i) {
+          const int st = r * NWAVE * RB + wave + NWAVE * i;
+          float a = dot2_bf16(kr[i].x, qv[0], 0.0f);
+          a = dot2_bf16(kr[i].y, qv[1], a);
+          a = dot2_bf16(kr[i].z, qv[2], a);
+          a = dot2_bf16(kr[i].w, qv[3], a);
+          a = sum8(a);
+          s[i] = (st * 8 + kk < pos) ? a * sc : -INFINITY;
+          rmax = fmaxf(rmax, s[i]);
+        }
+        const float mn = fmaxf(mx, max_stride8(rmax));
         const float mu = (mn == -INFINITY) ? 0.0f : mn;
         const float corr = __builtin_amdgcn_exp2f(mx - mu);
-        const float pw = __builtin_amdgcn_exp2f(sn - mu);
-        lsum = lsum * corr + pw;
+        lsum *= corr;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          o[2 * e] = __builtin_fmaf(pw, bflo(vw[e]), o[2 * e] * corr);
-          o[2 * e + 1] = __builtin_fmaf(pw, bfhi(vw[e]), o[2 * e + 1] * corr);
-        }
+        for (int e = 0; e < 8; ++e) o[e] *= corr;
         mx = mn;
-      }
-    }
-    lsum = sum_stride8(lsum);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = sum_stride8(o[e]);
-    float* mywp = wpart + wave * 66;
-    if (kk == 0) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) mywp[2 + ds * 8 + e] = o[e];
-    }
-    if (lane == 0) {
-      mywp[0] = mx;
-      mywp[1] = lsum;
-    }
-    lds_barrier();
-    if (tid < 64) {
-      float M_ = -INFINITY, Ls = 0.0f, O = 0.0f;
-      for (int w = 0; w < NWAVE; ++w) M_ = fmaxf(M_, wpart[w * 66]);
-      for (int w = 0; w < NWAVE; ++w) {
-        const float* wp = wpart + w * 66;
-        const float e = (wp[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wp[0] - M_);
-        Ls += wp[1] * e;
-        O += wp[2 + tid] * e;
+        for (int i = 0; i < RB; ++i) {
+          const float pw = __builtin_amdgcn_exp2f(s[i] - mu);
+          lsum += pw;
+          o[0] = __builtin_fmaf(pw, bflo(vr[i].x), o[0]);
+          o[1] = __builtin_fmaf(pw, bfhi(vr[i].x), o[1]);
+          o[2] = __builtin_fmaf(pw, bflo(vr[i].y), o[2]);
+          o[3] = __builtin_fmaf(pw, bfhi(vr[i].y), o[3]);
+          o[4] = __builtin_fmaf(pw, bflo(vr[i].z), o[4]);
+          o[5] = __builtin_fmaf(pw, bfhi(vr[i].z), o[5]);
+          o[6] = __builtin_fmaf(pw, bflo(vr[i].w), o[6]);
+          o[7] = __builtin_fmaf(pw, bfhi(vr[i].w), o[7]);
+        }
       }
-      st_coh_u32(p.attn + (size_t)m * p.D + hq * 64 + tid, f2bf(O / Ls) | (otag << 16));
+      if (wave == 0) {  // the new tokens' keys, 8 per step, masked by amask[m][.]
+        for (int s0 = 0; s0 < M; s0 += 8) {
+          const int jn = s0 + kk;
+          const bool valid = jn < M && amk[mi * M + min(jn, M - 1)] != 0;
+          const int js = min(jn, M - 1);
+          const uint32_t* kw = att32 + FL_MAX_VERIFY * 32 + js * 32 + ds * 4;
+          const uint32_t* vw = att32 + 2 * FL_MAX_VERIFY * 32 + js * 32 + ds * 4;
+          float a = dot2_bf16(kw[0], qv[0], 0.0f);
+          a = dot2_bf16(kw[1], qv[1], a);
+          a = dot2_bf16(kw[2], qv[2], a);
+          a = dot2_bf16(kw[3], qv[3], a);
+          a = sum8(a);
+          const float sn = valid ? a * sc : -INFINITY;
+          const float mn = fmaxf(mx, max_stride8(sn));
+          const float mu = (mn == -INFINITY) ? 0.0f : mn;
+          const float corr = __builtin_amdgcn_exp2f(mx - mu);
+          const float pw = __builtin_amdgcn_exp2f(sn - mu);
+          lsum = lsum * corr + pw;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[2 * e] = __builtin_fmaf(pw, bflo(vw[e]), o[2 * e] * corr);
+            o[2 * e + 1] = __builtin_fmaf(pw, bfhi(vw[e]), o[2 * e + 1] * corr);
+          }
+          mx = mn;
+        }
+      }
+      lsum = sum_stride8(lsum);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = sum_stride8(o[e]);
+      float* mywp = wpart + wave * 66;
+      if (kk == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mywp[2 + ds * 8 + e] = o[e];
+      }
+      if (lane == 0) {
+        mywp[0] = mx;
+        mywp[1] = lsum;
+      }
+      lds_barrier();
+      if (tid < 64) {
+        float M_ = -INFINITY, Ls = 0.0f, O = 0.0f;
+        for (int w = 0; w < NWAVE; ++w) M_ = fmaxf(M_, wpart[w * 66]);
+        for (int w = 0; w < NWAVE; ++w) {
+          const float* wp = wpart + w * 66;
+          const float e = (wp[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wp[0] - M_);
+          Ls += wp[1] * e;
+          O += wp[2 + tid] * e;
+        }
+        st_coh_u32(p.attn + (size_t)m * p.D + hq * 64 + tid, f2bf(O / Ls) | (otag << 16));
+      }
+      lds_barrier();
     }
-    lds_barrier();
   }
 }
 
@@ -1511,8 +1552,10 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
   uint16_t* xs = reinterpret_cast<uint16_t*>(vsm);
   float* part = reinterpret_cast<float*>(vsm + (((size_t)(M + 1) * ld * 2 + 15) & ~(size_t)15));
   uint16_t* att = reinterpret_cast<uint16_t*>(part + NWAVE * 256);
-  uint8_t* amk = reinterpret_cast<uint8_t*>(att + 64 + 2 * FL_MAX_VERIFY * 64);
+  uint8_t* amk = reinterpret_cast<uint8_t*>(att + 3 * FL_MAX_VERIFY * 64);
   for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + M * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
+  int slot = 0;  // optional timestamps, same slots as k_decode's
+  stamp(p, slot);
 
   auto token_at = [&](int m) {
     int t = p.tokens[m];
@@ -1538,7 +1581,11 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
     const uint32_t t_prev = tag_of(e0 - 1), t_qkv = tag_of(e0), t_attn = tag_of(e0 + 1),
                    t_h1 = tag_of(e0 + 2), t_act = tag_of(e0 + 3), t_h2 = tag_of(e0 + 4);
     // ---------------- P1: RMSNorm + QKV + RoPE + KV append ----------------
+    const uint32_t* const qkv_q = p.w.wqkv_q + (size_t)l * NQKV * (D >> 3);
+    const uint32_t* const qkv_sz = p.w.wqkv_sz + (size_t)l * NQKV * (D >> 7);
     if (wg < NQKV / 16) {
+      TileW tw;
+      tile_load(qkv_q, qkv_sz, wg * 16, 16, D, 0, D >> 7, tw);
       if (l == 0) {  // bf16(embed[token] * emb_mult)  (engine/model.py:138)
         for (int i = tid; i < M * (D >> 1); i += NT) {
           const int m = i / (D >> 1), c = i - m * (D >> 1);
@@ -1550,13 +1597,15 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
         stage_rows(p, p.h, D, M, 0, D, t_prev, xs, ld);
       }
       lds_barrier();
-      norm_rows(xs, ld, M, D, p.w.attn_norm + (size_t)l * D, p.eps);
+      norm_rows(xs, ld, M, D, p.w.attn_norm + (size_t)l * D, p.eps, part);
       lds_barrier();
+      stamp(p, slot);
       for (int t = wg; t < NQKV / 16; t += G) {
         const int n0 = t * 16;
+        const TileW cur = tw;
+        if (t + G < NQKV / 16) tile_load(qkv_q, qkv_sz, (t + G) * 16, 16, D, 0, D >> 7, tw);
         fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        tile_mma_int4(p.w.wqkv_q + (size_t)l * NQKV * (D >> 3), p.w.wqkv_sz + (size_t)l * NQKV * (D >> 7),
-                      n0, 16, D, 0, D >> 7, xs, ld, M, acc);
+        tile_mma(cur, D >> 7, xs, ld, M, acc);
         tile_publish(part, acc);
         if (tid < 128) {  // (token, NEOX pair) of the tile
           const int m = tid >> 3, pp = tid & 7;
@@ -1583,18 +1632,31 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
         }
         lds_barrier();
       }
+    } else {
+      stamp(p, slot);
     }
+    stamp(p, slot);
     // ---------------- P2: attention ----------------
+    stamp(p, slot);
+    stamp(p, slot);
     attention_verify(p, l, t_qkv, t_attn, att, amk, part);
+    stamp(p, slot);
+    stamp(p, slot);
     // ---------------- P3: O projection + residual ----------------
     if (wg < D / 16) {
+      const uint32_t* const o_q = p.w.wo_q + (size_t)l * D * (D >> 3);
+      const uint32_t* const o_sz = p.w.wo_sz + (size_t)l * D * (D >> 7);
+      TileW tw;
+      tile_load(o_q, o_sz, wg * 16, 16, D, 0, D >> 7, tw);
       stage_rows(p, p.attn, D, M, 0, D, t_attn, xs, ld);
       lds_barrier();
+      stamp(p, slot);
       for (int t = wg; t < D / 16; t += G) {
         const int n0 = t * 16;
+        const TileW cur = tw;
+        if (t + G < D / 16) tile_load(o_q, o_sz, (t + G) * 16, 16, D, 0, D >> 7, tw);
         fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        tile_mma_int4(p.w.wo_q + (size_t)l * D * (D >> 3), p.w.wo_sz + (size_t)l * D * (D >> 7), n0, 16,
-                      D, 0, D >> 7, xs, ld, M, acc);
+        tile_mma(cur, D >> 7, xs, ld, M, acc);
         tile_publish(part, acc);
         if (tid < 256) {
           const int m = tid >> 4, n = tid & 15;
@@ -1614,16 +1676,25 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
       }
     }
     // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
+    if (wg >= D / 16) stamp(p, slot);
+    stamp(p, slot);
     if (wg < (2 * F) / 16) {
+      const uint32_t* const gu_q = p.w.wgu_q + (size_t)l * 2 * F * (D >> 3);
+      const uint32_t* const gu_sz = p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7);
+      const int nt = ((2 * F) / 16 - wg + G - 1) / G;  // this workgroup's tiles wg, wg+G, ...
+      TileW tw;
+      tile_load(gu_q, gu_sz, wg * 16, 16, D, 0, D >> 7, tw);
       stage_rows(p, p.h, D, M, 0, D, t_h1, xs, ld);
       lds_barrier();
-      norm_rows(xs, ld, M, D, p.w.ffn_norm + (size_t)l * D, p.eps);
+      norm_rows(xs, ld, M, D, p.w.ffn_norm + (size_t)l * D, p.eps, part);
       lds_barrier();
+      stamp(p, slot);
       for (int t = wg; t < (2 * F) / 16; t += G) {
         const int n0 = t * 16;
+        const TileW cur = tw;
+        if (t + G < (2 * F) / 16) tile_load(gu_q, gu_sz, (t + G) * 16, 16, D, 0, D >> 7, tw);
         fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        tile_mma_int4(p.w.wgu_q + (size_t)l * 2 * F * (D >> 3), p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7),
-                      n0, 16, D, 0, D >> 7, xs, ld, M, acc);
+        tile_mma(cur, D >> 7, xs, ld, M, acc);
         tile_publish(part, acc);
         if (tid < 128) {
           const int m = tid >> 3, pp = tid & 7;
@@ -1635,19 +1706,35 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
         lds_barrier();
       }
     }
+    if (wg >= (2 * F) / 16) stamp(p, slot);
+    stamp(p, slot);
     // ---------------- P5: down projection + residual (K staged in blocks of D) ----------------
+    int p5slot = slot;
+    slot += 2;
     if (wg < D / 16) {
-      for (int t = wg; t < D / 16; t += G) {
-        const int n0 = t * 16;
-        fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int k0 = 0; k0 < F; k0 += D) {
-          const int kn = min(D, F - k0);
-          stage_rows(p, p.act, F, M, k0, kn, t_act, xs, ld);
-          lds_barrier();
-          tile_mma_int4(p.w.wd_q + (size_t)l * D * (F >> 3), p.w.wd_sz + (size_t)l * D * (F >> 7), n0, 16,
-                        F, k0 >> 7, kn >> 7, xs, ld, M, acc);
-          lds_barrier();
-        }
+      const uint32_t* const d_q = p.w.wd_q + (size_t)l * D * (F >> 3);
+      const uint32_t* const d_sz = p.w.wd_sz + (size_t)l * D * (F >> 7);
+      // work items (tile, K block of D) in order; the next item's weights load ahead
+      const int nkb = (F + D - 1) / D, nit = ((D / 16 - wg + G - 1) / G) * nkb;
+      auto load_item = [&](int it, TileW& w) {
+        const int k0 = (it % nkb) * D;
+        tile_load(d_q, d_sz, (wg + (it / nkb) * G) * 16, 16, F, k0 >> 7, min(D, F - k0) >> 7, w);
+      };
+      TileW tw;
+      load_item(0, tw);
+      fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int it = 0; it < nit; ++it) {
+        const int kb = it % nkb, k0 = kb * D, kn = min(D, F - k0);
+        const int n0 = (wg + (it / nkb) * G) * 16;
+        if (kb == 0) acc = fl_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        stage_rows(p, p.act, F, M, k0, kn, t_act, xs, ld);
+        lds_barrier();
+        if (it == 0) stamp(p, p5slot);
+        const TileW cur = tw;
+        if (it + 1 < nit) load_item(it + 1, tw);
+        tile_mma(cur, kn >> 7, xs, ld, M, acc);
+        lds_barrier();
+        if (kb != nkb - 1) continue;
         tile_publish(part, acc);
         if (tid < 256) {
           const int m = tid >> 4, n = tid & 15;
@@ -1661,6 +1748,8 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
         lds_barrier();
       }
     }
+    if (wg >= D / 16) stamp(p, p5slot);
+    stamp(p, p5slot);
   }
 
   // ---------------- final norm + tied bf16 LM head + per-token argmax ----------------
@@ -1669,8 +1758,9 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
   if (wg < ntile || (p.feat && wg == 0)) {
     stage_rows(p, p.h, D, M, 0, D, tag_of(p.epoch + 5u * (uint32_t)p.NL - 1u), xs, ld);
     lds_barrier();
-    norm_rows(xs, ld, M, D, p.w.final_norm, p.eps);
+    norm_rows(xs, ld, M, D, p.w.final_norm, p.eps, part);
     lds_barrier();
+    stamp(p, slot);
     if (p.feat && wg == 0)
       for (int i = tid; i < M * D; i += NT) p.feat[i] = xs[(i / D) * ld + (i % D)];
     const int lane = tid & 63, wave = tid >> 6, r = lane & 15, c = lane >> 4;
@@ -1709,7 +1799,10 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
       }
       lds_barrier();
     }
+  } else {
+    stamp(p, slot);
   }
+  stamp(p, slot);
   // per-token argmax: the 16 threads of a token row are lanes 16k..16k+15 of one wave
   if (tid < 256) {
 #pragma unroll
@@ -2097,6 +2190,8 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
   p.tokens_out = tokens_out;
   p.logits = logits;
   p.feat = feat;
+  p.prof = st->prof;
+  p.prof_slots = st->prof_slots;
   void* args[] = {&p};
   const unsigned lds = (unsigned)verify_lds_bytes(m, st->d.dim);
   const hipError_t e =
