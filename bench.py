@@ -181,6 +181,27 @@ def spec_loop(model, args, prompt, ref, n, rounds=40):
     return res
 
 
+def sampling_latency(args, dev, reps=50):
+    """fl_sample on one logit row of the model's vocabulary (temperature 0.8, top_k 200, Philox
+    noise), events around `reps` back-to-back launches, beside the same with top_k off."""
+    from flint_amd.generate import sample
+    g = torch.Generator(device=dev).manual_seed(5)
+    lg = torch.randn(args.vocab_size, device=dev, generator=g).to(torch.bfloat16).float() * 2
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    res = {}
+    for name, k in (("top_k_200_us", 200), ("no_top_k_us", None)):
+        for i in range(3):
+            sample(lg, 0.8, k, seed=1, offset=i)
+        torch.cuda.synchronize()
+        e0.record()
+        for i in range(reps):
+            sample(lg, 0.8, k, seed=1, offset=i)
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = round(e0.elapsed_time(e1) * 1000.0 / reps, 1)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -265,6 +286,9 @@ def main():
                 f"per pass, {r['ms_per_pass']} ms per pass (full acceptance {r['full_acceptance']} "
                 f"after {r['reseeds']} re-seeds)")
 
+    sampling = sampling_latency(args, dev)
+    log(f"fl_sample over {args.vocab_size} logits: {sampling}")
+
     if a.copy_probe_mb > 0:
         n = a.copy_probe_mb * (1 << 20)
         src = torch.ones(n, dtype=torch.uint8, device=dev)
@@ -306,6 +330,7 @@ def main():
         "cpu_baseline": cpu,
         "verify": verify,
         "spec": spec,
+        "sampling": sampling,
     }
     print(json.dumps(out), flush=True)
 

@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libflint_amd.so")
 OBJDIR = os.path.join(HERE, "_build")
-SOURCES = ["fl_quant.hip", "fl_decode.hip"]
+SOURCES = ["fl_quant.hip", "fl_decode.hip", "fl_sample.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 

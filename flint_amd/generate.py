@@ -41,13 +41,46 @@ def prefill(model, x, input_pos, chunk=16):
     return out
 
 
-def decode_one_token(model, x, input_pos, logits=None):
-    """(next_token int32 device [1], logits) for one token at input_pos (greedy)."""
+def sample(logits, temperature=1.0, top_k=None, seed=0, offset=0, noise=None, probs=False):
+    """Sample one token per logit row on the GPU (reference engine/generate.py:36-55:
+    logits_to_probs + multinomial_sample_one_no_sync). logits: fp32 device [V] or [rows, V]
+    (bf16 values, as the decode and verify kernels write them). The exponential noise comes from
+    Philox4x32-10 keyed by `seed` at counter (index, row, offset), or from `noise` (same shape as
+    logits). Returns (tokens int32 device [rows], probs fp32 [rows, V] or None)."""
+    from . import _lib
+    lg = logits.float().contiguous()
+    rows, vocab = (1, lg.numel()) if lg.dim() == 1 else (lg.shape[0], lg.shape[-1])
+    if top_k is not None and int(top_k) < 1:
+        raise ValueError("top_k must be >= 1")
+    out = torch.empty(rows, dtype=torch.int32, device=lg.device)
+    pr = torch.empty(rows, vocab, dtype=torch.float32, device=lg.device) if probs else None
+    nz = None if noise is None else noise.float().contiguous()
+    if nz is not None and nz.numel() != lg.numel():
+        raise ValueError("noise must have the logits' shape")
+    _lib.call("fl_sample", _lib.ptr(lg), rows, vocab, float(temperature), int(top_k or 0),
+              int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1), _lib.ptr(nz), _lib.ptr(out),
+              _lib.ptr(pr), _lib.stream_ptr())
+    return out, pr
+
+
+def logits_to_probs(logits, temperature=1.0, top_k=None):
+    """Reference generate.py:41-49 on the GPU: probs fp32 device (bf16 values), logits' shape."""
+    _, pr = sample(logits, temperature, top_k, probs=True)
+    return pr.view(logits.shape)
+
+
+def decode_one_token(model, x, input_pos, logits=None, temperature=None, top_k=None, seed=0):
+    """(next_token int32 device [1], logits) for one token at input_pos: greedy, or sampled when
+    temperature or top_k is given (reference generate.py:62-66, sample at :52-55), with the
+    position as the noise counter."""
     pos = int(input_pos.reshape(-1)[0]) if torch.is_tensor(input_pos) else int(input_pos)
     if logits is None:
         logits = torch.empty(model.config.vocab_size, dtype=torch.float32, device=model.device)
     out = torch.empty(1, dtype=torch.int32, device=model.device)
     model.decode_step(x.reshape(-1)[:1].to(torch.int32), pos, token_out=out, logits=logits)
+    if temperature is not None or top_k is not None:
+        t = 1.0 if temperature is None else temperature
+        out, _ = sample(logits, t, top_k, seed=seed, offset=pos)
     return out, logits
 
 
@@ -66,8 +99,11 @@ def decode_n_tokens(model, cur_token, input_pos, num_new_tokens, out=None):
 
 
 @torch.no_grad()
-def generate(model, prompt, max_new_tokens):
-    """Greedy generate: returns int32 device [T + max_new_tokens] = prompt + new tokens."""
+def generate(model, prompt, max_new_tokens, temperature=None, top_k=None, seed=0):
+    """Generate: returns int32 device [T + max_new_tokens] = prompt + new tokens. Greedy (the
+    argmax fused into the decode kernel) unless temperature or top_k is given; then each step's
+    logits go through fl_sample with the step's position as the noise counter. Tokens stay on
+    the device either way (no host synchronisation in the loop)."""
     prompt = prompt.reshape(-1).to(device=model.device, dtype=torch.int32)
     T = prompt.numel()
     model.setup_caches(1, T + max_new_tokens)
@@ -75,7 +111,13 @@ def generate(model, prompt, max_new_tokens):
     seq[:T] = prompt
     if T > 1:
         prefill(model, prompt[:-1], 0)
+    sampled = temperature is not None or top_k is not None
+    logits = torch.empty(model.config.vocab_size, dtype=torch.float32, device=model.device) if sampled else None
     # the last prompt token produces the first new token
     for i in range(max_new_tokens):
-        model.decode_step(seq[T - 1 + i:T + i], T - 1 + i, token_out=seq[T + i:T + i + 1])
+        p = T - 1 + i
+        model.decode_step(seq[p:p + 1], p, token_out=seq[p + 1:p + 2], logits=logits)
+        if sampled:
+            tok, _ = sample(logits, 1.0 if temperature is None else temperature, top_k, seed=seed, offset=p)
+            seq[p + 1:p + 2] = tok
     return seq

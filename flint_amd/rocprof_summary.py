@@ -1,6 +1,6 @@
 """Condense rocprofv3 CSV output into the short text kept under profiles/.
 
-    python -m flint_amd.rocprof_summary <dir> [--kernel k_decode] [--last N]
+    python -m flint_amd.rocprof_summary <dir> [--kernel k_decode] [--last N] [--skip-last S]
         from `rocprofv3 --kernel-trace --stats -f csv`: the per-kernel stats table and, for the
         named kernel, the average duration of its last N dispatches (the timed window of a
         bench run, whose earlier dispatches are prefill / warmup at other context lengths);
@@ -28,7 +28,7 @@ def _short(name, width=60):
     return name if len(name) <= width else name[: width - 3] + "..."
 
 
-def summarise(d, kernel="k_decode", last=0, top=8):
+def summarise(d, kernel="k_decode", last=0, top=8, skip_last=0):
     out = []
     stats = _find(d, "kernel_stats.csv")
     with open(stats) as f:
@@ -44,6 +44,8 @@ def summarise(d, kernel="k_decode", last=0, top=8):
     with open(trace) as f:
         disp = [r for r in csv.DictReader(f) if kernel in r["Kernel_Name"]]
     disp.sort(key=lambda r: int(r["Start_Timestamp"]))
+    if skip_last:  # leave out the last skip_last dispatches (a later window of the same kernel)
+        disp = disp[:-skip_last]
     durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in disp]
     if durs:
         win = durs[-last:] if last else durs
@@ -101,6 +103,7 @@ def main(argv=None):
     ap.add_argument("dir", nargs="*")
     ap.add_argument("--kernel", default="k_decode")
     ap.add_argument("--last", type=int, default=0)
+    ap.add_argument("--skip-last", type=int, default=0)
     ap.add_argument("--traffic", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0)
     ap.add_argument("--config", default="")
@@ -108,7 +111,7 @@ def main(argv=None):
     if a.traffic:
         print(traffic(a.dir[0], a.dir[1], a.kernel, a.last, a.copy_bytes, a.config))
     else:
-        print(summarise(a.dir[0], a.kernel, a.last))
+        print(summarise(a.dir[0], a.kernel, a.last, skip_last=a.skip_last))
 
 
 if __name__ == "__main__":

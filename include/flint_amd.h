@@ -146,6 +146,19 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
  * Replaces the reference's per-step index copies spec_tree.py:124-127. */
 int fl_kv_move(fl_state* st, const int32_t* src, const int32_t* dst, int32_t n, void* stream);
 
+/* Temperature / top-k sampling of `rows` logit rows [rows, vocab] (fp32 holding bf16 values, as
+ * fl_decode_step / fl_verify write them), vocab <= 65536, one token per row into tokens_out:
+ * x = bf16(logit / max(temperature, 1e-5)); with 0 < top_k < vocab every x below the top_k-th
+ * largest is dropped (ties with it stay); p = bf16(softmax(x)); the token is the first index of
+ * the largest bf16(p / q). q is noise[rows, vocab] when given, else bf16(-log u) with u from
+ * Philox4x32-10, key = seed, counter = (index, row, offset low, offset high). probs_out
+ * [rows, vocab] (optional) receives p. top_k = 0 means no top-k.
+ * Replaces reference engine/generate.py:36-55 (multinomial_sample_one_no_sync, logits_to_probs,
+ * sample). */
+int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperature, int32_t top_k,
+              uint64_t seed, uint64_t offset, const float* noise, int32_t* tokens_out,
+              float* probs_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
