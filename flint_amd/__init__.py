@@ -3,6 +3,7 @@
 Modules: _lib (ctypes C-ABI binding), quantize (int4 quantise / dequantise / GEMV, gpt-fast's
 WeightOnlyInt4Linear), synth (ModelArgs + seeded synthetic weights), model (packed model +
 Transformer handle), generate (prefill / decode_one_token / decode_n_tokens / generate),
-spec (speculative verify host loop).
+spec (speculative chain / tree loops over verify, KV compaction), checkpoint (HF / gpt-fast /
+packed int4 files on disk).
 """
 __version__ = "0.1.0"

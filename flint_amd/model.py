@@ -65,6 +65,29 @@ class PackedModel:
         self.embed = sd["embed"].to(**bf).contiguous()
         self.rope = freqs_cis_table(args.block_size, args.head_dim, args.rope_base).to(self.device).contiguous()
 
+    @classmethod
+    def from_tensors(cls, args: ModelArgs, t, device="cuda"):
+        """A packed model from already-quantised tensors in this layout (flint_amd.checkpoint's
+        packed file); shapes are checked against args."""
+        self = object.__new__(cls)
+        self.args = args
+        self.device = torch.device(device)
+        L, D, F, N = args.n_layer, args.dim, args.intermediate_size, args.qkv_dim
+        want = {"wqkv_q": (L, N, D // 8), "wqkv_sz": (L, N, D // 128), "wo_q": (L, D, D // 8),
+                "wo_sz": (L, D, D // 128), "wgu_q": (L, 2 * F, D // 8), "wgu_sz": (L, 2 * F, D // 128),
+                "wd_q": (L, D, F // 8), "wd_sz": (L, D, F // 128), "attn_norm": (L, D), "ffn_norm": (L, D),
+                "final_norm": (D,), "embed": (args.vocab_size, D)}
+        for name, shp in want.items():
+            x = t[name]
+            if tuple(x.shape) != shp:
+                raise ValueError(f"{name}: shape {tuple(x.shape)}, the model arguments need {shp}")
+            dt = torch.int32 if name.endswith(("_q", "_sz")) else torch.bfloat16
+            if x.dtype != dt:
+                raise ValueError(f"{name}: dtype {x.dtype}, expected {dt}")
+            setattr(self, name, x.to(self.device).contiguous())
+        self.rope = freqs_cis_table(args.block_size, args.head_dim, args.rope_base).to(self.device).contiguous()
+        return self
+
     def nbytes_int4(self):
         return sum(t.numel() * 4 for t in (self.wqkv_q, self.wo_q, self.wgu_q, self.wd_q,
                                            self.wqkv_sz, self.wo_sz, self.wgu_sz, self.wd_sz))
