@@ -1,19 +1,22 @@
 // Temperature / top-k sampling of logit rows on the GPU (reference engine/generate.py:36-55).
 //
-// One workgroup per row keeps the row in LDS as bf16 (up to 65536 values, 128 KB) and applies
-// the reference's steps with its bf16 rounding points: x = bf16(l / max(T, 1e-5)); the
-// top-k pivot is the k-th largest x, found by a two-pass radix select over the 16-bit ordered
-// keys of the bf16 values (256-bin LDS histograms); x < pivot drops out; p = bf16(exp(x - max)
-// / sum); q = bf16(-log(u)) with u from Philox4x32-10 keyed by the caller's seed, or q given;
-// the sample is the first index of the largest bf16(p / q), which is
-// multinomial_sample_one_no_sync's argmax(probs / exponential noise).
+// Each row is split over SP_C chunks, one workgroup each, in one cooperative launch; grid-wide
+// syncs separate the steps that need the whole row. The reference's steps with its bf16 rounding
+// points: x = bf16(l / max(T, 1e-5)); the top-k pivot is the k-th largest x, found by a two-pass
+// radix select over the 16-bit ordered keys of the bf16 values (each chunk's 256-bin histogram
+// of the high byte, summed over the row in a fixed order, then the low byte within the selected
+// bin); x < pivot drops out; p = bf16(exp(x - max) / sum), the sum of the chunks' partial sums in
+// chunk order; q = bf16(-log(u)) with u from Philox4x32-10 keyed by the caller's seed, or q
+// given; the sample is the first index of the largest bf16(p / q), which is
+// multinomial_sample_one_no_sync's argmax(probs / exponential noise): 64-bit atomicMax of
+// (ratio, ~index) per row, read out by the row's last chunk to finish.
+#include <hip/hip_cooperative_groups.h>
+#include <algorithm>
 #include "fl_common.h"
 
 namespace {
 
-constexpr int SAMPLE_NT = 1024;
-constexpr int SAMPLE_MAXV = 65536;            // vocab limit: the row lives in LDS as bf16
-constexpr int SAMPLE_NWAVE = SAMPLE_NT / FL_WAVE;
+constexpr int SAMPLE_MAXV = 65536;            // vocab limit
 
 // Philox4x32-10 (Salmon et al., SC 2011): 10 rounds of two 32x32->64 multiplies, Weyl key bumps
 __device__ __forceinline__ uint32_t philox_x0(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
@@ -38,43 +41,6 @@ __device__ __forceinline__ uint32_t philox_x0(uint32_t c0, uint32_t c1, uint32_t
 __device__ __forceinline__ uint32_t bf_key(float x) {
   const uint32_t b = __float_as_uint(x) >> 16;
   return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
-}
-
-__device__ __forceinline__ float block_max(float v, float* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  v = red[0];
-  for (int w = 1; w < SAMPLE_NWAVE; ++w) v = fmaxf(v, red[w]);
-  return v;
-}
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  v = 0.0f;
-  for (int w = 0; w < SAMPLE_NWAVE; ++w) v += red[w];
-  return v;
-}
-__device__ __forceinline__ unsigned long long block_umax(unsigned long long v, unsigned long long* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const unsigned long long w = (unsigned long long)__shfl_xor((long long)v, o, 64);
-    v = w > v ? w : v;
-  }
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  v = red[0];
-  for (int w = 1; w < SAMPLE_NWAVE; ++w) v = red[w] > v ? red[w] : v;
-  return v;
 }
 
 // The bin of a 256-bin histogram (counts in hist) that holds the k-th largest key, scanning from
@@ -115,97 +81,199 @@ __device__ __forceinline__ int select_bin(const int* hist, int k, int* above, in
   return bin;
 }
 
-// LDS: the row as bf16 (vocab values, padded to 16 bytes), then the per-wave histograms
-inline size_t sample_lds_bytes(int V) { return (((size_t)V * 2 + 15) & ~(size_t)15) + SAMPLE_NWAVE * 256 * 4; }
+constexpr int SP_NT = 256;                     // threads per chunk workgroup
+constexpr int SP_C = 64;                       // chunks per row (at most)
+constexpr int SP_PT = 4;                       // values per thread: chunk <= 1024, vocab <= 65536
+constexpr int SP_NWAVE = SP_NT / FL_WAVE;
 
-__global__ __launch_bounds__(SAMPLE_NT) void k_sample(const float* __restrict__ logits, int V,
-                                                      float tdiv, int top_k, uint32_t seed_lo,
-                                                      uint32_t seed_hi, uint32_t off_lo,
-                                                      uint32_t off_hi, const float* __restrict__ noise,
-                                                      int32_t* __restrict__ tokens_out,
-                                                      float* __restrict__ probs_out) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-  int* whist = reinterpret_cast<int*>(smem + (((size_t)V * 2 + 15) & ~(size_t)15));
+// per-row scratch of the cooperative sampler (device memory owned by the library)
+struct SampleWs {
+  int hist[SP_C][2][256];                      // per chunk: high-byte, low-byte key histograms
+  float mx[SP_C], ps[SP_C];                    // per chunk: max x, partial sum of exp(x - max)
+  unsigned long long best;                     // (ratio bits, ~index), atomicMax
+  unsigned int arrived;                        // chunks done (the last one reads best out)
+};
+
+// scratch words written before a grid sync and read after it by other workgroups (possibly on
+// other XCDs): device-coherent accesses
+__device__ __forceinline__ void st_ws(unsigned* a, unsigned v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_ws(float* a, unsigned v) { st_ws(reinterpret_cast<unsigned*>(a), v); }
+__device__ __forceinline__ unsigned ld_ws(unsigned* a) {
+  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float wg_max(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  v = red[0];
+  for (int w = 1; w < SP_NWAVE; ++w) v = fmaxf(v, red[w]);
+  return v;
+}
+__device__ __forceinline__ float wg_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  v = 0.0f;
+  for (int w = 0; w < SP_NWAVE; ++w) v += red[w];
+  return v;
+}
+__device__ __forceinline__ unsigned long long wg_umax(unsigned long long v, unsigned long long* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long w = (unsigned long long)__shfl_xor((long long)v, o, 64);
+    v = w > v ? w : v;
+  }
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  v = red[0];
+  for (int w = 1; w < SP_NWAVE; ++w) v = red[w] > v ? red[w] : v;
+  return v;
+}
+
+__global__ __launch_bounds__(SP_NT) void k_sample(const float* __restrict__ logits, int V, int C, int row0,
+                                                  float tdiv, int top_k, uint32_t seed_lo,
+                                                  uint32_t seed_hi, uint32_t off_lo, uint32_t off_hi,
+                                                  const float* __restrict__ noise,
+                                                  int32_t* __restrict__ tokens_out,
+                                                  float* __restrict__ probs_out, SampleWs* __restrict__ wsa) {
+  namespace cg = cooperative_groups;
+  cg::grid_group grid = cg::this_grid();
   __shared__ int hist[256];
   __shared__ int sel[2];
-  __shared__ float red[SAMPLE_NWAVE];
-  __shared__ unsigned long long ured[SAMPLE_NWAVE];
-  const int tid = threadIdx.x, row = blockIdx.x;
+  __shared__ float red[SP_NWAVE];
+  __shared__ unsigned long long ured[SP_NWAVE];
+  __shared__ bool last;
+  const int tid = threadIdx.x, row = blockIdx.x / C, c = blockIdx.x % C;
+  const int CH = (V + C - 1) / C, j0 = c * CH, j1 = min(V, j0 + CH);
+  SampleWs* ws = wsa + row;
   const float* lg = logits + (size_t)row * V;
-  // x = bf16(bf16(logit) / max(T, 1e-5))  (generate.py:42)
-  for (int j = tid; j < V; j += SAMPLE_NT) xs[j] = (uint16_t)f2bf(rbf(lg[j]) / tdiv);
-  __syncthreads();
-  // top-k pivot (generate.py:44-47): keys >= the k-th largest key stay. Each wave counts into
-  // its own histogram (the keys of a row crowd into a few bins), the 16 are summed, and the bin
-  // holding the k-th largest key is selected: first over the high byte, then over the low byte
-  // of the keys in that bin.
+  float x[SP_PT];
+  // x = bf16(bf16(logit) / max(T, 1e-5))  (generate.py:42); max over the chunk
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < SP_PT; ++e) {
+    const int j = j0 + tid + e * SP_NT;
+    x[e] = j < j1 ? rbf(rbf(lg[j]) / tdiv) : -INFINITY;
+    mx = fmaxf(mx, x[e]);
+  }
+  mx = wg_max(mx, red);
+  if (tid == 0) st_ws(&ws->mx[c], __float_as_uint(mx));
+  // top-k pivot (generate.py:44-47): keys >= the k-th largest key stay
   uint32_t pivot = 0;
-  if (top_k > 0 && top_k < V) {
+  const bool topk = top_k > 0 && top_k < V;
+  if (topk) {
     int k = top_k;
-    auto count = [&](bool low) {
-      for (int b = tid; b < SAMPLE_NWAVE * 256; b += SAMPLE_NT) whist[b] = 0;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      hist[tid] = 0;  // SP_NT == 256 bins
       __syncthreads();
-      int* h = whist + (tid >> 6) * 256;
-      for (int j = tid; j < V; j += SAMPLE_NT) {
-        const uint32_t key = bf_key(bf2f(xs[j]));
-        if (!low || (key >> 8) == (pivot >> 8)) atomicAdd(&h[low ? (key & 0xFFu) : (key >> 8)], 1);
+#pragma unroll
+      for (int e = 0; e < SP_PT; ++e) {
+        const uint32_t key = bf_key(x[e]);
+        const bool in = (j0 + tid + e * SP_NT < j1) & (pass == 0 || (key >> 8) == (pivot >> 8));
+        if (in) atomicAdd(&hist[pass == 0 ? (key >> 8) : (key & 0xFFu)], 1);
       }
       __syncthreads();
-      if (tid < 256) {
-        int c = 0;
-        for (int w = 0; w < SAMPLE_NWAVE; ++w) c += whist[w * 256 + tid];
-        hist[tid] = c;
+      st_ws(reinterpret_cast<unsigned*>(&ws->hist[c][pass][tid]), (unsigned)hist[tid]);
+      grid.sync();
+      // the row's counts: thread t sums bins 4(t % 64) .. +3 over chunks t / 64, t / 64 + 4, ...
+      // (16-byte coherent loads, all issued before any is used), then the 4 partial sums meet in LDS
+      const auto hr = buf_rsrc(&ws->hist[0][0][0], (uint32_t)sizeof(ws->hist));
+      uint4 hv[SP_C / 4];
+#pragma unroll
+      for (int i = 0; i < SP_C / 4; ++i) {
+        const int cc = (tid >> 6) + 4 * i;
+        hv[i] = buf_ld128_coh(hr, cc < C ? (uint32_t)(((cc * 2 + pass) * 256 + 4 * (tid & 63)) * 4) : 0xFFFFFFF0u);
       }
+      uint4 acc = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int i = 0; i < SP_C / 4; ++i) {
+        acc.x += hv[i].x;
+        acc.y += hv[i].y;
+        acc.z += hv[i].z;
+        acc.w += hv[i].w;
+      }
+      __syncthreads();
+      hist[tid] = 0;
+      __syncthreads();
+      atomicAdd(&hist[4 * (tid & 63)], (int)acc.x);
+      atomicAdd(&hist[4 * (tid & 63) + 1], (int)acc.y);
+      atomicAdd(&hist[4 * (tid & 63) + 2], (int)acc.z);
+      atomicAdd(&hist[4 * (tid & 63) + 3], (int)acc.w);
       __syncthreads();
       int above = 0;
       const int bin = select_bin(hist, k, &above, sel);
       k -= above;
+      pivot = pass == 0 ? ((uint32_t)bin << 8) : (pivot | (uint32_t)bin);
       __syncthreads();
-      return bin;
-    };
-    pivot = (uint32_t)count(false) << 8;
-    pivot |= (uint32_t)count(true);
-  }
-  float mx = -INFINITY;
-  for (int j = tid; j < V; j += SAMPLE_NT) {  // drop x < pivot (bf16 -inf is 0xFF80)
-    float x = bf2f(xs[j]);
-    if (bf_key(x) < pivot) {
-      xs[j] = 0xFF80u;
-      x = -INFINITY;
     }
-    mx = fmaxf(mx, x);
+  } else {
+    grid.sync();
   }
-  mx = block_max(mx, red);
-  // softmax (generate.py:48): p = bf16(exp(x - max) / sum); exp is evaluated again below
-  auto ex = [&](int j) {
-    const float v = bf2f(xs[j]);
-    return v == -INFINITY ? 0.0f : expf(v - mx);
-  };
+  // the row's max (kept entries include it), then the partial sum of exp(x - max) over kept x
+  // chunk cc's value is loaded by thread cc (one round trip), then reduced over the workgroup
+  float gmx = tid < C ? __uint_as_float(ld_ws(reinterpret_cast<unsigned*>(&ws->mx[tid]))) : -INFINITY;
+  gmx = wg_max(gmx, red);
   float s = 0.0f;
-  for (int j = tid; j < V; j += SAMPLE_NT) s += ex(j);
-  s = block_sum(s, red);
-  // argmax(bf16(p / q)), the first index among equal ratios (generate.py:36-38)
-  unsigned long long best = 0ull;
-  for (int j = tid; j < V; j += SAMPLE_NT) {
-    const float p = rbf(ex(j) / s);
-    if (probs_out) probs_out[(size_t)row * V + j] = p;
-    if (p == 0.0f) continue;  // ratio 0 never beats the kept maximum's (p > 0): no noise needed
-    float q;
-    if (noise) {
-      q = rbf(noise[(size_t)row * V + j]);
-    } else {
-      const uint32_t r = philox_x0((uint32_t)j, (uint32_t)row, off_lo, off_hi, seed_lo, seed_hi);
-      const double u = ((double)(r >> 8) + 0.5) * (1.0 / 16777216.0);
-      q = rbf((float)(-log(u)));
-    }
-    const float ratio = rbf(p / q);
-    const unsigned long long key =
-        ((unsigned long long)__float_as_uint(ratio) << 32) | (0xFFFFFFFFu - (uint32_t)j);
-    best = key > best ? key : best;
+#pragma unroll
+  for (int e = 0; e < SP_PT; ++e) {
+    if (bf_key(x[e]) < pivot) x[e] = -INFINITY;
+    x[e] = x[e] == -INFINITY ? 0.0f : expf(x[e] - gmx);  // from here x holds exp(x - max)
+    s += x[e];
   }
-  best = block_umax(best, ured);
-  if (tid == 0) tokens_out[row] = (int32_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+  s = wg_sum(s, red);
+  if (tid == 0) st_ws(reinterpret_cast<unsigned*>(&ws->ps[c]), __float_as_uint(s));
+  grid.sync();
+  s = tid < C ? __uint_as_float(ld_ws(reinterpret_cast<unsigned*>(&ws->ps[tid]))) : 0.0f;
+  s = wg_sum(s, red);  // a fixed reduction tree: the same sum in every chunk
+  // p = bf16(exp(x - max) / sum); argmax(bf16(p / q)), the first index among equal ratios
+  unsigned long long best = 0ull;
+#pragma unroll
+  for (int e = 0; e < SP_PT; ++e) {
+    const int j = j0 + tid + e * SP_NT;
+    if (j < j1) {
+      const float p = rbf(x[e] / s);
+      if (probs_out) probs_out[(size_t)row * V + j] = p;
+      if (p != 0.0f) {  // ratio 0 never beats the kept maximum's (p > 0): no noise needed
+        float q;
+        if (noise) {
+          q = rbf(noise[(size_t)row * V + j]);
+        } else {
+          const uint32_t r = philox_x0((uint32_t)j, (uint32_t)(row0 + row), off_lo, off_hi, seed_lo, seed_hi);
+          const double u = ((double)(r >> 8) + 0.5) * (1.0 / 16777216.0);
+          q = rbf((float)(-log(u)));
+        }
+        const float ratio = rbf(p / q);
+        const unsigned long long key =
+            ((unsigned long long)__float_as_uint(ratio) << 32) | (0xFFFFFFFFu - (uint32_t)j);
+        best = key > best ? key : best;
+      }
+    }
+  }
+  best = wg_umax(best, ured);
+  if (tid == 0) {
+    if (best) __hip_atomic_fetch_max(&ws->best, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned prev = __hip_atomic_fetch_add(&ws->arrived, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == (unsigned)(C - 1);
+  }
+  __syncthreads();
+  if (last && tid == 0) {  // every chunk's atomicMax precedes its arrival: read out, reset for the next call
+    const unsigned long long b =
+        __hip_atomic_exchange(&ws->best, 0ull, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    tokens_out[row] = (int32_t)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull));
+    __hip_atomic_store(&ws->arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 }  // namespace
@@ -215,24 +283,41 @@ extern "C" {
 int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperature, int32_t top_k,
               uint64_t seed, uint64_t offset, const float* noise, int32_t* tokens_out,
               float* probs_out, void* stream) {
-  if (!logits || !tokens_out || rows < 1 || vocab < 1 || vocab > SAMPLE_MAXV || top_k < 0)
+  if (!logits || !tokens_out || rows < 1 || vocab < 1 || vocab > SAMPLE_MAXV ||
+      top_k < 0)
     return FL_E_ARG;
   if (!(temperature == temperature)) return FL_E_ARG;  // NaN
   const float tdiv = temperature > 1e-5f ? temperature : 1e-5f;
-  const size_t lds = sample_lds_bytes(vocab);
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return FL_E_HIP;
-  static unsigned long long lds_set = 0;  // devices whose LDS limit for k_sample is raised
-  if (dev < 64 && !(lds_set & (1ull << dev))) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_sample), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sample_lds_bytes(SAMPLE_MAXV)) != hipSuccess)
-      return FL_E_HIP;
-    lds_set |= 1ull << dev;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FL_E_HIP;
+  // per-device scratch, allocated (and zeroed) on the first call on that device and kept until
+  // the process ends; calls on one device must be stream-ordered
+  static SampleWs* ws[64] = {};
+  if (!ws[dev]) {
+    SampleWs* w = nullptr;
+    if (hipMalloc(&w, sizeof(SampleWs) * FL_MAX_VERIFY) != hipSuccess) return FL_E_HIP;
+    if (hipMemset(w, 0, sizeof(SampleWs) * FL_MAX_VERIFY) != hipSuccess) return FL_E_HIP;
+    ws[dev] = w;
   }
-  hipLaunchKernelGGL(k_sample, dim3(rows), dim3(SAMPLE_NT), lds, reinterpret_cast<hipStream_t>(stream),
-                     logits, vocab, tdiv, top_k, (uint32_t)seed, (uint32_t)(seed >> 32), (uint32_t)offset,
-                     (uint32_t)(offset >> 32), noise, tokens_out, probs_out);
-  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+  const int C = std::min(SP_C, std::max(1, (vocab + SP_NT - 1) / SP_NT));  // chunks of <= SP_PT * SP_NT
+  if ((vocab + C - 1) / C > SP_PT * SP_NT) return FL_E_ARG;
+  int v = vocab, ci = C, tk = top_k;
+  uint32_t slo = (uint32_t)seed, shi = (uint32_t)(seed >> 32), olo = (uint32_t)offset, ohi = (uint32_t)(offset >> 32);
+  float td = tdiv;
+  SampleWs* wsp = ws[dev];
+  for (int r0 = 0; r0 < rows; r0 += FL_MAX_VERIFY) {  // FL_MAX_VERIFY rows per launch (the scratch's rows)
+    const int n = std::min(FL_MAX_VERIFY, rows - r0);
+    const float* lg = logits + (size_t)r0 * vocab;
+    const float* nz = noise ? noise + (size_t)r0 * vocab : nullptr;
+    int32_t* to = tokens_out + r0;
+    float* po = probs_out ? probs_out + (size_t)r0 * vocab : nullptr;
+    int rb = r0;
+    void* args[] = {(void*)&lg, &v, &ci, &rb, &td, &tk, &slo, &shi, &olo, &ohi, (void*)&nz, &to, &po, &wsp};
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_sample), dim3(n * C),
+                                                    dim3(SP_NT), args, 0, reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return FL_E_LAUNCH;
+  }
+  return FL_OK;
 }
 
 }  // extern "C"

@@ -152,7 +152,9 @@ int fl_kv_move(fl_state* st, const int32_t* src, const int32_t* dst, int32_t n, 
  * largest is dropped (ties with it stay); p = bf16(softmax(x)); the token is the first index of
  * the largest bf16(p / q). q is noise[rows, vocab] when given, else bf16(-log u) with u from
  * Philox4x32-10, key = seed, counter = (index, row, offset low, offset high). probs_out
- * [rows, vocab] (optional) receives p. top_k = 0 means no top-k.
+ * [rows, vocab] (optional) receives p. top_k = 0 means no top-k. Up to FL_MAX_VERIFY rows per
+ * cooperative launch (more rows: several launches); the library keeps one scratch block per device
+ * (allocated on the first call), so calls on one device must be stream-ordered.
  * Replaces reference engine/generate.py:36-55 (multinomial_sample_one_no_sync, logits_to_probs,
  * sample). */
 int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperature, int32_t top_k,
