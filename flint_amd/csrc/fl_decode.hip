@@ -1234,7 +1234,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
 // (bf16) and the unit's mask row [16]
 inline size_t verify_lds_bytes(int M, int D) {
   const size_t xs = ((size_t)(M + 1) * (D + 8) * 2 + 15) & ~(size_t)15;
-  return xs + NWAVE * 256 * 4 + 3 * FL_MAX_VERIFY * 64 * 2 + FL_MAX_VERIFY * FL_MAX_VERIFY;
+  return xs + 4 * NWAVE * 256 * 4 + 3 * FL_MAX_VERIFY * 64 * 2 + FL_MAX_VERIFY * FL_MAX_VERIFY;
 }
 
 // Token rows [M, kn] of a tagged exchange buffer (row stride `stride` words, columns k0 ..
@@ -1381,6 +1381,16 @@ __device__ __forceinline__ void tile_publish(float* part, const fl_f32x4& acc) {
   const int r = lane & 15, c = lane >> 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i) part[wave * 256 + (c * 4 + i) * 16 + r] = acc[i];
+  lds_barrier();
+}
+// four tiles' partials at once: tile i's go to part + i * NWAVE * 256; ends with a barrier
+__device__ __forceinline__ void tile_publish4(float* part, const fl_f32x4 (&acc)[4]) {
+  const int lane = tid_here() & 63, wave = tid_here() >> 6;
+  const int r = lane & 15, c = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[(t * NWAVE + wave) * 256 + (c * 4 + i) * 16 + r] = acc[t][i];
   lds_barrier();
 }
 // sum over the waves (fixed order) of entry t = token * 16 + row
@@ -1551,7 +1561,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
   const int ld = D + 8;
   uint16_t* xs = reinterpret_cast<uint16_t*>(vsm);
   float* part = reinterpret_cast<float*>(vsm + (((size_t)(M + 1) * ld * 2 + 15) & ~(size_t)15));
-  uint16_t* att = reinterpret_cast<uint16_t*>(part + NWAVE * 256);
+  uint16_t* att = reinterpret_cast<uint16_t*>(part + 4 * NWAVE * 256);
   uint8_t* amk = reinterpret_cast<uint8_t*>(att + 3 * FL_MAX_VERIFY * 64);
   for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + M * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
   int slot = 0;  // optional timestamps, same slots as k_decode's
@@ -1681,25 +1691,36 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
     if (wg < (2 * F) / 16) {
       const uint32_t* const gu_q = p.w.wgu_q + (size_t)l * 2 * F * (D >> 3);
       const uint32_t* const gu_sz = p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7);
-      const int nt = ((2 * F) / 16 - wg + G - 1) / G;  // this workgroup's tiles wg, wg+G, ...
-      TileW tw;
-      tile_load(gu_q, gu_sz, wg * 16, 16, D, 0, D >> 7, tw);
+      // this workgroup's tiles wg, wg+G, ... in rounds of up to 4: the round's MFMAs run back to
+      // back into 4 accumulators, one publish and one epilogue per round. The first tile's
+      // weights are requested before the input wait, the rest once the inputs are in (requesting
+      // them after the norm instead was measured slower).
+      const int nt = ((2 * F) / 16 - wg + G - 1) / G;
+      TileW tw[4] = {};
+      tile_load(gu_q, gu_sz, wg * 16, 16, D, 0, D >> 7, tw[0]);
       stage_rows(p, p.h, D, M, 0, D, t_h1, xs, ld);
+#pragma unroll
+      for (int i = 1; i < 4; ++i)
+        if (i < nt) tile_load(gu_q, gu_sz, (wg + i * G) * 16, 16, D, 0, D >> 7, tw[i]);
       lds_barrier();
       norm_rows(xs, ld, M, D, p.w.ffn_norm + (size_t)l * D, p.eps, part);
       lds_barrier();
       stamp(p, slot);
-      for (int t = wg; t < (2 * F) / 16; t += G) {
-        const int n0 = t * 16;
-        const TileW cur = tw;
-        if (t + G < (2 * F) / 16) tile_load(gu_q, gu_sz, (t + G) * 16, 16, D, 0, D >> 7, tw);
-        fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        tile_mma(cur, D >> 7, xs, ld, M, acc);
-        tile_publish(part, acc);
-        if (tid < 128) {
-          const int m = tid >> 3, pp = tid & 7;
-          if (m < M) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
-            const float gg = rbf(tile_sum(part, m * 16 + 2 * pp)), uu = rbf(tile_sum(part, m * 16 + 2 * pp + 1));
+      for (int b4 = 0; b4 < nt; b4 += 4) {
+        fl_f32x4 acc[4] = {};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (b4 + i < nt) tile_mma(tw[i], D >> 7, xs, ld, M, acc[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (b4 + i + 4 < nt) tile_load(gu_q, gu_sz, (wg + (b4 + i + 4) * G) * 16, 16, D, 0, D >> 7, tw[i]);
+        tile_publish4(part, acc);
+        for (int it = tid; it < 4 * 128; it += NT) {
+          const int i = it >> 7, m = (it >> 3) & 15, pp = it & 7;
+          if (b4 + i < nt && m < M) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
+            const float* pt = part + i * NWAVE * 256;
+            const float gg = rbf(tile_sum(pt, m * 16 + 2 * pp)), uu = rbf(tile_sum(pt, m * 16 + 2 * pp + 1));
+            const int n0 = (wg + (b4 + i) * G) * 16;
             st_coh_u32(p.act + (size_t)m * F + (n0 >> 1) + pp, f2bf(rbf(silu_f(gg)) * uu) | (t_act << 16));
           }
         }
