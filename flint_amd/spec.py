@@ -203,6 +203,11 @@ class SpecDecoder:
         h[nv:nv + m] = tree_depths(parents)
         h[2 * nv:].view(np.uint8)[:m * m] = tree_mask(parents).reshape(-1)
         self._dev.copy_(self._host, non_blocking=True)
+        if m == 1:
+            # a lone root is one decode step (same cache slot, RoPE position, argmax and final-norm
+            # feature as a verify of M = 1), and the decode kernel is the faster of the two
+            self.model.decode_step(self._dev[:1], pos, token_out=self._tout[:1], feat=self._feat[0])
+            return self._tout[:1].tolist(), self._feat[:1]
         amask = self._dev[2 * nv:].view(torch.uint8)[:m * m].view(m, m)
         tout, _, feat = self.model.verify(self._dev[:m], pos, depth=self._dev[nv:nv + m], amask=amask,
                                           logits=False, feat=self._feat[:m], tokens_out=self._tout[:m])

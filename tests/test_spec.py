@@ -187,13 +187,14 @@ class _Cfg:
 
 class StandInModel:
     """Implements the Transformer calls the spec loop and generate.prefill make (setup_caches,
-    verify, kv_move) over a cache of (token, rope position) rows."""
+    verify, decode_step, kv_move) over a cache of (token, rope position) rows."""
     device = torch.device("cpu")
     config = _Cfg()
 
     def __init__(self):
         self.slots = []
         self.moves = 0
+        self.decodes = 0
 
     def setup_caches(self, b, s):
         self.slots = [None] * s
@@ -227,6 +228,13 @@ class StandInModel:
             tokens_out[:m] = out
             out = tokens_out
         return out, logits, feat
+
+    def decode_step(self, token, pos, token_out=None, logits=None, feat=None):
+        self.decodes += 1
+        tout, _, _ = self.verify(token.reshape(1), pos, depth=torch.zeros(1, dtype=torch.int32),
+                                 amask=torch.ones(1, 1, dtype=torch.uint8), feat=None if feat is None else feat.view(1, -1),
+                                 tokens_out=token_out)
+        return tout
 
     def kv_move(self, src, dst):
         assert len(src) == len(dst) <= 16
@@ -321,7 +329,8 @@ def test_spec_loop_k0_eos_and_lengths():
     ref = greedy(prompt, 50)
     model = StandInModel()
     out, st = SpecDecoder(model, OracleDraft(prompt, 0), k=0).generate(prompt, 50)
-    assert out == ref and st.passes == 49          # one verify per token after the first
+    assert out == ref and st.passes == 49          # one pass per token after the first
+    assert model.decodes == 50                     # a lone root goes through the decode step
     eos = ref[len(prompt) + 20]
     stop = ref.index(eos, len(prompt))
     for mode in ("chain", "tree"):
