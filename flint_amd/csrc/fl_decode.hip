@@ -1383,6 +1383,38 @@ __device__ __forceinline__ void tile_publish(float* part, const fl_f32x4& acc) {
   for (int i = 0; i < 4; ++i) part[wave * 256 + (c * 4 + i) * 16 + r] = acc[i];
   lds_barrier();
 }
+// One group per wave (group g0 + wave of a 16-row tile, waves past ng idle): the down
+// projection's K parts, whose tiles are all requested at once.
+struct TileW1 {
+  uint4 w;
+  uint32_t s;
+};
+__device__ __forceinline__ void tile_load1(const uint32_t* __restrict__ q, const uint32_t* __restrict__ sz,
+                                           int n0, int K, int g0, int ng, TileW1& tw) {
+  const int lane = tid_here() & 63, wave = tid_here() >> 6;
+  const int r = lane & 15, c = lane >> 4, groups = K >> 7;
+  const auto wr = buf_rsrc(q + (size_t)n0 * (K >> 3), 16u * (uint32_t)(K >> 1));
+  const auto sr = buf_rsrc(sz + (size_t)n0 * groups, 16u * (uint32_t)groups * 4u);
+  const bool in = wave < ng;
+  const uint32_t gg = (uint32_t)(g0 + wave);
+  tw.w = buf_ld128(wr, in ? (uint32_t)r * (uint32_t)(K >> 1) + gg * 64u + (uint32_t)c * 16u : 0xFFFFFFF0u);
+  tw.s = buf_ld32(sr, in ? ((uint32_t)r * (uint32_t)groups + gg) * 4u : 0xFFFFFFF0u);
+}
+__device__ __forceinline__ void tile_mma1(const TileW1& tw, int ng, const uint16_t* xs, int ld, int M,
+                                          fl_f32x4& acc) {
+  const int lane = tid_here() & 63, wave = tid_here() >> 6;
+  const int r = lane & 15, c = lane >> 4;
+  if (wave < ng) {  // wave-uniform
+    const uint16_t* xrow = xs + (r < M ? r : M) * ld + c * 32 + wave * 128;
+    uint4 xa[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xa[e] = *reinterpret_cast<const uint4*>(xrow + e * 8);
+    uint32_t d[4][4];
+    dq32(tw.w, dq_const(tw.s), d);
+    mfma_chunk(d, xa, acc);
+  }
+}
+
 // four tiles' partials at once: tile i's go to part + i * NWAVE * 256; ends with a barrier
 __device__ __forceinline__ void tile_publish4(float* part, const fl_f32x4 (&acc)[4]) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
@@ -1729,47 +1761,78 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
     }
     if (wg >= (2 * F) / 16) stamp(p, slot);
     stamp(p, slot);
-    // ---------------- P5: down projection + residual (K staged in blocks of D) ----------------
+    // ---------------- P5: down projection + residual, K split over workgroups ----------------
+    // The 8192-long K of each 16-row tile is cut into parts of 8 groups (1024 inputs; fewer when
+    // D < 1024, as a part is staged into one xs row), one group per wave. Workgroup w takes part k = w % KP of the tiles w / KP, w / KP + G / KP, ...: it
+    // stages only its part's 1024 inputs, runs one group per wave for each of its tiles (weights
+    // requested before the input wait), and publishes each tile's part sum (fp32, tagged) to
+    // p.part. The tile's owner (workgroup t % G) sums the parts in order and adds the residual.
     int p5slot = slot;
     slot += 2;
-    if (wg < D / 16) {
+    {
       const uint32_t* const d_q = p.w.wd_q + (size_t)l * D * (F >> 3);
       const uint32_t* const d_sz = p.w.wd_sz + (size_t)l * D * (F >> 7);
-      // work items (tile, K block of D) in order; the next item's weights load ahead
-      const int nkb = (F + D - 1) / D, nit = ((D / 16 - wg + G - 1) / G) * nkb;
-      auto load_item = [&](int it, TileW& w) {
-        const int k0 = (it % nkb) * D;
-        tile_load(d_q, d_sz, (wg + (it / nkb) * G) * 16, 16, F, k0 >> 7, min(D, F - k0) >> 7, w);
-      };
-      TileW tw;
-      load_item(0, tw);
-      fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int it = 0; it < nit; ++it) {
-        const int kb = it % nkb, k0 = kb * D, kn = min(D, F - k0);
-        const int n0 = (wg + (it / nkb) * G) * 16;
-        if (kb == 0) acc = fl_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        stage_rows(p, p.act, F, M, k0, kn, t_act, xs, ld);
+      // groups per part: one per wave, and no more than an xs row holds (D inputs)
+      const int ntile = D / 16, ng = F >> 7, GPP = min(NWAVE, D >> 7), KP = (ng + GPP - 1) / GPP, GK = G / KP;
+      const int k = wg % KP, kg0 = k * GPP, kgn = min(GPP, ng - kg0);
+      const int nmine = (wg < GK * KP) ? max(0, (ntile - wg / KP + GK - 1) / GK) : 0;
+      unsigned long long* const dpart = p.part;  // [tile][part][FL_MAX_VERIFY][16]
+      constexpr int TMAX = 8;  // tiles per workgroup whose weights are all requested up front
+      TileW1 tw[TMAX] = {};
+#pragma unroll
+      for (int i = 0; i < TMAX; ++i)
+        if (i < nmine) tile_load1(d_q, d_sz, (wg / KP + i * GK) * 16, F, kg0, kgn, tw[i]);
+      if (nmine > 0) {
+        stage_rows(p, p.act, F, M, kg0 * 128, kgn * 128, t_act, xs, ld);
         lds_barrier();
-        if (it == 0) stamp(p, p5slot);
-        const TileW cur = tw;
-        if (it + 1 < nit) load_item(it + 1, tw);
-        tile_mma(cur, kn >> 7, xs, ld, M, acc);
-        lds_barrier();
-        if (kb != nkb - 1) continue;
-        tile_publish(part, acc);
-        if (tid < 256) {
-          const int m = tid >> 4, n = tid & 15;
-          if (m < M) {
-            const int row = n0 + n;
-            const float hold = bflo(ld_coh_u32(p.h + (size_t)m * D + row));  // written in P3 by this thread
-            const float o = rbf(rbf(tile_sum(part, tid)) * p.resid_mult);
-            st_coh_u32(p.h + (size_t)m * D + row, f2bf(hold + o) | (t_h2 << 16));
+        stamp(p, p5slot);
+      }
+      for (int j0 = 0; j0 < nmine; j0 += 4) {
+        if (j0 >= TMAX) {  // more tiles than prefetched (few workgroups): one round at a time
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (j0 + i < nmine) tile_load1(d_q, d_sz, (wg / KP + (j0 + i) * GK) * 16, F, kg0, kgn, tw[i]);
+        }
+        fl_f32x4 acc[4] = {};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (j0 + i < nmine) {
+            const TileW1& w = j0 >= TMAX ? tw[i] : (j0 == 0 ? tw[i] : tw[4 + i]);
+            tile_mma1(w, kgn, xs, ld, M, acc[i]);
+          }
+        tile_publish4(part, acc);
+        for (int it = tid; it < 4 * 256; it += NT) {
+          const int i = it >> 8, m = (it >> 4) & 15, n = it & 15;
+          if (j0 + i < nmine && m < M) {
+            const int t = wg / KP + (j0 + i) * GK;
+            const float v = tile_sum(part + i * NWAVE * 256, m * 16 + n);
+            st_coh_u64(dpart + (((size_t)t * KP + k) * FL_MAX_VERIFY + m) * 16 + n,
+                       (unsigned long long)__float_as_uint(v) | ((unsigned long long)t_h2 << 32));
           }
         }
         lds_barrier();
       }
+      if (nmine == 0) stamp(p, p5slot);
+      // owner: tile t = wg, wg + G, ...; thread (m, n) sums its row's KP parts in order
+      for (int t = wg; t < ntile; t += G) {
+        if (tid < 16 * M) {
+          const int m = tid >> 4, n = tid & 15, row = t * 16 + n;
+          auto ok = [t_h2](unsigned long long v) { return (uint32_t)(v >> 32) == t_h2; };
+          float sum = 0.0f;
+          for (int kk = 0; kk < KP; ++kk) {
+            const unsigned long long* a = dpart + (((size_t)t * KP + kk) * FL_MAX_VERIFY + m) * 16 + n;
+            unsigned long long v = ld_coh_u64(a);
+            if (!ok(v)) v = spin_until(p, v, ok, [a]() { return ld_coh_u64(a); });
+            sum += __uint_as_float((uint32_t)v);
+          }
+          uint32_t hw = ld_coh_u32(p.h + (size_t)m * D + row);  // h1 of this row (O phase)
+          auto ok1 = [t_h1](uint32_t v) { return (v >> 16) == t_h1; };
+          if (!ok1(hw)) hw = spin_until(p, hw, ok1, [&]() { return ld_coh_u32(p.h + (size_t)m * D + row); });
+          const float o = rbf(rbf(sum) * p.resid_mult);
+          st_coh_u32(p.h + (size_t)m * D + row, f2bf(bflo(hw) + o) | (t_h2 << 16));
+        }
+      }
     }
-    if (wg >= D / 16) stamp(p, p5slot);
     stamp(p, p5slot);
   }
 
@@ -2203,6 +2266,11 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
   if (m < 1 || m > FL_MAX_VERIFY) return FL_E_M;
   if (pos < 0 || pos + m > st->max_seq) return FL_E_POS;
   if (!st->verify_ok) return FL_E_ARG;
+  // the down projection splits K into parts of 8 groups, each needing a workgroup of its own
+  {
+    const int gpp = std::min(NWAVE, st->d.dim >> 7);
+    if (st->vgrid < ((st->d.inter >> 7) + gpp - 1) / gpp) return FL_E_ARG;
+  }
   DecodeParams p = base_params(w, st, pos);
   p.M = m;
   p.tokens = tokens;
