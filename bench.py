@@ -1,12 +1,12 @@
 #!/usr/bin/env python3
-"""Batch-1 int4 greedy decode benchmark on one MI355X.
+"""Batch-1 int4 greedy decode benchmark on one MI355X: prompt 512, then timed greedy decode.
 
 One "step" = one decoded token = ONE persistent cooperative kernel launch (fl_decode_step) over
 the 40-layer 3B-class synthetic int4 model: all layers, final norm, tied bf16 LM head, greedy
 argmax. Tokens chain on the device (step i reads the token step i-1 wrote), so the timed loop
 has no host synchronisation. Weights are seeded random (no checkpoint exists); the prompt is
 512 seeded-uniform token ids prefilled before timing (through the verify kernel, 16 tokens per
-launch). After the timed decode, BASELINE config 4's speculative-verify latency (k = 4, 7 at
+launch). After the timed decode, the speculative-verify latency (k = 4, 7 draft tokens at
 context 1024) is measured beside the decode latency at the same context.
 
 Prints ONE JSON line (the driver's contract) with `roofline` (HBM-bound: algorithmic bytes per
@@ -85,7 +85,7 @@ def cpu_baseline(args, sd, ctx, steps):
 
 
 def verify_latency(model, args, dev, ctx=1024, reps=20):
-    """accept-agnostic latency of one speculative verify pass over M = k+1
+    """Accept-agnostic latency of one speculative verify pass over M = k+1
     tokens (k = 4, 7; chain mask) at context `ctx`, beside the M = 1 decode step latency at the
     same context. The cache prefix is synthetic (random bf16 rows): the timing depends only on
     its length."""
@@ -212,7 +212,7 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true",
-                    help="skip the speculative-verify latency of BASELINE config 4")
+                    help="skip the speculative-verify latency (k = 4, 7 at context 1024)")
     ap.add_argument("--no-spec", action="store_true",
                     help="skip the speculative-loop timing (chain / tree with a known draft)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
@@ -233,7 +233,7 @@ def main():
     sd = synth_weights(args, seed=0, device=dev)
     model = Transformer.from_weights(args, sd, dev)
     torch.cuda.synchronize()
-    total = max(a.ctx + a.warmup + a.steps + 8, 1024 + 32)  # + config 4's verify context
+    total = max(a.ctx + a.warmup + a.steps + 8, 1024 + 32)  # + the verify timing's context
     model.setup_caches(1, total)
     g = torch.Generator().manual_seed(1234)
     prompt = torch.randint(0, args.vocab_size, (a.ctx,), generator=g, dtype=torch.int32).to(dev)

@@ -50,7 +50,7 @@ class ModelArgs:
 
 
 CONFIGS = {
-    # BASELINE's 40-layer 3B-class dense int4 model (configs 0-4; config 0 uses n_layer=1)
+    # the benchmark's 40-layer 3B-class dense int4 model (and its one-layer parity variant)
     "flint-3b": dict(block_size=16384, n_layer=40, n_head=40, n_local_heads=8, dim=2560,
                      intermediate_size=8192, vocab_size=49152, rope_base=10000),
     "flint-3b-l1": dict(block_size=16384, n_layer=1, n_head=40, n_local_heads=8, dim=2560,

@@ -155,7 +155,7 @@ def test_decode_large_chunk_budget(dev, monkeypatch, name, budget):
 
 @pytest.mark.parametrize("pos", [4095, 8191])
 def test_decode_long_context(dev, pos):
-    """BASELINE config 3 shape (one layer of the 3B model, 40 Q / 8 KV heads) at context 4096 and
+    """The long-context shape (one layer of the 3B model, 40 Q / 8 KV heads) at context 4096 and
     8192: several slices per head and several rounds per wave."""
     args, sd, eng, orc = make_pair("flint-3b-l1", seed=2)
     eng.setup_caches(1, 8192)
