@@ -1972,10 +1972,34 @@ struct fl_state {
   void* blocks[16];
   int nblocks;
   void* uc[8];  // pooled uncached exchange buffers
+  size_t uc_bytes[8];
   int nuc;
+  // Tags are 16 bits (1..65535) and advance 5 per layer per launch, so a word left over from an
+  // older launch could carry the tag a reader is waiting for once the tags have gone round. The
+  // exchange buffers are zeroed (tag 0: never valid) every clear_period launches, fewer than
+  // take the tags round.
+  uint32_t clear_period, since_clear;
 };
 
 namespace {
+__global__ __launch_bounds__(256) void k_zero(uint4* __restrict__ p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+// zero every exchange buffer (a kernel, not hipMemsetAsync, so a captured stream stays valid)
+int clear_exchange(fl_state* st, hipStream_t s) {
+  for (int i = 0; i < st->nuc; ++i) {
+    const size_t n16 = st->uc_bytes[i] / 16;
+    hipLaunchKernelGGL(k_zero, dim3((unsigned)std::min<size_t>((n16 + 255) / 256, 4096)), dim3(256), 0, s,
+                       reinterpret_cast<uint4*>(st->uc[i]), n16);
+  }
+  st->since_clear = 0;
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+}
+// before each decode / verify launch
+int maybe_clear(fl_state* st, hipStream_t s) {
+  return ++st->since_clear >= st->clear_period ? clear_exchange(st, s) : FL_OK;
+}
 template <typename T>
 int dev_alloc(fl_state* st, T** p, size_t count) {
   void* v = nullptr;
@@ -2025,6 +2049,7 @@ int uc_alloc(fl_state* st, T** p, size_t count) {
     }
   }
   if (hipMemset(v, 0, bytes) != hipSuccess) return FL_E_HIP;
+  st->uc_bytes[st->nuc] = bytes;
   st->uc[st->nuc++] = v;
   *p = reinterpret_cast<T*>(v);
   return FL_OK;
@@ -2135,6 +2160,14 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   st->kc = k_cache;
   st->vc = v_cache;
   st->epoch = 1;
+  {
+    // epochs advance 5 * NL per launch; a tag repeats after 65535 epochs. Within a window of
+    // P launches, 5 * NL * (P + 1) < 65535 keeps every (launch, layer, phase) tag distinct.
+    long per = 5L * d->n_layer, P = 65535L / per - 2;
+    if (const char* e = getenv("FL_CLEAR_PERIOD")) P = std::min(P, std::max(1L, atol(e)));  // tests
+    st->clear_period = (uint32_t)std::max(1L, P);
+    st->since_clear = 0;
+  }
   st->att_spw = 8;
   // Plain launches by default: one workgroup per CU is all that fits (LDS), the grid is one per
   // CU, and on a device not shared with concurrent work every workgroup is resident at once. A
@@ -2195,7 +2228,7 @@ int fl_state_reset(fl_state* st, void* stream) {
     return FL_E_HIP;
   if (hipMemsetAsync(st->done, 0, sizeof(uint32_t), s) != hipSuccess) return FL_E_HIP;
   if (hipMemsetAsync(st->err, 0, sizeof(int32_t), s) != hipSuccess) return FL_E_HIP;
-  return FL_OK;
+  return clear_exchange(st, s);
 }
 
 int fl_state_profile(fl_state* st, uint64_t* buf, int32_t slots_per_wg, int32_t* grid) {
@@ -2242,6 +2275,7 @@ int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, i
                    int32_t* token_out, float* logits, uint16_t* feat, void* stream) {
   if (!st || !token_in || !token_out || !weights_ok(w)) return FL_E_ARG;
   if (pos < 0 || pos >= st->max_seq || pos >= w->rope_len) return FL_E_POS;
+  if (maybe_clear(st, as_stream(stream)) != FL_OK) return FL_E_LAUNCH;
   DecodeParams p = base_params(w, st, pos);
   p.token_in = token_in;
   p.token_out = token_out;
@@ -2271,6 +2305,7 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
     const int gpp = std::min(NWAVE, st->d.dim >> 7);
     if (st->vgrid < ((st->d.inter >> 7) + gpp - 1) / gpp) return FL_E_ARG;
   }
+  if (maybe_clear(st, as_stream(stream)) != FL_OK) return FL_E_LAUNCH;
   DecodeParams p = base_params(w, st, pos);
   p.M = m;
   p.tokens = tokens;

@@ -102,7 +102,9 @@ int fl_gemm_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint1
 int fl_state_create(const fl_model_desc* desc, int32_t max_seq, uint16_t* k_cache,
                     uint16_t* v_cache, fl_state** out);
 int fl_state_destroy(fl_state* st);
-/* Zero all scratch counters (not the KV cache). */
+/* Zero all scratch counters and exchange buffers (not the KV cache). The exchange buffers are
+ * also zeroed every few hundred launches by the launches themselves (a kernel on the launch's
+ * stream), before their 16-bit tags could come round to a value an old word still carries. */
 int fl_state_reset(fl_state* st, void* stream);
 /* Diagnostics, no counterpart in the reference: when buf (device, uint64 [grid * slots_per_wg])
  * is non-NULL, every later decode launch writes per-workgroup timestamps of the 100 MHz

@@ -195,3 +195,28 @@ def test_engine_matches_reference_golden(dev):
             assert d <= LOGIT_TOL, (st["pos"] + m, d)
             assert int(out.item()) == int(torch.argmax(ref))
     log(f"golden: worst |dlogit| {worst:.3e}")
+
+
+def test_exchange_clearing_keeps_results(dev, monkeypatch):
+    """The exchange buffers are zeroed every few hundred launches (their 16-bit tags would
+    otherwise come round to a value an old word carries); zeroing before every other launch
+    (FL_CLEAR_PERIOD=2, read when the state is created) must leave prefill, decode and verify
+    results unchanged, and so must fl_state_reset."""
+    from flint_amd.generate import generate
+    args, _, eng, _ = make_pair("tiny", seed=6)
+    prompt = torch.arange(3, 40, dtype=torch.int32)
+    ref = generate(eng, prompt, 20).cpu()
+    _, lg_ref, _ = eng.verify(ref[40:45].to(dev), 45)
+    lg_ref = lg_ref.cpu()
+    eng.close()
+    monkeypatch.setenv("FL_CLEAR_PERIOD", "2")
+    eng.max_seq_length = -1
+    out = generate(eng, prompt, 20).cpu()
+    assert torch.equal(out, ref)
+    _, lg, _ = eng.verify(ref[40:45].to(dev), 45)
+    assert torch.equal(lg.cpu(), lg_ref)
+    from flint_amd import _lib
+    _lib.call("fl_state_reset", eng._state, _lib.stream_ptr())
+    _, lg2, _ = eng.verify(ref[40:45].to(dev), 45)
+    assert torch.equal(lg2.cpu(), lg_ref)
+    eng.check()
