@@ -18,6 +18,14 @@ as 1, 2, 3", SC 2011; the published Random123 known-answer vectors pin it) keyed
 with counter (vocab index, row, offset low, offset high), u = ((x0 >> 8) + 0.5) 2^-24 and
 q = bf16(-log(u)) with the log in float64. Given the same q, the sample is a deterministic
 function of the logits, and that function is what the GPU parity tests compare.
+
+Pinned by: the Random123 known-answer vectors (Philox), the noise's moments and distance to
+Exp(1), torch CPU's own bf16 ops on the same six lines (logits_to_probs_torch: within one bf16
+ulp, nearly always identical), closed forms (top_k = 1 and constant noise give the argmax; ties
+at the pivot stay) and the sample distribution (chi-square). The reference runs these ops on
+CUDA, whose softmax and division may round the last fp32 bit differently from torch's CPU
+kernels; that last-bit agreement is parity unpinned (no CUDA here), below the bf16 rounding that
+follows except at rounding boundaries.
 """
 import numpy as np
 import torch
