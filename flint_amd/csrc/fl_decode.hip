@@ -1849,24 +1849,27 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
       for (int i = tid; i < M * D; i += NT) p.feat[i] = xs[(i / D) * ld + (i % D)];
     const int lane = tid & 63, wave = tid >> 6, r = lane & 15, c = lane >> 4;
     const int ksteps = D >> 5;
-    for (int t = wg; t < ntile; t += G) {
-      const int n0 = t * 16;
-      const int rows = min(16, p.V - n0);
-      const auto er = buf_rsrc(p.w.embed + (size_t)n0 * D, (uint32_t)rows * (uint32_t)D * 2u);
-      const uint16_t* xrow = xs + (r < M ? r : M) * ld + c * 8;
-      fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      constexpr int SPW = 16;  // k-steps per wave (D <= 4096)
-      uint4 bw[SPW];
+    const uint16_t* xrow = xs + (r < M ? r : M) * ld + c * 8;
+    constexpr int SPW = 16;  // k-steps per wave (D <= 4096)
+    // double-buffered: the next tile's embedding rows are requested before this tile's MFMAs; a
+    // tile past the vocabulary requests nothing (empty range), so the loads stay branch-free
+    auto load_tile = [&](int t, uint4 (&bw)[SPW]) {
+      const int rows = max(0, min(16, p.V - t * 16));
+      const auto er = buf_rsrc(p.w.embed + (size_t)t * 16 * D, (uint32_t)rows * (uint32_t)D * 2u);
 #pragma unroll
       for (int i = 0; i < SPW; ++i) {
-        const int s = wave + NWAVE * i;
-        bw[i] = buf_ld128(er, s < ksteps ? (uint32_t)(r * D + s * 32 + c * 8) * 2u : 0xFFFFFFF0u);
+        const int st = wave + NWAVE * i;
+        bw[i] = buf_ld128(er, st < ksteps ? (uint32_t)(r * D + st * 32 + c * 8) * 2u : 0xFFFFFFF0u);
       }
+    };
+    auto do_tile = [&](int t, const uint4 (&bw)[SPW]) {
+      const int n0 = t * 16, rows = min(16, p.V - n0);
+      fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < SPW; ++i) {
-        const int s = wave + NWAVE * i;
-        if (s < ksteps) {
-          const uint4 xa = *reinterpret_cast<const uint4*>(xrow + s * 32);
+        const int st = wave + NWAVE * i;
+        if (st < ksteps) {
+          const uint4 xa = *reinterpret_cast<const uint4*>(xrow + st * 32);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(fl_bf16x8, xa),
                                                         __builtin_bit_cast(fl_bf16x8, bw[i]), acc, 0, 0, 0);
         }
@@ -1882,6 +1885,15 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
         }
       }
       lds_barrier();
+    };
+    uint4 bwa[SPW], bwb[SPW];
+    load_tile(wg, bwa);
+    for (int t = wg; t < ntile; t += 2 * G) {
+      load_tile(t + G, bwb);
+      do_tile(t, bwa);
+      if (t + G >= ntile) break;
+      load_tile(t + 2 * G, bwa);
+      do_tile(t + G, bwb);
     }
   } else {
     stamp(p, slot);
