@@ -116,14 +116,28 @@ class LookupDraft:
         self.width, self.depth = int(width), int(depth)
         self.max_nodes = min(int(max_nodes), _lib.MAX_VERIFY)
 
+    def _index(self, ctx):
+        """Positions of every n-gram (min_ngram <= n <= max_ngram) of ctx, oldest first, kept
+        across calls and extended when ctx extends the previous context (the loop's case,
+        recognised by the previous length and its first and last 8 tokens)."""
+        n0 = getattr(self, "_n", 0)
+        if not (n0 and len(ctx) >= n0 and tuple(ctx[:8]) == self._head
+                and tuple(ctx[max(0, n0 - 8):n0]) == self._tail):
+            n0, self._pos = 0, {}
+        for n in range(self.min_ngram, self.max_ngram + 1):
+            for i in range(max(0, n0 - n + 1), len(ctx) - n + 1):
+                self._pos.setdefault(tuple(ctx[i:i + n]), []).append(i)
+        self._n, self._head, self._tail = len(ctx), tuple(ctx[:8]), tuple(ctx[max(0, len(ctx) - 8):])
+        return self._pos
+
     def _continuations(self, context, k, limit):
-        ctx = [int(t) for t in context]
+        ctx = context if isinstance(context, list) else [int(t) for t in context]
         n_ctx = len(ctx)
+        pos = self._index(ctx)
         found, seen = [], set()
         for n in range(min(self.max_ngram, n_ctx - 1), self.min_ngram - 1, -1):
-            key = ctx[n_ctx - n:]
-            for start in range(n_ctx - n - 1, -1, -1):
-                if ctx[start:start + n] != key:
+            for start in reversed(pos.get(tuple(ctx[n_ctx - n:]), ())):
+                if start >= n_ctx - n:          # the suffix itself
                     continue
                 cont = tuple(ctx[start + n:start + n + k])
                 if cont and cont not in seen:

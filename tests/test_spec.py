@@ -362,3 +362,19 @@ def test_spec_loop_rejects_bad_drafts():
         SpecDecoder(StandInModel(), k=16)
     with pytest.raises(ValueError):
         SpecDecoder(StandInModel()).generate([], 4)
+
+
+def test_lookup_draft_incremental_index_equals_fresh():
+    """The n-gram index grows with the context the loop passes back (the same list, longer each
+    pass) and is rebuilt for an unrelated context; proposals equal a fresh draft's every time."""
+    rng = np.random.default_rng(7)
+    ctx = [int(x) for x in rng.integers(0, 12, size=40)]
+    d = LookupDraft(width=3, depth=4)
+    for step in range(120):
+        ctx.append(int(rng.integers(0, 12)))
+        if step == 60:                                  # an unrelated context of another length
+            other = [int(x) for x in rng.integers(0, 12, size=70)]
+            assert d.tree(other, None) == LookupDraft(width=3, depth=4).tree(list(other), None)
+        fresh = LookupDraft(width=3, depth=4)
+        assert d.tree(ctx, None) == fresh.tree(list(ctx), None)
+        assert d.chain(ctx, None, 5) == fresh.chain(list(ctx), None, 5)
