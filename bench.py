@@ -56,19 +56,23 @@ def step_bytes(args, packed, T):
     return int4 + lm + norms + emb_row + kv_read + kv_write
 
 
-def cpu_baseline(args, sd, ctx, steps):
+def cpu_baseline(args, sd, prompt, steps):
+    """The reference int4 decode path on the host CPU (oracle/cpu_int4.py, torch's CPU int4
+    kernel; test infrastructure, timed here as the baseline): the same prompt prefilled (untimed),
+    then `steps` greedy decode steps timed."""
     from oracle.cpu_int4 import CpuInt4Decoder
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
     log(f"cpu baseline: packing int4 weights for the CPU kernel ({ncores} threads)")
     dec = CpuInt4Decoder(args, sd)
-    dec.setup_caches(ctx + steps + 8, fill_upto=ctx, seed=5)
-    tok = 1
-    for i in range(2):  # warmup
-        tok = dec.step(tok, ctx + i)
+    ctx = prompt.numel()
+    dec.setup_caches(ctx + steps + 8)
+    t0 = time.perf_counter()
+    tok = dec.prefill(prompt.cpu(), 0)
+    log(f"cpu baseline: prefill of {ctx} tokens took {time.perf_counter() - t0:.1f} s")
     t0 = time.perf_counter()
     for i in range(steps):
-        tok = dec.step(tok, ctx + 2 + i)
+        tok = dec.step(tok, ctx + i)
     dt = time.perf_counter() - t0
     model = ""
     try:
@@ -80,8 +84,9 @@ def cpu_baseline(args, sd, ctx, steps):
     except OSError:
         pass
     return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": ncores, "kind": "port",
-            "sample": f"{steps} greedy int4 decode steps at ctx {ctx} (random KV) of the same "
-                      f"40-layer model via aten::_weight_int4pack_mm_for_cpu; {model}"}
+            "sample": f"{steps} greedy int4 decode steps at ctx {ctx}..{ctx + steps - 1} after a "
+                      f"{ctx}-token prefill of the same prompt, same 40-layer model, int4 linears "
+                      f"via aten::_weight_int4pack_mm_for_cpu; {model}"}
 
 
 def verify_latency(model, args, dev, ctx=1024, reps=20):
@@ -153,6 +158,20 @@ class KnownDraft:
         return toks, pars
 
 
+def decode_margin(model, seq, t):
+    """Top-2 logit margin of plain decode (fl_decode_step) for the token at index t of seq, given
+    seq[:t] (teacher-forced: prefill seq[:t-1], one decode step of seq[t-1])."""
+    from flint_amd.generate import prefill
+    dev = model.device
+    toks = torch.tensor(seq[:t], dtype=torch.int32, device=dev)
+    if t > 1:
+        prefill(model, toks[:t - 1], 0)
+    lg = torch.empty(model.config.vocab_size, dtype=torch.float32, device=dev)
+    model.decode_step(toks[t - 1:t], t - 1, logits=lg)
+    v = torch.topk(lg, 2).values.tolist()
+    return v[0] - v[1]
+
+
 def spec_loop(model, args, prompt, ref, n, rounds=40):
     """Speculative greedy decoding through flint_amd.spec (one fl_verify launch per pass, plus
     fl_kv_move for a tree) at full acceptance: chain k = 4 and 7, a 16-node tree (depth 5, width
@@ -161,24 +180,113 @@ def spec_loop(model, args, prompt, ref, n, rounds=40):
     depend on M, so a draft built from plain decode loses agreement at the first tie broken the
     other way; the draft is therefore re-seeded with each run's own output until a run accepts its
     whole draft (a fixed point, reached within `rounds`), and that run is the one reported.
-    Wall-clock tok/s over the decode loop (prefill excluded), host loop included."""
+    Wall-clock tok/s over the decode loop (prefill excluded), host loop included. Wherever a
+    re-seed changed the output, the first changed token's top-2 margin under plain decode is
+    recorded: a change is expected only where that margin is within the 40-layer parity bar
+    (verify and decode sum in different fp32 orders); a wider margin is flagged."""
     from flint_amd.spec import SpecDecoder
+    bar = 2 * 0.2578125     # twice the oracle's own fp32-order floor at 40 layers
     res = []
     for mode, k in (("chain", 0), ("chain", 4), ("chain", 7), ("tree", 0)):
         cur = ref
+        margins = []
         for r in range(rounds):
             dec = SpecDecoder(model, KnownDraft(cur, args.vocab_size), k=k)
             out, st = dec.generate(prompt, n, mode=mode)
             if out == cur:
                 break
+            t = next(i for i in range(min(len(out), len(cur))) if out[i] != cur[i])
+            margins.append(round(decode_margin(model, out, t), 4))
             cur = out
         model.check()
         res.append({"mode": mode, "k": k if mode == "chain" else 15, "tokens": st.tokens,
                     "passes": st.passes, "tokens_per_pass": round(st.tokens_per_pass, 2),
                     "tok_s": round(st.tokens / st.seconds, 1),
                     "ms_per_pass": round(1000 * st.seconds / max(st.passes, 1), 3),
-                    "full_acceptance": out == cur, "reseeds": r})
+                    "full_acceptance": out == cur, "reseeds": r,
+                    "reseed_margins": margins,
+                    "reseeds_beyond_bar": sum(1 for m in margins if m > bar)})
     return res
+
+
+def gemv_sweep(args, dev, sets=40, rounds=3):
+    """fl_gemv_int4 at M = 1 over the four per-layer shapes, 40 distinct weight
+    sets per shape, called in layer order (QKV, O, gate/up, down of set 0, then set 1, ...) so the
+    1.67 GB rotation exceeds the 256 MB Infinity Cache and every call reads its weights from HBM.
+    HIP events around every call; per shape the mean call time and algorithmic GB/s
+    (N*K/2 int4 + N*K/128*4 scale/zero + 2K x + 2N y bytes). Weights are seeded random int4 words
+    with bf16 scales 1e-3 and zeros 0 (the time does not depend on the values)."""
+    from flint_amd import _lib
+    D, F = args.dim, args.intermediate_size
+    shapes = [("qkv", args.qkv_dim, D), ("o", D, D), ("gate_up", 2 * F, D), ("down", D, F)]
+    g = torch.Generator(device=dev).manual_seed(9)
+    sz_word = 0x3A83  # bf16(1e-3) scale, zero 0
+    W = {}
+    for name, n, k in shapes:
+        q = torch.randint(-2 ** 31, 2 ** 31 - 1, (sets, n, k // 8), generator=g, device=dev, dtype=torch.int32)
+        sz = torch.full((sets, n, k // 128), sz_word, dtype=torch.int32, device=dev)
+        x = torch.randn(k, generator=g, device=dev).to(torch.bfloat16)
+        y = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        W[name] = (q, sz, x, y, n, k)
+    stream = torch.cuda.current_stream()
+    sp = _lib.stream_ptr()
+
+    def call(name, i):
+        q, sz, x, y, n, k = W[name]
+        _lib.call("fl_gemv_int4", _lib.ptr(q[i]), _lib.ptr(sz[i]), _lib.ptr(x), _lib.ptr(y), n, k, sp)
+    for i in range(sets):                       # warm-up pass
+        for name, _, _ in shapes:
+            call(name, i)
+    torch.cuda.synchronize()
+    ev = {name: [] for name, _, _ in shapes}
+    for _ in range(rounds):
+        for i in range(sets):
+            for name, _, _ in shapes:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                call(name, i)
+                e1.record(stream)
+                ev[name].append((e0, e1))
+    torch.cuda.synchronize()
+    out = {}
+    for name, n, k in shapes:
+        us = sum(a.elapsed_time(b) for a, b in ev[name]) * 1000.0 / len(ev[name])
+        nbytes = n * k // 2 + n * (k // 128) * 4 + 2 * k + 2 * n
+        out[name] = {"n": n, "k": k, "us": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    rot = sets * sum(W[nm][0][0].numel() * 4 + W[nm][1][0].numel() * 4 for nm, _, _ in shapes)
+    return {"sets_per_shape": sets, "rotation_bytes": rot, "shapes": out}
+
+
+def long_context(model, args, dev, ctx=8192, steps=128):
+    """greedy decode of `steps` tokens after a context of `ctx` keys (KV
+    40 x 8 x 64 x ctx bf16, a quarter of each step's bytes). The cache prefix is synthetic (random
+    bf16 rows; the step time depends only on its length); tokens chain on the device as in the
+    headline loop."""
+    need = ctx + steps + 8
+    if model.max_seq_length < need:
+        model.setup_caches(1, need)
+    g = torch.Generator(device=dev).manual_seed(8192)
+    model.k_cache[:, :, :ctx].normal_(generator=g)
+    model.v_cache[:, :, :ctx].normal_(generator=g)
+    seq = torch.empty(steps + 1, dtype=torch.int32, device=dev)
+    seq[0] = 1
+    for i in range(4):                                          # warm-up at the same positions
+        model.decode_step(seq[i:i + 1], ctx + i, token_out=seq[i + 1:i + 2])
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(steps):
+        model.decode_step(seq[i:i + 1], ctx + i, token_out=seq[i + 1:i + 2])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    model.check()
+    ms = e0.elapsed_time(e1) / steps
+    mean_bytes = sum(step_bytes(args, model.packed, ctx + i + 1) for i in range(steps)) / steps
+    gbs = mean_bytes / (ms * 1e-3) / 1e9
+    return {"ctx": ctx, "steps": steps, "tok_s": round(1000.0 / ms, 1), "us_per_step": round(ms * 1000, 1),
+            "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def sampling_latency(args, dev, reps=50):
@@ -209,7 +317,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--ctx", type=int, default=512)
     ap.add_argument("--config", default="flint-3b")
-    ap.add_argument("--cpu-steps", type=int, default=16)
+    ap.add_argument("--cpu-steps", type=int, default=64)
+    ap.add_argument("--spec-tokens", type=int, default=128)
+    ap.add_argument("--no-long", action="store_true", help="skip config 3 (decode at ctx 8192)")
+    ap.add_argument("--no-gemv", action="store_true", help="skip config 1 (HBM-cold GEMV sweep)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true",
                     help="skip the speculative-verify latency (k = 4, 7 at context 1024)")
@@ -233,7 +344,8 @@ def main():
     sd = synth_weights(args, seed=0, device=dev)
     model = Transformer.from_weights(args, sd, dev)
     torch.cuda.synchronize()
-    total = max(a.ctx + a.warmup + a.steps + 8, 1024 + 32)  # + the verify timing's context
+    total = max(a.ctx + a.warmup + a.steps + 8, 1024 + 32,  # + the verify timing's context
+                0 if a.no_long else 8192 + 128 + 16)                # + config 3's
     model.setup_caches(1, total)
     g = torch.Generator().manual_seed(1234)
     prompt = torch.randint(0, args.vocab_size, (a.ctx,), generator=g, dtype=torch.int32).to(dev)
@@ -279,12 +391,31 @@ def main():
 
     spec = None
     if not a.no_spec:
-        n = min(128, a.warmup + a.steps)
-        spec = spec_loop(model, args, prompt.tolist(), seq[:a.ctx + n].tolist(), n)
+        n = a.spec_tokens
+        # the known continuation: plain greedy decode of n tokens after the prompt
+        ref = torch.empty(a.ctx + n, dtype=torch.int32, device=dev)
+        ref[:a.ctx] = prompt
+        from flint_amd.generate import prefill
+        prefill(model, ref[:a.ctx - 1], 0)
+        for i in range(n):
+            model.decode_step(ref[a.ctx - 1 + i:a.ctx + i], a.ctx - 1 + i, token_out=ref[a.ctx + i:a.ctx + i + 1])
+        spec = spec_loop(model, args, prompt.tolist(), ref.tolist(), n)
         for r in spec:
-            log(f"spec {r['mode']} k={r['k']}: {r['tok_s']} tok/s, {r['tokens_per_pass']} tokens "
-                f"per pass, {r['ms_per_pass']} ms per pass (full acceptance {r['full_acceptance']} "
-                f"after {r['reseeds']} re-seeds)")
+            log(f"spec {r['mode']} k={r['k']}: {r['tok_s']} tok/s over {r['tokens']} tokens, "
+                f"{r['tokens_per_pass']} tokens per pass ({r['passes']} passes), {r['ms_per_pass']} ms "
+                f"per pass (full acceptance {r['full_acceptance']} after {r['reseeds']} re-seeds, "
+                f"margins {r['reseed_margins']})")
+
+    long = None
+    if not a.no_long:
+        long = long_context(model, args, dev)
+        log(f"config 3 (ctx {long['ctx']}): {long['tok_s']} tok/s, {long['us_per_step']} us/step, "
+            f"{long['achieved_GBs']} GB/s")
+
+    gemv = None
+    if not a.no_gemv:
+        gemv = gemv_sweep(args, dev)
+        log(f"config 1 (fl_gemv_int4, {gemv['rotation_bytes'] / 1e9:.2f} GB rotation): {gemv['shapes']}")
 
     sampling = sampling_latency(args, dev)
     log(f"fl_sample over {args.vocab_size} logits: {sampling}")
@@ -302,7 +433,7 @@ def main():
     cpu = None
     if not a.no_cpu_baseline:
         try:
-            cpu = cpu_baseline(args, sd, a.ctx, a.cpu_steps)
+            cpu = cpu_baseline(args, sd, prompt, a.cpu_steps)
             log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
         except Exception as e:  # the GPU figure stands on its own
             log(f"cpu baseline failed: {e!r}")
@@ -330,9 +461,14 @@ def main():
         "cpu_baseline": cpu,
         "verify": verify,
         "spec": spec,
+        "long_context": long,
+        "gemv_sweep": gemv,
         "sampling": sampling,
     }
     print(json.dumps(out), flush=True)
+    # release the decode state (and its device memory) before interpreter shutdown
+    torch.cuda.synchronize()
+    model.close()
 
 
 if __name__ == "__main__":

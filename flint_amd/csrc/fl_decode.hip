@@ -80,6 +80,7 @@ struct DecodeParams {
   int32_t* err;                // abort flag (spin timeout / bad token)
   const int32_t* token_in;
   int32_t* token_out;
+  uint16_t* h_io;              // decode from a hidden state: bf16 [D] input, final residual out
   float* logits;
   uint16_t* feat;
   int D, NH, NKV, F, V, NL, S, pos;
@@ -936,13 +937,22 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
   const int pos = p.pos;
   int slot = 0;
   stamp(p, slot);
-  int token = *p.token_in;
-  if (token < 0 || token >= p.V) {  // bad device-side token: record it, read row 0 (no fault)
-    if (tid == 0 && wg == 0)
-      __hip_atomic_store(p.err, (int32_t)FL_E_ARG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    token = 0;
+  // the layer-0 input: bf16(embed[token] * emb_mult), or the caller's hidden state h_io as it is
+  // (reference kernels/megakernel_decode.cu:204-208 takes h; chat.py:72 forms it on the host)
+  const uint16_t* erow;
+  float emult = p.emb_mult;
+  if (p.h_io) {
+    erow = p.h_io;
+    emult = 1.0f;  // bf16(x * 1) = x
+  } else {
+    int token = *p.token_in;
+    if (token < 0 || token >= p.V) {  // bad device-side token: record it, read row 0 (no fault)
+      if (tid == 0 && wg == 0)
+        __hip_atomic_store(p.err, (int32_t)FL_E_ARG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      token = 0;
+    }
+    erow = p.w.embed + (size_t)token * D;
   }
-  const uint16_t* erow = p.w.embed + (size_t)token * D;
 
   int r0d, rowsd;  // this workgroup's rows of every [D]-output GEMV (O, down): it owns h there
   row_range(D, wg, G, r0d, rowsd);
@@ -954,8 +964,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     const int jd = tid >> (lgd + 1);
     if ((tid & ((2 << lgd) - 1)) == 0 && 2 * jd < rowsd) {
       const uint32_t e2 = reinterpret_cast<const uint32_t*>(erow + r0d)[jd];
-      ha = rbf(bflo(e2) * p.emb_mult);
-      hb = rbf(bfhi(e2) * p.emb_mult);
+      ha = rbf(bflo(e2) * emult);
+      hb = rbf(bfhi(e2) * emult);
     }
   }
 
@@ -994,7 +1004,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     if (rows > 0) {
       if (l == 0) {
         rope_cs = buf_ld32(rope_r, rope_off);
-        norm_embed(erow, p.emb_mult, p.w.attn_norm, D, p.eps, xs, red);
+        norm_embed(erow, emult, p.w.attn_norm, D, p.eps, xs, red);
         gemv_predq_reg(w_qkv, s_qkv, dq_qkv, [](int) {});
       } else {
         norm_tagged(p, p.h, t_prev, p.w.attn_norm + (size_t)l * D, xs, red, [&](auto refresh) {
@@ -1144,6 +1154,15 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
         });
     stamp(p, slot);
   }
+  // the final residual back into the caller's hidden state (reference decode_mega mutates h in
+  // place). Every workgroup read h_io in layer 0 before its outputs could reach anyone's last
+  // layer (each phase waits for every producer of the one before), so no reader remains.
+  if (p.h_io) {
+    const int lgd = row_lanes_lg(rowsd);
+    const int jd = tid >> (lgd + 1);
+    if ((tid & ((2 << lgd) - 1)) == 0 && 2 * jd < rowsd)
+      reinterpret_cast<uint32_t*>(p.h_io + r0d)[jd] = pack_bf16x2(ha, hb);
+  }
 
   // ---------------- final norm + tied bf16 LM head + greedy argmax ----------------
   const int lane = tid & 63, wave = tid >> 6;
@@ -1212,7 +1231,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
     const uint32_t old = __hip_atomic_fetch_add(p.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == (uint32_t)(G - 1)) {
       const unsigned long long fin = ld_coh_u64(p.amax);
-      *p.token_out = (int32_t)amax_index(fin);
+      if (p.token_out) *p.token_out = (int32_t)amax_index(fin);
       __hip_atomic_store(p.amax, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -2008,6 +2027,12 @@ int clear_exchange(fl_state* st, hipStream_t s) {
   st->since_clear = 0;
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
+// after each decode / verify launch: 5 phases per layer. The epoch is kept reduced mod 65535 (the
+// tag period), so the kernel's epoch + 5 * layer + phase never wraps the 32-bit range and every
+// tag in a clear window stays distinct.
+void advance_epoch(fl_state* st) {
+  st->epoch = (st->epoch + 5u * (uint32_t)st->d.n_layer) % 65535u;
+}
 // before each decode / verify launch
 int maybe_clear(fl_state* st, hipStream_t s) {
   return ++st->since_clear >= st->clear_period ? clear_exchange(st, s) : FL_OK;
@@ -2112,6 +2137,30 @@ DecodeParams base_params(const fl_weights* w, fl_state* st, int pos) {
   p.epoch = st->epoch;
   p.M = 1;
   return p;
+}
+}  // namespace
+
+namespace {
+int decode_launch(const fl_weights* w, fl_state* st, const int32_t* token_in, uint16_t* h_io,
+                  int32_t pos, int32_t* token_out, float* logits, uint16_t* feat, void* stream) {
+  if (pos < 0 || pos >= st->max_seq || pos >= w->rope_len) return FL_E_POS;
+  if (maybe_clear(st, as_stream(stream)) != FL_OK) return FL_E_LAUNCH;
+  DecodeParams p = base_params(w, st, pos);
+  p.token_in = token_in;
+  p.h_io = h_io;
+  p.token_out = token_out;
+  p.logits = logits;
+  p.feat = feat;
+  p.prof = st->prof;
+  p.prof_slots = st->prof_slots;
+  void* args[] = {&p};
+  const hipError_t e =
+      st->coop ? hipLaunchCooperativeKernel(st->kdec, dim3(st->grid), dim3(NT), args, 0,
+                                            as_stream(stream))
+               : hipLaunchKernel(st->kdec, dim3(st->grid), dim3(NT), args, 0, as_stream(stream));
+  if (e != hipSuccess) return FL_E_LAUNCH;
+  advance_epoch(st);
+  return FL_OK;
 }
 }  // namespace
 
@@ -2283,26 +2332,17 @@ int fl_kv_move(fl_state* st, const int32_t* src, const int32_t* dst, int32_t n, 
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
 
+
 int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, int32_t pos,
                    int32_t* token_out, float* logits, uint16_t* feat, void* stream) {
   if (!st || !token_in || !token_out || !weights_ok(w)) return FL_E_ARG;
-  if (pos < 0 || pos >= st->max_seq || pos >= w->rope_len) return FL_E_POS;
-  if (maybe_clear(st, as_stream(stream)) != FL_OK) return FL_E_LAUNCH;
-  DecodeParams p = base_params(w, st, pos);
-  p.token_in = token_in;
-  p.token_out = token_out;
-  p.logits = logits;
-  p.feat = feat;
-  p.prof = st->prof;
-  p.prof_slots = st->prof_slots;
-  void* args[] = {&p};
-  const hipError_t e =
-      st->coop ? hipLaunchCooperativeKernel(st->kdec, dim3(st->grid), dim3(NT), args, 0,
-                                            as_stream(stream))
-               : hipLaunchKernel(st->kdec, dim3(st->grid), dim3(NT), args, 0, as_stream(stream));
-  if (e != hipSuccess) return FL_E_LAUNCH;
-  st->epoch += 5u * (uint32_t)st->d.n_layer;
-  return FL_OK;
+  return decode_launch(w, st, token_in, nullptr, pos, token_out, logits, feat, stream);
+}
+
+int fl_decode_hidden(const fl_weights* w, fl_state* st, uint16_t* h, int32_t pos,
+                     int32_t* token_out, float* logits, uint16_t* feat, void* stream) {
+  if (!st || !h || !weights_ok(w)) return FL_E_ARG;
+  return decode_launch(w, st, nullptr, h, pos, token_out, logits, feat, stream);
 }
 
 int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t m,
@@ -2336,7 +2376,7 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
                : hipLaunchKernel(reinterpret_cast<const void*>(k_verify), dim3(st->vgrid),
                                  dim3(NT), args, lds, as_stream(stream));
   if (e != hipSuccess) return FL_E_LAUNCH;
-  st->epoch += 5u * (uint32_t)st->d.n_layer;
+  advance_epoch(st);
   return FL_OK;
 }
 

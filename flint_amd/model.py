@@ -155,14 +155,24 @@ class Transformer:
             pass
 
     def activations(self):
-        """Diagnostics: the last step's activations (h, qkv pair-interleaved, attn, act) as views
-        of the library's scratch (valid until the next launch)."""
+        """Diagnostics: the last launch's activations, copied out of the library's tagged exchange
+        buffers (so no tensor keeps viewing library memory): h, attn [D] and act [F] as bf16 (each
+        exchange word holds a bf16 value in its low 16 bits and a phase tag above), and qkv
+        [(NH + 2 NKV) * 64] bf16 in model order (a word holds dims i and i + 32 of a head).
+        Synchronises the current stream first."""
+        torch.cuda.current_stream().synchronize()
         ptrs = [_lib.ctypes.c_void_p() for _ in range(4)]
         _lib.call("fl_state_buffers", self._state, *[_lib.ctypes.byref(p) for p in ptrs])
         a = self.config
-        sizes = [a.dim, a.qkv_dim, a.dim, a.intermediate_size]
-        return {k: _lib.device_view(p.value, n, torch.bfloat16)
-                for k, p, n in zip(("h", "qkv", "attn", "act"), ptrs, sizes)}
+        out = {}
+        for k, p, n in (("h", ptrs[0], a.dim), ("attn", ptrs[2], a.dim), ("act", ptrs[3], a.intermediate_size)):
+            w = _lib.device_view(p.value, n, torch.int32).clone()
+            out[k] = (w & 0xFFFF).to(torch.int16).view(torch.bfloat16)
+        w = _lib.device_view(ptrs[1].value, a.qkv_dim // 2, torch.int64).clone()
+        lo = (w & 0xFFFF).to(torch.int16).view(torch.bfloat16).view(-1, 32)
+        hi = ((w >> 16) & 0xFFFF).to(torch.int16).view(torch.bfloat16).view(-1, 32)
+        out["qkv"] = torch.cat([lo, hi], dim=1).reshape(-1)
+        return out
 
     def check(self):
         """Raise if a kernel recorded an error (synchronises)."""
@@ -180,6 +190,22 @@ class Transformer:
             if t is not None and (not t.is_cuda or t.dtype != dt):
                 raise ValueError(f"{nm} must be a {dt} device tensor")
         _lib.call("fl_decode_step", _lib.ctypes.byref(self._cw), self._state, _lib.ptr(token), int(pos),
+                  _lib.ptr(token_out), _lib.ptr(logits), _lib.ptr(feat), _lib.stream_ptr())
+        return token_out
+
+    def decode_hidden(self, h, pos, token_out=None, logits=None, feat=None):
+        """One decode step from a hidden state (reference decode_mega_launch's h argument): h (bf16
+        [D] device tensor) is the layer-0 input and holds the final residual afterwards (in place).
+        Optional outputs as decode_step; returns token_out (None if not given)."""
+        if self._state is None:
+            raise RuntimeError("call setup_caches first")
+        for t, dt, nm in ((h, torch.bfloat16, "h"), (token_out, torch.int32, "token_out"),
+                          (logits, torch.float32, "logits"), (feat, torch.bfloat16, "feat")):
+            if t is not None and (not t.is_cuda or t.dtype != dt):
+                raise ValueError(f"{nm} must be a {dt} device tensor")
+        if h.numel() != self.config.dim or not h.is_contiguous():
+            raise ValueError(f"h must be a contiguous [{self.config.dim}] tensor")
+        _lib.call("fl_decode_hidden", _lib.ctypes.byref(self._cw), self._state, _lib.ptr(h), int(pos),
                   _lib.ptr(token_out), _lib.ptr(logits), _lib.ptr(feat), _lib.stream_ptr())
         return token_out
 

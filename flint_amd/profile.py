@@ -95,3 +95,62 @@ def analyse(buf, grid, slots, n_layer):
     out["final_norm_wait_us"] = float((t[:, 1 + PER_LAYER * L] - lay[:, -1, 11]).mean())
     out["lm_head_us"] = float((t[:, 2 + PER_LAYER * L] - t[:, 1 + PER_LAYER * L]).max())
     return out
+
+
+def format_report(res, n_layer, label):
+    """Text table of analyse()'s result (the summary kept under profiles/)."""
+    out = [f"{label}: step {res['total_us']:.1f} us ({n_layer} layers; layer critical path "
+           f"{res['layer_critical_us']:.2f} us; final norm wait {res['final_norm_wait_us']:.2f} us; "
+           f"LM head {res['lm_head_us']:.2f} us)", "",
+           f"{'phase (per layer, mean over workgroups)':42s} {'input wait us':>14s} {'compute us':>11s} "
+           f"{'compute, slowest wg':>20s}"]
+    for name, d in res["phases"].items():
+        out.append(f"{name:42s} {d.get('input_wait_mean_us', float('nan')):14.2f} "
+                   f"{d['compute_mean_us']:11.2f} {d['compute_max_us']:20.2f}")
+    if res["attention_units"]:
+        a = res["attention_units"]
+        out += ["", f"attention workgroups: q/k/v wait {a['inputs_wait_us']:.2f} us, key loop "
+                    f"{a['chunks_us']:.2f} us, wave merge {a['merge_us']:.2f} us"]
+    out += ["", f"{'hand-off (per layer)':20s} {'producer spread':>16s} {'first consumer':>15s} "
+                f"{'median consumer':>16s} {'last consumer':>14s}   (us after the last producer)"]
+    for name, d in res["handoffs"].items():
+        out.append(f"{name:20s} {d['producer_spread_us']:16.2f} {d['first_consumer_us']:15.2f} "
+                   f"{d['median_consumer_us']:16.2f} {d['last_consumer_us']:14.2f}")
+    return "\n".join(out)
+
+
+def main(argv=None):
+    """python -m flint_amd.profile [--config flint-3b] [--ctx 512] [--steps 8]: one model on the
+    GPU, a ctx-token prompt prefilled, `steps` decode steps with timestamps on; prints the
+    per-phase table of the last step."""
+    import argparse
+    from .generate import prefill
+    from .model import Transformer
+    from .synth import ModelArgs, synth_weights
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--config", default="flint-3b")
+    ap.add_argument("--ctx", type=int, default=512)
+    ap.add_argument("--steps", type=int, default=8)
+    a = ap.parse_args(argv)
+    args = ModelArgs.from_name(a.config)
+    dev = torch.device("cuda:0")
+    model = Transformer.from_weights(args, synth_weights(args, 0, device=dev), dev)
+    model.setup_caches(1, a.ctx + a.steps + 8)
+    g = torch.Generator().manual_seed(1234)
+    seq = torch.empty(a.ctx + a.steps, dtype=torch.int32, device=dev)
+    seq[:a.ctx] = torch.randint(0, args.vocab_size, (a.ctx,), generator=g, dtype=torch.int32).to(dev)
+    prefill(model, seq[:a.ctx - 1], 0)
+    buf, grid, slots = enable(model)
+    for i in range(a.steps):
+        p = a.ctx - 1 + i
+        model.decode_step(seq[p:p + 1], p, token_out=seq[p + 1:p + 2])
+    model.check()
+    disable(model)
+    res = analyse(buf, grid, slots, args.n_layer)
+    print(format_report(res, args.n_layer, f"{a.config} k_decode at ctx {a.ctx + a.steps - 1}, "
+                                           f"{grid} workgroups"))
+    model.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -116,18 +116,22 @@ class LookupDraft:
         self.width, self.depth = int(width), int(depth)
         self.max_nodes = min(int(max_nodes), _lib.MAX_VERIFY)
 
+    def reset(self):
+        """Forget the indexed context (SpecDecoder.generate calls this at the start of a run)."""
+        self._ctx, self._pos = [], {}
+
     def _index(self, ctx):
         """Positions of every n-gram (min_ngram <= n <= max_ngram) of ctx, oldest first, kept
-        across calls and extended when ctx extends the previous context (the loop's case,
-        recognised by the previous length and its first and last 8 tokens)."""
-        n0 = getattr(self, "_n", 0)
-        if not (n0 and len(ctx) >= n0 and tuple(ctx[:8]) == self._head
-                and tuple(ctx[max(0, n0 - 8):n0]) == self._tail):
+        across calls and extended when ctx extends the indexed context (the loop's case: the
+        whole indexed context must be a prefix of ctx, compared element by element)."""
+        old = getattr(self, "_ctx", [])
+        n0 = len(old)
+        if not (n0 and len(ctx) >= n0 and ctx[:n0] == old):
             n0, self._pos = 0, {}
         for n in range(self.min_ngram, self.max_ngram + 1):
             for i in range(max(0, n0 - n + 1), len(ctx) - n + 1):
                 self._pos.setdefault(tuple(ctx[i:i + n]), []).append(i)
-        self._n, self._head, self._tail = len(ctx), tuple(ctx[:8]), tuple(ctx[max(0, len(ctx) - 8):])
+        self._ctx = list(ctx)
         return self._pos
 
     def _continuations(self, context, k, limit):
@@ -231,6 +235,8 @@ class SpecDecoder:
     def generate(self, prompt, max_new, mode="chain", eos=None):
         if mode not in ("chain", "tree"):
             raise ValueError("mode is 'chain' or 'tree'")
+        if hasattr(self.draft, "reset"):
+            self.draft.reset()
         ids = [int(t) for t in (prompt.reshape(-1).tolist() if torch.is_tensor(prompt) else prompt)]
         if not ids:
             raise ValueError("empty prompt")

@@ -113,9 +113,10 @@ int fl_state_reset(fl_state* st, void* stream);
  * merge), then the final norm's input arrival and the end of the LM head. NULL disables.
  * *grid receives the number of workgroups. */
 int fl_state_profile(fl_state* st, uint64_t* buf, int32_t slots_per_wg, int32_t* grid);
-/* Diagnostics, no counterpart in the reference: device pointers of the last launch's
- * activations: residual h [D], this step's q/k/v (pair-interleaved: word hh*32+i holds dims i and
- * i+32 of head hh; heads [q | k | v]), attention output [D], SwiGLU output [F] (bf16). */
+/* Diagnostics, no counterpart in the reference: device pointers of the last launch's tagged
+ * exchange buffers (token row 0): residual h [D], attention output [D] and SwiGLU output [F] as
+ * uint32 words (bf16 bits | phase tag << 16), and this step's q/k/v as uint64 words [(NH+2*NKV)*32]
+ * (bf16 bits of dim i | bf16 bits of dim i+32 << 16 | tag << 32; word hh*32+i, heads [q|k|v]). */
 int fl_state_buffers(fl_state* st, uint16_t** h, uint16_t** qkv, uint16_t** attn, uint16_t** act);
 /* Last error recorded by a kernel (FL_OK or FL_E_TIMEOUT); synchronises the stream. */
 int fl_state_check(fl_state* st, void* stream);
@@ -129,6 +130,16 @@ int fl_state_check(fl_state* st, void* stream);
  * engine/generate.py:62-66 decode_one_token (greedy). */
 int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, int32_t pos,
                    int32_t* token_out, float* logits, uint16_t* feat, void* stream);
+
+/* The same decode step from a hidden state instead of a token: h (device, bf16 [D]) is the
+ * layer-0 input as it is (no embedding lookup, no embedding multiplier) and receives the final
+ * residual (before the final norm) when the launch completes, in place. token_out (greedy argmax),
+ * logits and feat are optional (NULL to skip).
+ * Replaces reference kernels/megakernel_decode.cu:204-237 decode_mega_launch(..., h, kc, vc, pos,
+ * ...), which takes h (formed on the host as bf16(embed[token] * mult), chat.py:71-74) and mutates
+ * it in place (:135, :159). */
+int fl_decode_hidden(const fl_weights* w, fl_state* st, uint16_t* h, int32_t pos,
+                     int32_t* token_out, float* logits, uint16_t* feat, void* stream);
 
 /* Speculative verify of M tokens in one pass (weights read once for all M):
  * token m sits at cache slot pos+m, RoPE position pos+depth[m]; it attends to the cache

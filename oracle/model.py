@@ -71,14 +71,56 @@ def hf_to_interleaved_perm(n_heads, head_dim):
     return (torch.arange(n_heads).unsqueeze(1) * head_dim + within.unsqueeze(0)).reshape(-1)
 
 
-def attention(q, kc, vc, valid, scale):
+def linear_g128(x, w):
+    """x . w^T with fp32 partial sums per 128-column group added in group order (bf16 result): a
+    second valid fp32 summation order of the reference linear (engine/quantize.py:517-525 fixes
+    the operands and the bf16 rounding of the result, not the order of the fp32 sum). Used to
+    measure the order-noise floor of the reference semantics on the inputs of a test."""
+    K = x.shape[-1]
+    acc = None
+    for b in range(0, K, 128):
+        part = x[..., b:b + 128].float() @ w[:, b:b + 128].float().T
+        acc = part if acc is None else acc + part
+    return acc.to(x.dtype)
+
+
+LOG2E = 1.4426950408889634
+
+
+def softmax_exp2(s):
+    """fp32 softmax with exp written as exp2(x * log2 e) (another valid fp32 implementation of the
+    reference softmax: the reference fixes the operation, not the last ulp of its exp)."""
+    p = torch.exp2((s - s.amax(dim=-1, keepdim=True)) * LOG2E)
+    return p / p.sum(dim=-1, keepdim=True)
+
+
+def silu_exp2(x):
+    """bf16 SiLU computed in fp32 as x * 1 / (1 + exp2(-x log2 e)) (another valid implementation
+    of torch's F.silu on a bf16 tensor: same operation, fp32 inside, one bf16 rounding)."""
+    xf = x.float()
+    return (xf * (1.0 / (1.0 + torch.exp2(-xf * LOG2E)))).to(x.dtype)
+
+
+# Named implementations of the reference semantics: (linear, softmax, silu). Every one fixes the
+# same operations and bf16 rounding points; they differ in fp32 summation order and in the last
+# ulps of exp, which is the freedom any implementation (the reference's own GPU path included) has.
+IMPLS = {
+    "torch": (F.linear, torch.softmax, F.silu),
+    "g128": (linear_g128, torch.softmax, F.silu),
+    "exp2": (F.linear, softmax_exp2, silu_exp2),
+    "g128+exp2": (linear_g128, softmax_exp2, silu_exp2),
+}
+LINEAR_ORDERS = {k: v[0] for k, v in IMPLS.items()}
+
+
+def attention(q, kc, vc, valid, scale, softmax=torch.softmax):
     """q bf16 [H, 64]; kc, vc bf16 [NKV, T, 64]; valid bool [T]. fp32 softmax attention, bf16 out [H*64]."""
     H, NKV = q.shape[0], kc.shape[0]
     rep = H // NKV
     k = kc[:, valid].float().repeat_interleave(rep, dim=0)   # [H, T', 64]
     v = vc[:, valid].float().repeat_interleave(rep, dim=0)
     s = torch.einsum("hd,htd->ht", q.float(), k) * scale
-    p = torch.softmax(s, dim=-1)
+    p = softmax(s, dim=-1) if softmax is torch.softmax else softmax(s)
     o = torch.einsum("ht,htd->hd", p, v)
     return o.to(torch.bfloat16).reshape(-1)
 
@@ -102,6 +144,14 @@ class OracleModel:
         self.embed = sd["embed"].cpu()
         self.table = freqs_cis(a.block_size, a.head_dim, a.rope_base)
         self.k_cache = self.v_cache = None
+        self.linear, self.softmax, self.silu = IMPLS["torch"]
+        self.last_residual = None
+
+    def set_order(self, name):
+        """Implementation of the reference semantics (IMPLS): "torch" (the default), "g128",
+        "exp2" or "g128+exp2". All are the reference semantics; their differences are the
+        noise floor any implementation has."""
+        self.linear, self.softmax, self.silu = IMPLS[name]
 
     def setup_caches(self, max_seq):
         a = self.args
@@ -119,7 +169,7 @@ class OracleModel:
         depth = torch.arange(M) if depth is None else depth
         amask = torch.tril(torch.ones(M, M, dtype=torch.bool)) if amask is None else amask.bool()
         xn = rms_norm(x, w["attn_norm"], a.norm_eps)
-        qkv = F.linear(xn, w["wqkv"])
+        qkv = self.linear(xn, w["wqkv"])
         q, k, v = qkv.split([a.n_head * hd, a.n_local_heads * hd, a.n_local_heads * hd], dim=-1)
         rows = self.table[pos + depth]                        # [M, 32, 2]
         q = rope_neox(q.view(M, a.n_head, hd), rows)
@@ -133,22 +183,28 @@ class OracleModel:
             valid = torch.zeros(T, dtype=torch.bool)
             valid[:pos] = True
             valid[pos:pos + M] = amask[m]
-            ys.append(attention(q[m], self.k_cache[l, :, :T], self.v_cache[l, :, :T], valid, a.attn_scale))
+            ys.append(attention(q[m], self.k_cache[l, :, :T], self.v_cache[l, :, :T], valid, a.attn_scale,
+                                self.softmax))
         y = torch.stack(ys)
-        return F.linear(y, w["wo"])
+        return self.linear(y, w["wo"])
 
-    def forward(self, idx, pos, depth=None, amask=None):
-        """idx int [M] at cache slots pos..pos+M-1 -> (logits bf16 [M, V], post-norm hidden bf16 [M, D])."""
+    def forward(self, idx, pos, depth=None, amask=None, h=None):
+        """idx int [M] at cache slots pos..pos+M-1 -> (logits bf16 [M, V], post-norm hidden bf16 [M, D]).
+        With h (bf16 [M, D]) the layer-0 input is h itself instead of the scaled embedding (the
+        reference megakernel's h argument, kernels/megakernel_decode.cu:204-208); idx is then
+        ignored. The final residual (before the final norm) is kept in self.last_residual."""
         a = self.args
-        x = self.embed[idx.long()] * a.embedding_multiplier
+        lin = self.linear
+        x = h.to(torch.bfloat16) if h is not None else self.embed[idx.long()] * a.embedding_multiplier
         for l in range(self.L):
             w = self.w[l]
-            h = x + self.layer_attention(l, x, pos, depth, amask) * a.residual_multiplier
-            hn = rms_norm(h, w["ffn_norm"], a.norm_eps)
-            ff = F.linear(F.silu(F.linear(hn, w["w1"])) * F.linear(hn, w["w3"]), w["w2"])
-            x = h + ff * a.residual_multiplier
+            h1 = x + self.layer_attention(l, x, pos, depth, amask) * a.residual_multiplier
+            hn = rms_norm(h1, w["ffn_norm"], a.norm_eps)
+            ff = lin(self.silu(lin(hn, w["w1"])) * lin(hn, w["w3"]), w["w2"])
+            x = h1 + ff * a.residual_multiplier
+        self.last_residual = x
         xn = rms_norm(x, self.norm, a.norm_eps)
-        logits = F.linear(xn, self.embed) / a.logits_scaling
+        logits = lin(xn, self.embed) / a.logits_scaling
         return logits, xn
 
     def decode_greedy(self, token, pos, steps):

@@ -49,23 +49,58 @@ def bf16_ulp(v):
     return torch.pow(2.0, torch.floor(torch.log2(a)) - 7)
 
 
-# fp32 summation-order noise floor of the reference semantics: two valid fp32 orders of the
-# CPU oracle itself differ by up to 0.03-0.06 in logits at the 3B model's dimensions (measured,
-# tests/test_oracle.py::test_fp32_order_noise_floor); the bar is twice the largest measured.
-NOISE_FLOOR = 0.125
+# fp32 summation-order noise floor of the reference semantics, per test configuration. The
+# reference fixes every bf16 rounding point but not the fp32 summation order inside a linear, and
+# an order difference flips single bf16 roundings that later layers spread. Each entry is
+# (max|dlogit|, mean|dlogit|): the largest of each between torch's F.linear order and three other
+# valid orders of the CPU oracle itself (per-128-group partial sums in order, reversed 4-way
+# split-K, 32-element chunks; and exp2-based softmax / SiLU), over several positions with random
+# N(0, 1) KV. tests/test_oracle_floor.py re-measures them (the 40-layer one opted in) and checks
+# that a planted rounding-point mistake exceeds the bars built from them. tiny measured 0: its sums
+# are too short for any of these to flip a bf16 rounding. The HIP kernels' own arithmetic still
+# flips a few (v_dot2_f32_bf16 is not correctly rounded in about 2e-5 of cases, by up to 8 ulp,
+# measured on the GPU; exp2 and rcp are the hardware's), so no bar is below one layer of the 3B
+# model's: one bf16 ulp of the top logits, and that layer's mean bar.
+ORDER_FLOOR = {
+    "tiny": (0.0, 0.0),
+    "small": (0.04736328125, 9.85e-3),    # 4 layers: down to 90.7% of logits within 2e-2
+    "wide": (0.037109375, 8.23e-3),
+    "flint-3b-l1": (0.03125, 1.84e-3),    # one bf16 ulp at |logit| in [4, 8); >= 99.97% within 2e-2
+    "flint-3b": (0.2578125, 4.93e-2),     # 40 layers: only 26-39% of logits within 2e-2
+}
+ULP_TOP = 2.0 ** -5            # one bf16 ulp at |logit| in [4, 8), the range of the top logits
+MEAN_MIN = 2.0 * ORDER_FLOOR["flint-3b-l1"][1]   # smallest mean bar: one 3B layer's
 NORTH_STAR_TOL = 2e-2
 
 
-def near_tie(ref_logits, margin=NOISE_FLOOR):
-    """True when the reference's top-2 logits are closer than the fp32-order noise floor, so the
-    argmax is not determined by the reference semantics themselves."""
+def logit_bar(name):
+    """Bar on max|dlogit| for configuration `name`: twice the oracle's own order floor, and at
+    least one bf16 ulp of the top logits."""
+    return max(2.0 * ORDER_FLOOR[name][0], ULP_TOP)
+
+
+def mean_bar(name):
+    """Bar on mean|dlogit| for configuration `name`: twice the oracle's own mean floor."""
+    return max(2.0 * ORDER_FLOOR[name][1], MEAN_MIN)
+
+
+def near_tie(ref_logits, bar):
+    """True when the reference's top-2 logits are within `bar`, so the argmax is not determined by
+    the reference semantics themselves (another valid fp32 order can flip it)."""
     v = torch.topk(ref_logits.float(), 2).values
-    return float(v[0] - v[1]) <= margin
+    return float(v[0] - v[1]) <= bar
 
 
-def compare_logits(eng, ref):
-    """(ok, max|d|, fraction of logits within 2e-2, fraction bit-identical)."""
-    e, r = eng.float(), ref.float()
-    d = (e - r).abs()
-    return (bool((d <= NOISE_FLOOR).all()), float(d.max()),
-            float((d <= NORTH_STAR_TOL).float().mean()), float((d == 0).float().mean()))
+def logit_stats(eng, ref):
+    """{max, mean, within (fraction of logits within 2e-2), same (fraction bit-identical)}."""
+    d = (eng.float() - ref.float()).abs()
+    return {"max": float(d.max()), "mean": float(d.mean()),
+            "within": float((d <= NORTH_STAR_TOL).float().mean()), "same": float((d == 0).float().mean())}
+
+
+def compare_logits(eng, ref, name):
+    """(ok, max|d|, fraction of logits within 2e-2, fraction bit-identical) against configuration
+    `name`'s bars: ok = max|d| <= logit_bar(name) and mean|d| <= mean_bar(name)."""
+    st = logit_stats(eng, ref)
+    ok = st["max"] <= logit_bar(name) and st["mean"] <= mean_bar(name)
+    return ok, st["max"], st["within"], st["same"]

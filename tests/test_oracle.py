@@ -183,45 +183,3 @@ def test_forward_chain_equals_sequential_steps():
         l2, h2 = o2.forward(toks[i:i + 1], i)
         assert float((l1[i].float() - l2[0].float()).abs().max()) <= 2e-2
     assert torch.equal(o1.k_cache, o2.k_cache) or float((o1.k_cache.float() - o2.k_cache.float()).abs().max()) <= 0.05
-
-
-def test_fp32_order_noise_floor():
-    """The reference semantics fix every bf16 rounding point but not the fp32 summation order of
-    a linear. Two valid orders of the oracle (torch's, and reversed 4-way split-K) flip rare bf16
-    roundings that later layers spread: logits then differ by more than 2e-2 but stay far below
-    the parity bar the GPU tests use (0.125). This measures that floor."""
-    from flint_amd.synth import CONFIGS, ModelArgs, synth_weights
-    cfg = dict(CONFIGS["small"])
-    a = ModelArgs(**cfg)
-    sd = synth_weights(a, 0)
-    oa, ob = om.OracleModel(a, sd), om.OracleModel(a, sd)
-
-    def lin_split(x, w):
-        K = x.shape[-1]
-        bs = K // 4
-        acc = None
-        for b in reversed(range(4)):
-            part = x[..., b * bs:(b + 1) * bs].float() @ w[:, b * bs:(b + 1) * bs].float().T
-            acc = part if acc is None else acc + part
-        return acc.to(x.dtype)
-
-    worst = 0.0
-    orig = om.F.linear
-    for pos in (64, 200):
-        for o in (oa, ob):
-            o.setup_caches(256)
-        g = torch.Generator().manual_seed(pos + 1)
-        k = torch.randn(a.n_layer, a.n_local_heads, pos, 64, generator=g).to(torch.bfloat16)
-        v = torch.randn(a.n_layer, a.n_local_heads, pos, 64, generator=g).to(torch.bfloat16)
-        for o in (oa, ob):
-            o.k_cache[:, :, :pos] = k
-            o.v_cache[:, :, :pos] = v
-        tok = torch.tensor([(7 * pos + 3) % a.vocab_size])
-        la, _ = oa.forward(tok, pos)
-        try:
-            om.F.linear = lin_split
-            lb, _ = ob.forward(tok, pos)
-        finally:
-            om.F.linear = orig
-        worst = max(worst, float((la.float() - lb.float()).abs().max()))
-    assert 2e-2 < worst <= 0.125, worst

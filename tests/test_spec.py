@@ -378,3 +378,24 @@ def test_lookup_draft_incremental_index_equals_fresh():
         fresh = LookupDraft(width=3, depth=4)
         assert d.tree(ctx, None) == fresh.tree(list(ctx), None)
         assert d.chain(ctx, None, 5) == fresh.chain(list(ctx), None, 5)
+
+
+def test_lookup_draft_reused_on_a_different_context():
+    """A reused LookupDraft given a context that shares the previous one's length, first and last
+    tokens but differs inside must propose what a fresh draft proposes (no stale n-gram
+    positions), and SpecDecoder-style reset() returns it to a fresh state."""
+    from flint_amd.spec import LookupDraft
+    a = [1, 2, 3, 4, 5, 6, 7, 8, 9, 1, 2, 3, 4, 5, 6, 7, 8, 40, 41, 42, 1, 2, 3, 4, 5, 6, 7, 8]
+    b = list(a)
+    b[9:17] = [50, 51, 52, 53, 54, 55, 56, 57]         # same length, head and tail
+    reused = LookupDraft(max_ngram=3, width=3, depth=4)
+    reused.chain(a, None, 4)
+    reused.tree(a, None)
+    fresh = LookupDraft(max_ngram=3, width=3, depth=4)
+    assert reused.chain(b, None, 4) == fresh.chain(b, None, 4)
+    assert reused.tree(b, None) == LookupDraft(max_ngram=3, width=3, depth=4).tree(b, None)
+    # extension of the indexed context keeps using (and extending) the index
+    ext = b + [9, 1, 2]
+    assert reused.chain(ext, None, 4) == LookupDraft(max_ngram=3, width=3, depth=4).chain(ext, None, 4)
+    reused.reset()
+    assert reused.tree(a, None) == LookupDraft(max_ngram=3, width=3, depth=4).tree(a, None)
