@@ -12,6 +12,7 @@
 // (ratio, ~index) per row, read out by the row's last chunk to finish.
 #include <hip/hip_cooperative_groups.h>
 #include <algorithm>
+#include <mutex>
 #include "fl_common.h"
 
 namespace {
@@ -157,6 +158,13 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float* __restrict__ logi
   const int tid = threadIdx.x, row = blockIdx.x / C, c = blockIdx.x % C;
   const int CH = (V + C - 1) / C, j0 = c * CH, j1 = min(V, j0 + CH);
   SampleWs* ws = wsa + row;
+  // the row's argmax word and arrival count start at zero: cleared here, before the first grid
+  // sync, which orders it before every chunk's use after the last one (so a scratch block that
+  // another call left in any state is valid input)
+  if (c == 0 && tid == 0) {
+    __hip_atomic_store(&ws->best, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&ws->arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   const float* lg = logits + (size_t)row * V;
   float x[SP_PT];
   // x = bf16(bf16(logit) / max(T, 1e-5))  (generate.py:42); max over the chunk
@@ -278,33 +286,25 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float* __restrict__ logi
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperature, int32_t top_k,
-              uint64_t seed, uint64_t offset, const float* noise, int32_t* tokens_out,
-              float* probs_out, void* stream) {
-  if (!logits || !tokens_out || rows < 1 || vocab < 1 || vocab > SAMPLE_MAXV ||
-      top_k < 0)
-    return FL_E_ARG;
-  if (!(temperature == temperature)) return FL_E_ARG;  // NaN
+// Scratch of fl_sample_noalloc: a fixed block per device for FL_MAX_VERIFY rows (2.1 MB), part of
+// the code object, so no call allocates. Host code must not pass `scratch` itself to a kernel (it
+// names a host-side stand-in): its device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) SampleWs scratch[FL_MAX_VERIFY];
+
+std::mutex g_scratch_mu;
+SampleWs* g_scratch_ptr[64] = {};
+
+int sample_launch(const float* logits, int32_t rows, int32_t vocab, float temperature, int32_t top_k,
+                  uint64_t seed, uint64_t offset, const float* noise, int32_t* tokens_out,
+                  float* probs_out, SampleWs* wsp, void* stream) {
   const float tdiv = temperature > 1e-5f ? temperature : 1e-5f;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FL_E_HIP;
-  // per-device scratch, allocated (and zeroed) on the first call on that device and kept until
-  // the process ends; calls on one device must be stream-ordered
-  static SampleWs* ws[64] = {};
-  if (!ws[dev]) {
-    SampleWs* w = nullptr;
-    if (hipMalloc(&w, sizeof(SampleWs) * FL_MAX_VERIFY) != hipSuccess) return FL_E_HIP;
-    if (hipMemset(w, 0, sizeof(SampleWs) * FL_MAX_VERIFY) != hipSuccess) return FL_E_HIP;
-    ws[dev] = w;
-  }
   const int C = std::min(SP_C, std::max(1, (vocab + SP_NT - 1) / SP_NT));  // chunks of <= SP_PT * SP_NT
   if ((vocab + C - 1) / C > SP_PT * SP_NT) return FL_E_ARG;
   int v = vocab, ci = C, tk = top_k;
   uint32_t slo = (uint32_t)seed, shi = (uint32_t)(seed >> 32), olo = (uint32_t)offset, ohi = (uint32_t)(offset >> 32);
   float td = tdiv;
-  SampleWs* wsp = ws[dev];
   for (int r0 = 0; r0 < rows; r0 += FL_MAX_VERIFY) {  // FL_MAX_VERIFY rows per launch (the scratch's rows)
     const int n = std::min(FL_MAX_VERIFY, rows - r0);
     const float* lg = logits + (size_t)r0 * vocab;
@@ -318,6 +318,57 @@ int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperatur
     if (e != hipSuccess) return FL_E_LAUNCH;
   }
   return FL_OK;
+}
+
+bool sample_args_ok(const float* logits, int32_t rows, int32_t vocab, float temperature, int32_t top_k,
+                    int32_t* tokens_out) {
+  return logits && tokens_out && rows >= 1 && vocab >= 1 && vocab <= SAMPLE_MAXV && top_k >= 0 &&
+         temperature == temperature;  // not NaN
+}
+
+}  // namespace
+
+extern "C" {
+
+int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperature, int32_t top_k,
+              uint64_t seed, uint64_t offset, const float* noise, int32_t* tokens_out,
+              float* probs_out, void* stream) {
+  if (!sample_args_ok(logits, rows, vocab, temperature, top_k, tokens_out)) return FL_E_ARG;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FL_E_HIP;
+  // per-device scratch, allocated on the first call on that device and kept until the process
+  // ends; calls on one device must be stream-ordered
+  static SampleWs* ws[64] = {};
+  if (!ws[dev]) {
+    SampleWs* w = nullptr;
+    if (hipMalloc(&w, sizeof(SampleWs) * FL_MAX_VERIFY) != hipSuccess) return FL_E_HIP;
+    if (hipMemset(w, 0, sizeof(SampleWs) * FL_MAX_VERIFY) != hipSuccess) return FL_E_HIP;
+    ws[dev] = w;
+  }
+  return sample_launch(logits, rows, vocab, temperature, top_k, seed, offset, noise, tokens_out,
+                       probs_out, ws[dev], stream);
+}
+
+int fl_sample_noalloc(const float* logits, int32_t rows, int32_t vocab, float temperature,
+                      int32_t top_k, uint64_t seed, uint64_t offset, const float* noise,
+                      int32_t* tokens_out, float* probs_out, void* stream) {
+  if (!sample_args_ok(logits, rows, vocab, temperature, top_k, tokens_out)) return FL_E_ARG;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FL_E_HIP;
+  SampleWs* wsp;
+  {
+    // the device address of this device's copy of `scratch`, looked up once (with the device
+    // current: each device holds its own copy at its own address)
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+      void* p = nullptr;
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return FL_E_HIP;
+      g_scratch_ptr[dev] = reinterpret_cast<SampleWs*>(p);
+    }
+    wsp = g_scratch_ptr[dev];
+  }
+  return sample_launch(logits, rows, vocab, temperature, top_k, seed, offset, noise, tokens_out,
+                       probs_out, wsp, stream);
 }
 
 }  // extern "C"

@@ -174,6 +174,18 @@ int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperatur
               uint64_t seed, uint64_t offset, const float* noise, int32_t* tokens_out,
               float* probs_out, void* stream);
 
+/* fl_sample that allocates nothing: the same arguments, results and limits (vocab <= 65536,
+ * FL_E_ARG beyond), bit-identical output, but its scratch (per-row histograms, partial sums, the
+ * argmax word: 2.1 MB for FL_MAX_VERIFY rows) is a fixed device array of the library, one per GPU,
+ * held until the process ends. No hipMalloc, hipFree or allocating library call. Calls on one GPU
+ * share that array: calls that overlap on one GPU (other streams or threads) race; keep them
+ * stream-ordered. The first call on a device looks the array's address up (no allocation).
+ * No counterpart in the reference: for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). */
+int fl_sample_noalloc(const float* logits, int32_t rows, int32_t vocab, float temperature,
+                      int32_t top_k, uint64_t seed, uint64_t offset, const float* noise,
+                      int32_t* tokens_out, float* probs_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
