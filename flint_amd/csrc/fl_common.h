@@ -55,26 +55,28 @@ __device__ __forceinline__ DqConst dq_const(uint32_t szw) {
   return k;
 }
 
-// Step j (nibbles j and j+4) of four words w0..w3 of one 128-group: o[i] = packed bf16
-// dequantised pair (element 2j, 2j+1) of word i. One asm block so the instruction order is
+// One step (nibbles 0 and 4, i.e. bits 0-3 and 16-19) of four words w0..w3 of one 128-group:
+// o[i] = packed bf16 dequantised pair of word i. SHIFT first moves the words right by 4 in place,
+// so consecutive steps walk the nibble pairs 0..3 of the same running words (no copy of the
+// original words is kept, which a shift by 4j from the original would need). One asm block so the instruction order is
 // fixed: the three-address (VOP3P) v_dot2_f32_bf16 needs no copy of its shared accumulator, and
 // the order puts at least three instructions between every write and its first read (a dot
 // reading a VGPR written just before it, and any read of a dot's result right after the dot,
 // need wait states that the compiler does not insert across inline asm), so the block needs no
 // s_nop of its own. It ends with two wait states, so the outputs may feed an MFMA or a VOP3P
 // instruction right away (the compiler sees no VALU write inside the asm).
-template <int J>
-__device__ __forceinline__ void dq_step4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+template <bool SHIFT>
+__device__ __forceinline__ void dq_step4(uint32_t& w0, uint32_t& w1, uint32_t& w2, uint32_t& w3,
                                          const DqConst& k, uint32_t magic, uint32_t one_lo,
                                          uint32_t one_hi, uint32_t (&o)[4]) {
   uint32_t m0, m1, m2, m3, p00, p01, p10, p11, p20, p21, p30, p31, p0, p1, p2, p3;
   uint32_t d00, d01, d10, d11, d20, d21, d30, d31;
-  if (J > 0) {
-    asm("v_lshrrev_b32 %0, %4, %0\n\t"
-        "v_lshrrev_b32 %1, %4, %1\n\t"
-        "v_lshrrev_b32 %2, %4, %2\n\t"
-        "v_lshrrev_b32 %3, %4, %3"
-        : "+v"(w0), "+v"(w1), "+v"(w2), "+v"(w3) : "I"(4 * J));
+  if (SHIFT) {
+    asm("v_lshrrev_b32 %0, 4, %0\n\t"
+        "v_lshrrev_b32 %1, 4, %1\n\t"
+        "v_lshrrev_b32 %2, 4, %2\n\t"
+        "v_lshrrev_b32 %3, 4, %3"
+        : "+v"(w0), "+v"(w1), "+v"(w2), "+v"(w3));
   }
   asm("v_and_or_b32 %[m0], %[w0], %[mask], %[magic]\n\t"
       "v_and_or_b32 %[m1], %[w1], %[mask], %[magic]\n\t"
@@ -122,10 +124,11 @@ __device__ __forceinline__ void dq_step4(uint32_t w0, uint32_t w1, uint32_t w2, 
 __device__ __forceinline__ void dq32(const uint4 w, const DqConst& k, uint32_t (&d)[4][4]) {
   const uint32_t magic = 0x43004300u;  // bf16 pair (128, 128)
   const uint32_t one_lo = 0x00003F80u, one_hi = 0x3F800000u;  // bf16 pairs (1, 0), (0, 1)
-  dq_step4<0>(w.x, w.y, w.z, w.w, k, magic, one_lo, one_hi, d[0]);
-  dq_step4<1>(w.x, w.y, w.z, w.w, k, magic, one_lo, one_hi, d[1]);
-  dq_step4<2>(w.x, w.y, w.z, w.w, k, magic, one_lo, one_hi, d[2]);
-  dq_step4<3>(w.x, w.y, w.z, w.w, k, magic, one_lo, one_hi, d[3]);
+  uint32_t a = w.x, b = w.y, c = w.z, e = w.w;  // running words, shifted by 4 per step
+  dq_step4<false>(a, b, c, e, k, magic, one_lo, one_hi, d[0]);
+  dq_step4<true>(a, b, c, e, k, magic, one_lo, one_hi, d[1]);
+  dq_step4<true>(a, b, c, e, k, magic, one_lo, one_hi, d[2]);
+  dq_step4<true>(a, b, c, e, k, magic, one_lo, one_hi, d[3]);
 }
 
 // dot of one 16-byte chunk (32 int4 elements of one 128-group) with 32 bf16 x values

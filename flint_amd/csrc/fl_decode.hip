@@ -113,6 +113,17 @@ __device__ __forceinline__ int grid_here() {
 
 __device__ __forceinline__ uint32_t tag_of(uint32_t epoch) { return epoch % 65535u + 1u; }
 
+// The launch's parameters read in place from the kernel-argument segment through a pointer the
+// compiler cannot follow across the empty asm: each use becomes a scalar load where it is needed
+// instead of a value held in an SGPR for the whole layer loop (the kernel's live scalar values
+// otherwise exceed the SGPR file and are parked in VGPR lanes, each restore a VALU instruction).
+__device__ __forceinline__ const DecodeParams& params_here() {
+  typedef const __attribute__((address_space(4))) DecodeParams KParams;
+  KParams* k = (KParams*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(k));
+  return *(const DecodeParams*)k;
+}
+
 __device__ __forceinline__ void row_range(int n, int wg, int G, int& r0, int& rows) {
   int R = (n + G - 1) / G;
   R += (R & 1);
@@ -921,7 +932,9 @@ __device__ __forceinline__ void residual_pair(const DecodeParams& p, int r0, int
 }
 
 template <class C>
-__global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
+__global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
+  (void)pv;  // read through params_here()
+  const DecodeParams& p = params_here();
   static_assert(PD_QKV <= C::QKV && PD_O <= C::O && PD_D + C::PR_D <= C::D &&
                     C::G3 + PD_GU + C::PR_GU <= C::NPRE_GU && C::NPRE_GU <= C::GU,
                 "chunk budget");
@@ -981,7 +994,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams p) {
   row_range(NQKV, wg, G, r0, rows);
   gemv_load(p.w.wqkv_q, p.w.wqkv_sz, r0, rows, D, map_qkv(rows), w_qkv, s_qkv);
 
-  for (int l = 0; l < p.NL; ++l) {
+  for (int l = 0; l < params_here().NL; ++l) {
+    const DecodeParams& p = params_here();
     const uint32_t e0 = p.epoch + 5u * (uint32_t)l;
     const uint32_t t_prev = tag_of(e0 - 1), t_qkv = tag_of(e0), t_attn = tag_of(e0 + 1),
                    t_h1 = tag_of(e0 + 2), t_act = tag_of(e0 + 3), t_h2 = tag_of(e0 + 4);
@@ -1604,7 +1618,9 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
   }
 }
 
-__global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
+__global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
+  (void)pv;  // read through params_here()
+  const DecodeParams& p = params_here();
   extern __shared__ __align__(16) unsigned char vsm[];
   const int tid = threadIdx.x, wg = blockIdx.x, G = gridDim.x;
   const int D = p.D, F = p.F, NH = p.NH, NKV = p.NKV, M = p.M, pos = p.pos;
@@ -1637,7 +1653,8 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams p) {
     return r;
   };
 
-  for (int l = 0; l < p.NL; ++l) {
+  for (int l = 0; l < params_here().NL; ++l) {
+    const DecodeParams& p = params_here();
     const uint32_t e0 = p.epoch + 5u * (uint32_t)l;
     const uint32_t t_prev = tag_of(e0 - 1), t_qkv = tag_of(e0), t_attn = tag_of(e0 + 1),
                    t_h1 = tag_of(e0 + 2), t_act = tag_of(e0 + 3), t_h2 = tag_of(e0 + 4);

@@ -4,6 +4,9 @@
         from `rocprofv3 --kernel-trace --stats -f csv`: the per-kernel stats table and, for the
         named kernel, the average duration of its last N dispatches (the timed window of a
         bench run, whose earlier dispatches are prefill / warmup at other context lengths);
+    python -m flint_amd.rocprof_summary --pmc <dir> [<dir> ...] --kernel k_decode --last N
+        from `rocprofv3 --pmc ...` runs: every counter's mean per dispatch over the kernel's last N
+        dispatches, and the same counters for the last device copy (copyBuffer) if there is one;
     python -m flint_amd.rocprof_summary --traffic <fetch dir> <write dir> --copy-bytes B ...
         from two `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of a bench command that
         ends with a device-to-device copy of B bytes: HBM bytes per dispatch of the kernel, each
@@ -77,6 +80,31 @@ def _per_dispatch(rows, pattern):
     return [vals[k] for k in sorted(vals)]
 
 
+def pmc(dirs, kernel, last, copy_kernel="copyBuffer"):
+    out = []
+    for d in dirs:
+        path, rows = _counter_rows(d)
+        per, names = {}, {}
+        for r in rows:
+            k = int(r.get("Dispatch_Id") or r.get("Correlation_Id") or 0)
+            names[k] = r["Kernel_Name"]
+            c = per.setdefault(k, {})
+            c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        ks = [k for k in sorted(per) if kernel in names[k]]
+        ks = ks[-last:] if last else ks
+        if not ks:
+            raise RuntimeError(f"no {kernel} dispatches in {path}")
+        out.append(f"{os.path.basename(path)}: {kernel}, mean of last {len(ks)} dispatches")
+        for cn in sorted(per[ks[0]]):
+            out.append(f"  {cn:28s} {sum(per[k][cn] for k in ks) / len(ks):18.1f}")
+        cp = [k for k in sorted(per) if copy_kernel in names[k]]
+        if cp:
+            out.append(f"  (device copy, {copy_kernel}):")
+            for cn in sorted(per[cp[-1]]):
+                out.append(f"  {cn:28s} {per[cp[-1]][cn]:18.1f}")
+    return "\n".join(out)
+
+
 def traffic(fetch_dir, write_dir, kernel, last, copy_bytes, config, copy_kernel="copyBuffer"):
     out = [f"config: {config}"]
     tot = 0.0
@@ -105,10 +133,13 @@ def main(argv=None):
     ap.add_argument("--last", type=int, default=0)
     ap.add_argument("--skip-last", type=int, default=0)
     ap.add_argument("--traffic", action="store_true")
+    ap.add_argument("--pmc", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0)
     ap.add_argument("--config", default="")
     a = ap.parse_args(argv)
-    if a.traffic:
+    if a.pmc:
+        print(pmc(a.dir, a.kernel, a.last))
+    elif a.traffic:
         print(traffic(a.dir[0], a.dir[1], a.kernel, a.last, a.copy_bytes, a.config))
     else:
         print(summarise(a.dir[0], a.kernel, a.last, skip_last=a.skip_last))
