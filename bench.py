@@ -289,6 +289,31 @@ def long_context(model, args, dev, ctx=8192, steps=128):
             "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def fused_sampling(model, args, dev, pos0, steps=64):
+    """Sampled decode (fl_decode_sample: temperature 0.8, top-k 200, the token drawn inside the
+    decode launch) against greedy decode over the same positions, tokens chained on the device:
+    time per step of each and the difference (the cost of the fused sampling)."""
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    seq = torch.ones(steps + 1, dtype=torch.int32, device=dev)
+    res = {}
+    for name in ("greedy", "sampled"):
+        for rep in range(2):  # the first pass warms up
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for i in range(steps):
+                if name == "greedy":
+                    model.decode_step(seq[i:i + 1], pos0 + i, token_out=seq[i + 1:i + 2])
+                else:
+                    model.decode_sample(seq[i:i + 1], pos0 + i, 0.8, 200, seed=1, token_out=seq[i + 1:i + 2])
+            e1.record(stream)
+            torch.cuda.synchronize()
+        res[f"{name}_us"] = round(e0.elapsed_time(e1) * 1000.0 / steps, 1)
+    model.check()
+    res["fused_sampling_us"] = round(res["sampled_us"] - res["greedy_us"], 1)
+    return res
+
+
 def sampling_latency(args, dev, reps=50):
     """fl_sample on one logit row of the model's vocabulary (temperature 0.8, top_k 200, Philox
     noise), events around `reps` back-to-back launches, beside the same with top_k off."""
@@ -418,7 +443,8 @@ def main():
         log(f"config 1 (fl_gemv_int4, {gemv['rotation_bytes'] / 1e9:.2f} GB rotation): {gemv['shapes']}")
 
     sampling = sampling_latency(args, dev)
-    log(f"fl_sample over {args.vocab_size} logits: {sampling}")
+    sampling.update(fused_sampling(model, args, dev, a.ctx))
+    log(f"sampling over {args.vocab_size} logits: {sampling}")
 
     if a.copy_probe_mb > 0:
         n = a.copy_probe_mb * (1 << 20)

@@ -27,7 +27,7 @@ EXPORTS = [
     "fl_version", "fl_device_info", "fl_quantize_int4", "fl_dequant_int4", "fl_gemv_int4",
     "fl_gemm_int4", "fl_state_create", "fl_state_destroy", "fl_state_reset", "fl_state_check",
     "fl_state_profile", "fl_state_buffers",
-    "fl_decode_step", "fl_decode_hidden", "fl_verify", "fl_kv_move", "fl_sample",
+    "fl_decode_step", "fl_decode_sample", "fl_decode_hidden", "fl_verify", "fl_kv_move", "fl_sample",
     "fl_sample_noalloc",
 ]
 
@@ -86,6 +86,8 @@ def load(path=LIB_PATH):
         "fl_state_buffers": ([vp, vp, vp, vp, vp], i32),
         "fl_decode_step": ([ctypes.POINTER(Weights), vp, vp, i32, vp, vp, vp, vp], i32),
         "fl_decode_hidden": ([ctypes.POINTER(Weights), vp, vp, i32, vp, vp, vp, vp], i32),
+        "fl_decode_sample": ([ctypes.POINTER(Weights), vp, vp, i32, f32, i32, ctypes.c_uint64, ctypes.c_uint64,
+                              vp, vp, vp, vp], i32),
         "fl_verify": ([ctypes.POINTER(Weights), vp, vp, i32, vp, vp, i32, vp, vp, vp, vp], i32),
         "fl_kv_move": ([vp, vp, vp, i32, vp], i32),
         "fl_sample": ([vp, i32, i32, f32, i32, ctypes.c_uint64, ctypes.c_uint64, vp, vp, vp, vp], i32),

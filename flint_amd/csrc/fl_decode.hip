@@ -89,6 +89,14 @@ struct DecodeParams {
   uint32_t epoch;              // epoch of this launch's first phase (5 per layer)
   unsigned long long* prof;    // optional per-workgroup phase timestamps (100 MHz clock)
   int prof_slots;
+  // decode only, fused sampling: samp_tdiv > 0 samples the token (temperature divisor
+  // max(T, 1e-5), top-k when 0 < samp_topk < V, Philox4x32-10 noise keyed by seed at counter
+  // (index, 0, offset)); samp_tdiv = 0 takes the greedy argmax
+  float samp_tdiv;
+  int samp_topk;
+  uint32_t seed_lo, seed_hi, off_lo, off_hi;
+  uint32_t* shist;              // [grid][256] tagged per-workgroup histogram counts (count | tag << 16)
+  unsigned long long* sword;    // tagged words: [256] bin totals, [grid] maxima, [grid] partial sums
   // verify only: M tokens, their RoPE depths, the [M][M] tree mask, per-token argmax output
   int M;
   const int32_t* tokens;
@@ -931,6 +939,119 @@ __device__ __forceinline__ void residual_pair(const DecodeParams& p, int r0, int
              (unsigned long long)n0 | ((unsigned long long)n1 << 32));
 }
 
+// Workgroup reductions in a fixed order (wave tree, then the waves' values in wave order), so every
+// workgroup computes the bit-identical result from the same inputs. red: NWAVE floats of LDS.
+__device__ __forceinline__ float wg_max_fixed(float v, float* red) {
+  const int tid = tid_here();
+  v = wave_max(v);
+  lds_barrier();
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  lds_barrier();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < NWAVE; ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+__device__ __forceinline__ float wg_sum_fixed(float v, float* red) {
+  const int tid = tid_here();
+  v = wave_sum(v);
+  lds_barrier();
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  lds_barrier();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < NWAVE; ++w) r += red[w];
+  return r;
+}
+__device__ __forceinline__ uint32_t wait_u32(const DecodeParams& p, const uint32_t* a, uint32_t tag) {
+  auto ld = [a]() { return ld_coh_u32(a); };
+  auto ok = [tag](uint32_t v) { return (v >> 16) == tag; };
+  uint32_t v = ld();
+  if (!ok(v)) v = spin_until(p, v, ok, ld);
+  return v;
+}
+
+// Temperature / top-k sampling fused into the decode launch, after the LM head (reference
+// engine/generate.py:38-55 logits_to_probs + multinomial_sample_one_no_sync, with the same steps
+// and bf16 rounding points as the standalone sampler k_sample): thread t of workgroup w holds
+// x = bf16(logit / T) of LM-head row r0 + t (xl: the rows' logits in LDS). The steps that need
+// the whole vocabulary exchange one value per workgroup through tagged words (tags of epochs
+// e .. e + 5 after the launch's layers): the maxima; for top-k, two radix passes over the
+// 16-bit ordered keys (each workgroup's 256-bin histogram; bin b's total summed by workgroup
+// b % G; every workgroup reads the 256 totals and selects the pivot's bin); the partial sums of
+// exp(x - max) over the kept entries, read by every workgroup and summed in one fixed order.
+// Returns this thread's sample key (bf16(p / q) bits << 32 | ~index; 0 for dropped entries): the
+// token is the first index of the largest key over the vocabulary.
+__device__ unsigned long long sample_epilogue(const DecodeParams& p, int r0, int rows, const float* xl,
+                                              int* hist, int* sel, float* red) {
+  const int tid = tid_here(), G = grid_here(), wg = blockIdx.x;
+  const uint32_t e = p.epoch + 5u * (uint32_t)p.NL;
+  unsigned long long* tot = p.sword;
+  unsigned long long* wmax = p.sword + 256;
+  unsigned long long* wsum = p.sword + 256 + G;
+  const bool on = tid < rows;
+  const int j = r0 + tid;
+  const float x = on ? rbf(xl[tid] / p.samp_tdiv) : -INFINITY;  // generate.py:42
+  const uint32_t key = bf_key(x);
+  const float lmx = wg_max_fixed(x, red);
+  if (tid == 0)
+    st_coh_u64(wmax + wg, (unsigned long long)__float_as_uint(lmx) | ((unsigned long long)tag_of(e) << 32));
+  uint32_t pivot = 0;
+  const bool topk = p.samp_topk > 0 && p.samp_topk < p.V;
+  if (topk) {  // generate.py:44-47: keys below the k-th largest drop out, ties with it stay
+    int k = p.samp_topk;
+    for (int pass = 0; pass < 2; ++pass) {
+      const uint32_t th = tag_of(e + 1 + 2 * pass), tt = tag_of(e + 2 + 2 * pass);
+      if (tid < 256) hist[tid] = 0;
+      lds_barrier();
+      if (on && (pass == 0 || (key >> 8) == (pivot >> 8)))
+        atomicAdd(&hist[pass == 0 ? (key >> 8) : (key & 0xFFu)], 1);
+      lds_barrier();
+      if (tid < 256) st_coh_u32(p.shist + (size_t)wg * 256 + tid, (uint32_t)hist[tid] | (th << 16));
+      // bin b's total over the workgroups (integer counts, exact in fp32: any order)
+      for (int b = wg; b < 256; b += G) {
+        float c = 0.0f;
+        for (int u = tid; u < G; u += NT) c += (float)(wait_u32(p, p.shist + (size_t)u * 256 + b, th) & 0xFFFFu);
+        c = wg_sum_fixed(c, red);
+        if (tid == 0) st_coh_u64(tot + b, (unsigned long long)(uint32_t)c | ((unsigned long long)tt << 32));
+      }
+      lds_barrier();
+      if (tid < 256) hist[tid] = (int)(uint32_t)wait_pair(p, tot + tid, tt);
+      lds_barrier();
+      int above = 0;
+      const int bin = select_bin(hist, k, &above, sel);
+      k -= above;
+      pivot = pass == 0 ? ((uint32_t)bin << 8) : (pivot | (uint32_t)bin);
+      lds_barrier();
+    }
+  }
+  // the vocabulary's max (always kept), then exp(x - max) summed over the kept entries
+  float gm = -INFINITY;
+  for (int u = tid; u < G; u += NT) gm = fmaxf(gm, __uint_as_float((uint32_t)wait_pair(p, wmax + u, tag_of(e))));
+  gm = wg_max_fixed(gm, red);
+  const bool kept = on && (!topk || key >= pivot);
+  const float ex = kept ? expf(x - gm) : 0.0f;
+  const float ls = wg_sum_fixed(ex, red);
+  const uint32_t ts = tag_of(e + 5);
+  if (tid == 0) st_coh_u64(wsum + wg, (unsigned long long)__float_as_uint(ls) | ((unsigned long long)ts << 32));
+  float sp = 0.0f;
+  for (int u = tid; u < G; u += NT) sp += __uint_as_float((uint32_t)wait_pair(p, wsum + u, ts));
+  const float sum = wg_sum_fixed(sp, red);  // the same fixed order in every workgroup
+  // p = bf16(exp(x - max) / sum); the first index of the largest bf16(p / q) (generate.py:36-38)
+  unsigned long long best = 0ull;
+  if (kept) {
+    const float pr = rbf(ex / sum);
+    if (pr != 0.0f) {  // a ratio of 0 never beats the kept maximum's
+      const uint32_t r = philox_x0((uint32_t)j, 0u, p.off_lo, p.off_hi, p.seed_lo, p.seed_hi);
+      const double u = ((double)(r >> 8) + 0.5) * (1.0 / 16777216.0);
+      const float q = rbf((float)(-log(u)));
+      const float ratio = rbf(pr / q);
+      best = ((unsigned long long)__float_as_uint(ratio) << 32) | (0xFFFFFFFFu - (uint32_t)j);
+    }
+  }
+  return best;
+}
+
 template <class C>
 __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
   (void)pv;  // read through params_here()
@@ -1218,6 +1339,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
         // logits = bf16(bf16(x . E^T) / logits_scaling)  (engine/model.py:144)
         const float lg = rbf(rbf(acc) / p.logits_scaling);
         if (p.logits && lane == 0) p.logits[r] = lg;
+        if (p.samp_tdiv > 0.0f && lane == 0) ws[rb + rr] = lg;  // the rows' logits for sampling
         best = u64max(best, amax_key(lg, (uint32_t)r));
       }
     }
@@ -1233,6 +1355,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
     lm_compute(ea, rb);
     if (rb + 2 * STEP < rows) lm_load(ea, rb + 2 * STEP);
     if (rb + STEP < rows) lm_compute(eb, rb + STEP);
+  }
+  if (p.samp_tdiv > 0.0f) {  // the sampled token instead of the greedy argmax
+    lds_barrier();             // the rows' logits are in ws
+    int* shl = reinterpret_cast<int*>(ws + WS_FLOATS - 512);
+    best = sample_epilogue(p, r0, rows, ws, shl, shl + 256, red);
+    best = wave_max_u64(best);
   }
   if (lane == 0) kred[wave] = best;
   lds_barrier();
@@ -2007,6 +2135,8 @@ struct fl_state {
   uint32_t *h, *attn, *act;
   unsigned long long* qkv;
   unsigned long long* part;
+  uint32_t* shist;              // fused sampling exchange: per-workgroup histograms
+  unsigned long long* sword;    // ... bin totals, maxima, partial sums
   int att_spw;
   int coop;       // launch with hipLaunchCooperativeKernel (else a plain launch, the default)
   const void* kdec;  // the k_decode instantiation whose chunk budget fits the model
@@ -2134,6 +2264,8 @@ DecodeParams base_params(const fl_weights* w, fl_state* st, int pos) {
   p.attn = st->attn;
   p.act = st->act;
   p.part = st->part;
+  p.shist = st->shist;
+  p.sword = st->sword;
   p.att_spw = st->att_spw;
   p.amax = st->amax;
   p.done = st->done;
@@ -2158,11 +2290,23 @@ DecodeParams base_params(const fl_weights* w, fl_state* st, int pos) {
 }  // namespace
 
 namespace {
+struct SampleArgs {
+  float tdiv;  // 0: greedy
+  int top_k;
+  uint64_t seed, offset;
+};
 int decode_launch(const fl_weights* w, fl_state* st, const int32_t* token_in, uint16_t* h_io,
-                  int32_t pos, int32_t* token_out, float* logits, uint16_t* feat, void* stream) {
+                  int32_t pos, int32_t* token_out, float* logits, uint16_t* feat, void* stream,
+                  SampleArgs sa = SampleArgs{0.0f, 0, 0, 0}) {
   if (pos < 0 || pos >= st->max_seq || pos >= w->rope_len) return FL_E_POS;
   if (maybe_clear(st, as_stream(stream)) != FL_OK) return FL_E_LAUNCH;
   DecodeParams p = base_params(w, st, pos);
+  p.samp_tdiv = sa.tdiv;
+  p.samp_topk = sa.top_k;
+  p.seed_lo = (uint32_t)sa.seed;
+  p.seed_hi = (uint32_t)(sa.seed >> 32);
+  p.off_lo = (uint32_t)sa.offset;
+  p.off_hi = (uint32_t)(sa.offset >> 32);
   p.token_in = token_in;
   p.h_io = h_io;
   p.token_out = token_out;
@@ -2279,6 +2423,8 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   if (rc == FL_OK) rc = uc_alloc(st, &st->act, (size_t)F * FL_MAX_VERIFY);
   if (rc == FL_OK)
     rc = uc_alloc(st, &st->part, (size_t)d->n_head * MAX_SLICES * 66 * FL_MAX_VERIFY);
+  if (rc == FL_OK) rc = uc_alloc(st, &st->shist, (size_t)G * 256);
+  if (rc == FL_OK) rc = uc_alloc(st, &st->sword, (size_t)256 + 2 * G);
   if (rc == FL_OK) rc = dev_alloc(st, &st->amax, FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->done, 1);
   if (rc == FL_OK) rc = dev_alloc(st, &st->err, 1);
@@ -2360,6 +2506,22 @@ int fl_decode_hidden(const fl_weights* w, fl_state* st, uint16_t* h, int32_t pos
                      int32_t* token_out, float* logits, uint16_t* feat, void* stream) {
   if (!st || !h || !weights_ok(w)) return FL_E_ARG;
   return decode_launch(w, st, nullptr, h, pos, token_out, logits, feat, stream);
+}
+
+int fl_decode_sample(const fl_weights* w, fl_state* st, const int32_t* token_in, int32_t pos,
+                     float temperature, int32_t top_k, uint64_t seed, uint64_t offset,
+                     int32_t* token_out, float* logits, uint16_t* feat, void* stream) {
+  if (!st || !token_in || !token_out || !weights_ok(w) || top_k < 0) return FL_E_ARG;
+  if (!(temperature == temperature) || st->d.vocab > 65536) return FL_E_ARG;
+  // one LM-head row per thread of a workgroup in the sampling epilogue
+  {
+    int R = (st->d.vocab + st->grid - 1) / st->grid;
+    R += (R & 1);
+    if (R > NT) return FL_E_ARG;
+  }
+  const float tdiv = temperature > 1e-5f ? temperature : 1e-5f;
+  return decode_launch(w, st, token_in, nullptr, pos, token_out, logits, feat, stream,
+                       SampleArgs{tdiv, top_k, seed, offset});
 }
 
 int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t m,

@@ -19,69 +19,6 @@ namespace {
 
 constexpr int SAMPLE_MAXV = 65536;            // vocab limit
 
-// Philox4x32-10 (Salmon et al., SC 2011): 10 rounds of two 32x32->64 multiplies, Weyl key bumps
-__device__ __forceinline__ uint32_t philox_x0(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
-                                              uint32_t k0, uint32_t k1) {
-#pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    if (r) {
-      k0 += 0x9E3779B9u;
-      k1 += 0xBB67AE85u;
-    }
-    const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
-    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
-    c0 = n0;
-    c1 = (uint32_t)p1;
-    c2 = n2;
-    c3 = (uint32_t)p0;
-  }
-  return c0;
-}
-
-// ordered 16-bit key of a bf16 value: larger value <-> larger key
-__device__ __forceinline__ uint32_t bf_key(float x) {
-  const uint32_t b = __float_as_uint(x) >> 16;
-  return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
-}
-
-// The bin of a 256-bin histogram (counts in hist) that holds the k-th largest key, scanning from
-// bin 255 down: returns the bin and, through above, how many keys lie in higher bins. Wave 0
-// scans (lane l owns bins 4l..4l+3); the result goes to every thread through sel.
-__device__ __forceinline__ int select_bin(const int* hist, int k, int* above, int* sel) {
-  const int tid = threadIdx.x;
-  if (tid < 64) {
-    const int b0 = 4 * tid;
-    const int c0 = hist[b0], c1 = hist[b0 + 1], c2 = hist[b0 + 2], c3 = hist[b0 + 3];
-    const int own = c0 + c1 + c2 + c3;
-    int incl = own;  // sum over lanes >= tid
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int t = __shfl_down(incl, o, 64);
-      if (tid + o < 64) incl += t;
-    }
-    const int hi = incl - own;  // keys in bins above this lane's four
-    if (hi < k && incl >= k) {
-      // the highest of the four bins where the running count from the top reaches k
-      int bin, acc;
-      if (hi + c3 >= k) {
-        bin = b0 + 3, acc = hi;
-      } else if (hi + c3 + c2 >= k) {
-        bin = b0 + 2, acc = hi + c3;
-      } else if (hi + c3 + c2 + c1 >= k) {
-        bin = b0 + 1, acc = hi + c3 + c2;
-      } else {
-        bin = b0, acc = hi + c3 + c2 + c1;
-      }
-      sel[0] = bin;
-      sel[1] = acc;
-    }
-  }
-  __syncthreads();
-  const int bin = sel[0];
-  *above = sel[1];
-  return bin;
-}
-
 constexpr int SP_NT = 256;                     // threads per chunk workgroup
 constexpr int SP_C = 64;                       // chunks per row (at most)
 constexpr int SP_PT = 4;                       // values per thread: chunk <= 1024, vocab <= 65536

@@ -77,10 +77,12 @@ def decode_one_token(model, x, input_pos, logits=None, temperature=None, top_k=N
     if logits is None:
         logits = torch.empty(model.config.vocab_size, dtype=torch.float32, device=model.device)
     out = torch.empty(1, dtype=torch.int32, device=model.device)
-    model.decode_step(x.reshape(-1)[:1].to(torch.int32), pos, token_out=out, logits=logits)
-    if temperature is not None or top_k is not None:
+    tok = x.reshape(-1)[:1].to(torch.int32)
+    if temperature is not None or top_k is not None:  # sampled in the decode launch itself
         t = 1.0 if temperature is None else temperature
-        out, _ = sample(logits, t, top_k, seed=seed, offset=pos)
+        model.decode_sample(tok, pos, t, top_k, seed=seed, offset=pos, token_out=out, logits=logits)
+    else:
+        model.decode_step(tok, pos, token_out=out, logits=logits)
     return out, logits
 
 
@@ -101,9 +103,9 @@ def decode_n_tokens(model, cur_token, input_pos, num_new_tokens, out=None):
 @torch.no_grad()
 def generate(model, prompt, max_new_tokens, temperature=None, top_k=None, seed=0):
     """Generate: returns int32 device [T + max_new_tokens] = prompt + new tokens. Greedy (the
-    argmax fused into the decode kernel) unless temperature or top_k is given; then each step's
-    logits go through fl_sample with the step's position as the noise counter. Tokens stay on
-    the device either way (no host synchronisation in the loop)."""
+    argmax fused into the decode kernel) unless temperature or top_k is given; then each step
+    samples in the decode launch itself (fl_decode_sample) with the step's position as the noise
+    counter. Tokens stay on the device either way (no host synchronisation in the loop)."""
     prompt = prompt.reshape(-1).to(device=model.device, dtype=torch.int32)
     T = prompt.numel()
     model.setup_caches(1, T + max_new_tokens)
@@ -112,12 +114,12 @@ def generate(model, prompt, max_new_tokens, temperature=None, top_k=None, seed=0
     if T > 1:
         prefill(model, prompt[:-1], 0)
     sampled = temperature is not None or top_k is not None
-    logits = torch.empty(model.config.vocab_size, dtype=torch.float32, device=model.device) if sampled else None
+    t = 1.0 if temperature is None else temperature
     # the last prompt token produces the first new token
     for i in range(max_new_tokens):
         p = T - 1 + i
-        model.decode_step(seq[p:p + 1], p, token_out=seq[p + 1:p + 2], logits=logits)
         if sampled:
-            tok, _ = sample(logits, 1.0 if temperature is None else temperature, top_k, seed=seed, offset=p)
-            seq[p + 1:p + 2] = tok
+            model.decode_sample(seq[p:p + 1], p, t, top_k, seed=seed, offset=p, token_out=seq[p + 1:p + 2])
+        else:
+            model.decode_step(seq[p:p + 1], p, token_out=seq[p + 1:p + 2])
     return seq

@@ -193,6 +193,27 @@ class Transformer:
                   _lib.ptr(token_out), _lib.ptr(logits), _lib.ptr(feat), _lib.stream_ptr())
         return token_out
 
+    def decode_sample(self, token, pos, temperature=1.0, top_k=None, seed=0, offset=None,
+                      token_out=None, logits=None, feat=None):
+        """One decode step whose token is sampled in the same launch (temperature / top-k, reference
+        engine/generate.py:38-55): Philox noise keyed by seed at counter offset (default: pos).
+        Returns token_out (int32 device [1])."""
+        if self._state is None:
+            raise RuntimeError("call setup_caches first")
+        if token_out is None:
+            token_out = self._tok_out[:1]
+        for t, dt, nm in ((token, torch.int32, "token"), (token_out, torch.int32, "token_out"),
+                          (logits, torch.float32, "logits"), (feat, torch.bfloat16, "feat")):
+            if t is not None and (not t.is_cuda or t.dtype != dt):
+                raise ValueError(f"{nm} must be a {dt} device tensor")
+        if top_k is not None and int(top_k) < 1:
+            raise ValueError("top_k must be >= 1")
+        off = int(pos) if offset is None else int(offset)
+        _lib.call("fl_decode_sample", _lib.ctypes.byref(self._cw), self._state, _lib.ptr(token), int(pos),
+                  float(temperature), int(top_k or 0), int(seed) & (2 ** 64 - 1), off & (2 ** 64 - 1),
+                  _lib.ptr(token_out), _lib.ptr(logits), _lib.ptr(feat), _lib.stream_ptr())
+        return token_out
+
     def decode_hidden(self, h, pos, token_out=None, logits=None, feat=None):
         """One decode step from a hidden state (reference decode_mega_launch's h argument): h (bf16
         [D] device tensor) is the layer-0 input and holds the final residual afterwards (in place).

@@ -131,24 +131,32 @@ def main(argv=None):
     ap.add_argument("--config", default="flint-3b")
     ap.add_argument("--ctx", type=int, default=512)
     ap.add_argument("--steps", type=int, default=8)
+    ap.add_argument("--verify", type=int, default=0,
+                    help="profile fl_verify of this many chain tokens (at position ctx) instead of decode")
     a = ap.parse_args(argv)
     args = ModelArgs.from_name(a.config)
     dev = torch.device("cuda:0")
     model = Transformer.from_weights(args, synth_weights(args, 0, device=dev), dev)
-    model.setup_caches(1, a.ctx + a.steps + 8)
+    model.setup_caches(1, a.ctx + a.steps + max(a.verify, 0) + 8)
     g = torch.Generator().manual_seed(1234)
     seq = torch.empty(a.ctx + a.steps, dtype=torch.int32, device=dev)
     seq[:a.ctx] = torch.randint(0, args.vocab_size, (a.ctx,), generator=g, dtype=torch.int32).to(dev)
     prefill(model, seq[:a.ctx - 1], 0)
     buf, grid, slots = enable(model)
-    for i in range(a.steps):
-        p = a.ctx - 1 + i
-        model.decode_step(seq[p:p + 1], p, token_out=seq[p + 1:p + 2])
+    if a.verify:
+        toks = torch.randint(0, args.vocab_size, (a.verify,), generator=g, dtype=torch.int32).to(dev)
+        for _ in range(a.steps):
+            model.verify(toks, a.ctx)
+        label = f"{a.config} k_verify M={a.verify} at ctx {a.ctx}, {grid} workgroups"
+    else:
+        for i in range(a.steps):
+            p = a.ctx - 1 + i
+            model.decode_step(seq[p:p + 1], p, token_out=seq[p + 1:p + 2])
+        label = f"{a.config} k_decode at ctx {a.ctx + a.steps - 1}, {grid} workgroups"
     model.check()
     disable(model)
     res = analyse(buf, grid, slots, args.n_layer)
-    print(format_report(res, args.n_layer, f"{a.config} k_decode at ctx {a.ctx + a.steps - 1}, "
-                                           f"{grid} workgroups"))
+    print(format_report(res, args.n_layer, label))
     model.close()
 
 

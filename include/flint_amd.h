@@ -131,6 +131,18 @@ int fl_state_check(fl_state* st, void* stream);
 int fl_decode_step(const fl_weights* w, fl_state* st, const int32_t* token_in, int32_t pos,
                    int32_t* token_out, float* logits, uint16_t* feat, void* stream);
 
+/* The same decode step with the token SAMPLED in the same launch instead of the greedy argmax:
+ * x = bf16(logit / max(temperature, 1e-5)); with 0 < top_k < vocab every x below the top_k-th
+ * largest drops out (ties with it stay); p = bf16(softmax(x)); the token is the first index of
+ * the largest bf16(p / q), q = bf16(-log u), u from Philox4x32-10 keyed by seed at counter
+ * (index, 0, offset low, offset high) — the same steps as fl_sample on this step's logits (the
+ * softmax sum runs in another order, so p may differ by a bf16 ulp). vocab <= 65536.
+ * Replaces reference engine/generate.py:62-66 decode_one_token with its sample (:52-55:
+ * logits_to_probs + multinomial_sample_one_no_sync) fused into the decode step. */
+int fl_decode_sample(const fl_weights* w, fl_state* st, const int32_t* token_in, int32_t pos,
+                     float temperature, int32_t top_k, uint64_t seed, uint64_t offset,
+                     int32_t* token_out, float* logits, uint16_t* feat, void* stream);
+
 /* The same decode step from a hidden state instead of a token: h (device, bf16 [D]) is the
  * layer-0 input as it is (no embedding lookup, no embedding multiplier) and receives the final
  * residual (before the final norm) when the launch completes, in place. token_out (greedy argmax),

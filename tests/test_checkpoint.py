@@ -77,9 +77,8 @@ def test_interleaved_to_hf_inverts_the_permute():
         assert torch.equal(interleaved_to_hf(w[hf_to_interleaved_perm(nh, hd)], nh, hd), w)
 
 
-def test_gptfast_checkpoint_round_trip(tmp_path):
-    args = _args()
-    sd = synth_weights(args, seed=4)
+def _gptfast_names(sd, args):
+    """gpt-fast bf16 state dict (convert_hf_checkpoint.py:57-71 names, q/k rows permuted)."""
     hd, D = args.head_dim, args.dim
     gf = {}
     for l in range(args.n_layer):
@@ -96,6 +95,13 @@ def test_gptfast_checkpoint_round_trip(tmp_path):
     gf["norm.weight"] = sd["norm"]
     gf["tok_embeddings.weight"] = sd["embed"]
     gf["output.weight"] = sd["embed"].clone()
+    return gf
+
+
+def test_gptfast_checkpoint_round_trip(tmp_path):
+    args = _args()
+    sd = synth_weights(args, seed=4)
+    gf = _gptfast_names(sd, args)
     torch.save(gf, tmp_path / "model.pth")
     _same(load_gptfast_checkpoint(str(tmp_path / "model.pth"), args), sd)
     q4 = dict(gf)
