@@ -18,7 +18,7 @@ ERRORS = {
     -5: "FL_E_HIP (HIP runtime error)",
     -6: "FL_E_TIMEOUT (an inter-workgroup wait hit its time limit)",
 }
-MAX_VERIFY = 16
+MAX_VERIFY = 32
 HEAD_DIM = 64
 GROUP = 128
 

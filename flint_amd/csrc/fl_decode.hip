@@ -74,7 +74,9 @@ struct DecodeParams {
   uint16_t *kc, *vc;           // [NL, NKV, S, 64] bf16 cache
   uint32_t *h, *attn, *act;    // tagged words: bf16 value | tag << 16
   unsigned long long* qkv;     // tagged NEOX pairs: dim i | dim i+32 << 16 | tag << 32
-  unsigned long long* part;    // attention slice partials (tagged fp32 words)
+  unsigned long long* part;    // attention slice partials / verify down-projection parts (tagged fp32)
+  uint16_t *vh, *vattn, *vact; // verify: bf16 [FL_MAX_VERIFY][D | D | F] rows, ready by vflag
+  uint32_t* vflag;             // verify: ready flags (tag << 16)
   unsigned long long* amax;    // argmax key
   uint32_t* done;              // final arrivals
   int32_t* err;                // abort flag (spin timeout / bad token)
@@ -1381,60 +1383,96 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
 }
 
 // ================================ speculative verify ==================================
-// M <= 16 tokens through all layers in one persistent cooperative launch (reference
-// kernels/verify_mega.cu:106-244 verify_mega<M>): token m sits at cache slot pos+m, takes RoPE
-// position pos+depth[m] and attends to the cache [0, pos) plus the new tokens j with
-// amask[m][j] != 0. Same tag protocol and five phases per layer as k_decode. Every GEMM runs on
-// the matrix cores: a workgroup takes 16-row weight tiles, its 8 waves split the K groups, each
-// lane dequantises one 16-byte chunk per group and feeds four v_mfma_f32_16x16x32_bf16 steps
-// against the M token rows staged in LDS (rows >= M read a zero row), so each weight is read and
-// dequantised once for all M tokens. The tied LM head is an MFMA tile over the bf16 embedding.
+// M <= 32 tokens through all layers in one persistent launch (reference kernels/verify_mega.cu:
+// 106-283 verify_mega<M>, M in {1..16, 20, 24, 28, 32}): token m sits at cache slot pos+m, takes
+// RoPE position pos+depth[m] and attends to the cache [0, pos) plus the new tokens j with
+// amask[m][j] != 0. Five phases per layer as k_decode. Every GEMM runs on the matrix cores: a
+// workgroup takes 16-row weight tiles, its 8 waves split the K groups, each lane dequantises one
+// 16-byte chunk per group and feeds four v_mfma_f32_16x16x32_bf16 steps against up to 16 token
+// rows staged in LDS (rows past the pass's tokens read a zero row); more than 16 tokens take two
+// passes over the phase's tiles. The tied LM head is an MFMA tile over the bf16 embedding.
+//
+// The vectors every workgroup stages (the residual h before the two RMSNorms and the LM head, the
+// attention output before the O projection, a K part of the SwiGLU output before the down
+// projection) go through plain bf16 buffers with one ready flag per producing block (a weight
+// tile, an attention unit): a producer stores its values, waits until they are written
+// (s_waitcnt) and only then stores its flag (the phase's tag); a consumer polls the flags of the
+// blocks it needs, then copies the rows. That is half the bytes of one tagged 32-bit word per
+// value, and those bytes bound these hand-offs: every workgroup reads the same M rows (about
+// 4 TB/s summed over the chip for these reads). q / k / v and the down projection's part sums
+// stay tagged words. Each workgroup keeps its own 16 rows of the residual in LDS for the whole
+// launch, as k_decode keeps them in registers.
+constexpr int VH = 16;  // token rows per pass through a GEMM phase (one MFMA row block)
 
-// dynamic LDS of k_verify: staged token rows [M + 1][D + 8] bf16 (row M stays zero), per-wave
-// tile partials [8][256] floats, then attention staging: q [64], new k [16][64], new v [16][64]
-// (bf16) and the unit's mask row [16]
-inline size_t verify_lds_bytes(int M, int D) {
-  const size_t xs = ((size_t)(M + 1) * (D + 8) * 2 + 15) & ~(size_t)15;
-  return xs + 4 * NWAVE * 256 * 4 + 3 * FL_MAX_VERIFY * 64 * 2 + FL_MAX_VERIFY * FL_MAX_VERIFY;
+// dynamic LDS of k_verify: staged token rows [VH + 1][D + 8] bf16 (row VH stays zero), per-wave
+// tile partials [4][8][256] floats, attention staging (q [VH][64], new k and v [32][64] bf16, the
+// unit's mask rows [VH][32]) and this workgroup's rows of the residual h [32][16] (bf16)
+__host__ __device__ inline size_t verify_xs_bytes(int D) { return ((size_t)(VH + 1) * (D + 8) * 2 + 15) & ~(size_t)15; }
+inline size_t verify_lds_bytes(int D) {
+  return verify_xs_bytes(D) + 4 * NWAVE * 256 * 4 + (size_t)(VH + 2 * FL_MAX_VERIFY) * 64 * 2 +
+         VH * FL_MAX_VERIFY + FL_MAX_VERIFY * 16 * 2;
 }
 
-// Token rows [M, kn] of a tagged exchange buffer (row stride `stride` words, columns k0 ..
-// k0+kn-1) -> bf16 rows of xs, once every word carries `tag`. Each thread requests up to SB
-// 16-byte groups at once (all of them for M <= 6 at D = 2560) and then waits for them one by
-// one. A phase requests its first weight tile before this: a poll that fails is re-sent behind
-// every load already issued, so weights requested after a failed poll delay the next look at
-// the inputs.
-__device__ void stage_rows(const DecodeParams& p, const uint32_t* src, int stride, int M, int k0,
-                           int kn, uint32_t tag, uint16_t* xs, int ld) {
+// verify's ready flags (uint32 words, tag << 16): per O tile (h1), per down tile (h2), per
+// attention unit (token group * NH + head), per gate/up tile (SwiGLU output)
+constexpr int VF_H1 = 0, VF_H2 = 256, VF_ATTN = 512, VF_ACT = VF_ATTN + 64 * FL_MAX_VERIFY;
+constexpr int VF_WORDS = VF_ACT + 2048;
+
+// tokens per attention unit and units per head: the fewest tokens per unit (at most VH) that give
+// every workgroup at most one unit, where such a count exists
+__device__ __forceinline__ void verify_units(int NH, int M, int G, int& tpu, int& ngrp) {
+  tpu = min(VH, (NH * M + G - 1) / G);
+  while (tpu < min(VH, M) && NH * ((M + tpu - 1) / tpu) > G) ++tpu;
+  ngrp = (M + tpu - 1) / tpu;
+}
+
+// Ready flags order the bf16 rows without fences (which on gfx950 write back / invalidate a whole
+// L2): rows are stored with agent-scope stores (sc1, written through to the coherence point) and
+// read with agent-scope loads (sc1, never served from a non-coherent cached copy). A producer
+// waits until all its stores are complete (s_waitcnt 0) before one thread stores the flag, and a
+// consumer issues its row loads only after the flag loads have returned the tag, so the rows it
+// reads are the ones written before the flag. The empty asm statements keep the compiler from
+// moving memory accesses across the hand-off.
+__device__ __forceinline__ void wait_flags(const DecodeParams& p, const uint32_t* flags, int n, uint32_t tag) {
+  for (int i = tid_here(); i < n; i += NT) (void)wait_u32(p, flags + i, tag);
+  asm volatile("" ::: "memory");
+  lds_barrier();
+  asm volatile("" ::: "memory");
+}
+// The workgroup's rows are written: every thread waits until its own stores are complete.
+__device__ __forceinline__ void release_rows() {
+  asm volatile("" ::: "memory");
+  wait_mem();
+  lds_barrier();
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void set_flag(uint32_t* flag, uint32_t tag) {
+  release_rows();
+  if (tid_here() == 0) st_coh_u32(flag, tag << 16);
+}
+
+// Rows m0 .. m0+mh-1 of a bf16 [*, stride] buffer, columns k0 .. k0+kn-1 (kn % 8 == 0), into xs
+// rows 0 .. mh-1 (row pitch ld): 16-byte device-coherent loads, up to SB per thread in flight.
+__device__ void stage_bf16(const uint16_t* src, int stride, int m0, int mh, int k0, int kn,
+                           uint16_t* xs, int ld) {
   constexpr int SB = 8;
   const int tid = tid_here();
-  const int gpr = kn >> 2, total = M * gpr;
-  auto ok = [tag](uint4 w) {
-    return ((w.x >> 16) == tag) & ((w.y >> 16) == tag) & ((w.z >> 16) == tag) & ((w.w >> 16) == tag);
-  };
-  auto addr = [&](int idx) {
-    const int m = idx / gpr, g = idx - m * gpr;
-    return src + (size_t)m * stride + k0 + 4 * g;
-  };
+  const int cpr = kn >> 3, total = mh * cpr;
+  const auto rsrc = buf_rsrc(src, (uint32_t)(m0 + mh) * (uint32_t)stride * 2u);
   for (int base = 0; base < total; base += SB * NT) {
     uint4 v[SB];
 #pragma unroll
     for (int i = 0; i < SB; ++i) {
       const int idx = base + tid + i * NT;
-      v[i] = idx < total ? ld_coh_u128(addr(idx)) : make_uint4(0u, 0u, 0u, 0u);
+      const int m = idx / cpr, c = idx - m * cpr;
+      v[i] = buf_ld128_coh(rsrc, idx < total ? (uint32_t)(((m0 + m) * stride + k0 + 8 * c) * 2) : 0xFFFFFFF0u);
     }
 #pragma unroll
     for (int i = 0; i < SB; ++i) {
       const int idx = base + tid + i * NT;
       if (idx < total) {
-        uint4 w = v[i];
-        if (!ok(w)) {
-          const uint32_t* a = addr(idx);
-          w = spin_until(p, w, ok, [a]() { return ld_coh_u128(a); });
-        }
-        const int m = idx / gpr, g = idx - m * gpr;
-        reinterpret_cast<uint2*>(xs + m * ld)[g] =
-            make_uint2((w.x & 0xFFFFu) | (w.y << 16), (w.z & 0xFFFFu) | (w.w << 16));
+        const int m = idx / cpr, c = idx - m * cpr;
+        *reinterpret_cast<uint4*>(xs + m * ld + 8 * c) = v[i];
       }
     }
   }
@@ -1516,12 +1554,12 @@ __device__ __forceinline__ void tile_load(const uint32_t* __restrict__ q, const 
     tw.s[i] = buf_ld32(sr, in ? ((uint32_t)r * (uint32_t)groups + gg) * 4u : 0xFFFFFFF0u);
   }
 }
-// acc += X(token rows of xs) . dq(tile)^T; xs column 0 = group g0 of the tile's K range
-__device__ __forceinline__ void tile_mma(const TileW& tw, int ng, const uint16_t* xs, int ld, int M,
+// acc += X(token rows 0 .. mh-1 of xs) . dq(tile)^T; xs column 0 = group g0 of the tile's K range
+__device__ __forceinline__ void tile_mma(const TileW& tw, int ng, const uint16_t* xs, int ld, int mh,
                                          fl_f32x4& acc) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
   const int r = lane & 15, c = lane >> 4;
-  const uint16_t* xrow = xs + (r < M ? r : M) * ld + c * 32;
+  const uint16_t* xrow = xs + (r < mh ? r : VH) * ld + c * 32;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int u = wave + NWAVE * i;
@@ -1561,12 +1599,12 @@ __device__ __forceinline__ void tile_load1(const uint32_t* __restrict__ q, const
   tw.w = buf_ld128(wr, in ? (uint32_t)r * (uint32_t)(K >> 1) + gg * 64u + (uint32_t)c * 16u : 0xFFFFFFF0u);
   tw.s = buf_ld32(sr, in ? ((uint32_t)r * (uint32_t)groups + gg) * 4u : 0xFFFFFFF0u);
 }
-__device__ __forceinline__ void tile_mma1(const TileW1& tw, int ng, const uint16_t* xs, int ld, int M,
+__device__ __forceinline__ void tile_mma1(const TileW1& tw, int ng, const uint16_t* xs, int ld, int mh,
                                           fl_f32x4& acc) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
   const int r = lane & 15, c = lane >> 4;
   if (wave < ng) {  // wave-uniform
-    const uint16_t* xrow = xs + (r < M ? r : M) * ld + c * 32 + wave * 128;
+    const uint16_t* xrow = xs + (r < mh ? r : VH) * ld + c * 32 + wave * 128;
     uint4 xa[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) xa[e] = *reinterpret_cast<const uint4*>(xrow + e * 8);
@@ -1595,11 +1633,12 @@ __device__ __forceinline__ float tile_sum(const float* part, int t) {
 }
 
 // Attention (engine/model.py:171-179 over the verify key set). A unit is one query head and a
-// group of TPU consecutive tokens, TPU the fewest that give every workgroup at most one unit; the
-// unit requests the head's cached keys and values once and runs its tokens one after another.
-// While the cache fits one round of registers (pos <= 8 * NWAVE * RB) the later tokens reuse it.
-// LDS att: q of the unit's tokens [16][64], then the new k and v of the group [16][64] each;
-// amk: the unit's amask rows.
+// group of TPU consecutive tokens (verify_units: the fewest that give every workgroup at most one
+// unit); the unit requests the head's cached keys and values once and runs its tokens one after
+// another. While the cache fits one round of registers (pos <= 8 * NWAVE * RB) the later tokens
+// reuse it. LDS att: q of the unit's tokens [VH][64], then the new k and v of the group
+// [FL_MAX_VERIFY][64] each; amk: the unit's amask rows [TPU][M]. The outputs go to the bf16
+// buffer vattn, then the unit's ready flag (VF_ATTN + group * NH + head).
 __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
                                  uint16_t* att, uint8_t* amk, float* wpart) {
   constexpr int RB = 12;
@@ -1609,10 +1648,12 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
   const int HALF = (NH + 2 * NKV) * 32;  // tagged pairs per token
   const int ns = (pos + 7) >> 3;         // 8-key steps over the cached keys [0, pos)
   const int nrounds = (ns + NWAVE * RB - 1) / (NWAVE * RB);
-  const int TPU = (NH * M + (int)gridDim.x - 1) / (int)gridDim.x;
-  const int ngrp = (M + TPU - 1) / TPU;
+  int TPU, ngrp;
+  verify_units(NH, M, (int)gridDim.x, TPU, ngrp);
   const float sc = p.attn_scale * 1.4426950408889634f;
   const uint32_t* att32 = reinterpret_cast<const uint32_t*>(att);
+  uint16_t* const katt = att + VH * 64;                  // new k [FL_MAX_VERIFY][64]
+  uint16_t* const vatt = att + (VH + FL_MAX_VERIFY) * 64;  // new v
   for (int u = blockIdx.x; u < NH * ngrp; u += gridDim.x) {
     const int g = u % NKV, rest = u / NKV, j = rest % QPG, grp = rest / QPG;
     const int hq = g * QPG + j, m0 = grp * TPU, mt = min(M, m0 + TPU) - m0;
@@ -1631,18 +1672,19 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
     if (nrounds > 0) issue(0);
     const int nq = 32 * mt;
     for (int i = tid; i < nq + 64 * M; i += NT) {
-      int hh, tok, d, dst;
+      int hh, tok, d;
+      uint16_t* dst;
       if (i < nq) {
-        hh = hq, tok = m0 + (i >> 5), d = i & 31, dst = (i >> 5) * 64;
+        hh = hq, tok = m0 + (i >> 5), d = i & 31, dst = att + (i >> 5) * 64;
       } else {
         const int i2 = i - nq, which = i2 / (32 * M), r2 = i2 - which * 32 * M;
         tok = r2 >> 5, d = r2 & 31;
         hh = which ? NH + NKV + g : NH + g;
-        dst = (1 + which) * FL_MAX_VERIFY * 64 + tok * 64;
+        dst = (which ? vatt : katt) + tok * 64;
       }
       const unsigned long long v = wait_pair(p, p.qkv + (size_t)tok * HALF + hh * 32 + d, qtag);
-      att[dst + d] = (uint16_t)v;
-      att[dst + d + 32] = (uint16_t)(v >> 16);
+      dst[d] = (uint16_t)v;
+      dst[d + 32] = (uint16_t)(v >> 16);
     }
     for (int i = tid; i < mt * M; i += NT) amk[i] = p.amask[m0 * M + i];
     lds_barrier();
@@ -1696,8 +1738,8 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
           const int jn = s0 + kk;
           const bool valid = jn < M && amk[mi * M + min(jn, M - 1)] != 0;
           const int js = min(jn, M - 1);
-          const uint32_t* kw = att32 + FL_MAX_VERIFY * 32 + js * 32 + ds * 4;
-          const uint32_t* vw = att32 + 2 * FL_MAX_VERIFY * 32 + js * 32 + ds * 4;
+          const uint32_t* kw = reinterpret_cast<const uint32_t*>(katt) + js * 32 + ds * 4;
+          const uint32_t* vw = reinterpret_cast<const uint32_t*>(vatt) + js * 32 + ds * 4;
           float a = dot2_bf16(kw[0], qv[0], 0.0f);
           a = dot2_bf16(kw[1], qv[1], a);
           a = dot2_bf16(kw[2], qv[2], a);
@@ -1739,10 +1781,11 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
           Ls += wp[1] * e;
           O += wp[2 + tid] * e;
         }
-        st_coh_u32(p.attn + (size_t)m * p.D + hq * 64 + tid, f2bf(O / Ls) | (otag << 16));
+        st_coh_u16(p.vattn + (size_t)m * p.D + hq * 64 + tid, f2bf(O / Ls));
       }
       lds_barrier();
     }
+    set_flag(p.vflag + VF_ATTN + grp * NH + hq, otag);
   }
 }
 
@@ -1755,10 +1798,11 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
   const int NQKV = (NH + 2 * NKV) * 64, HALF = NQKV / 2;
   const int ld = D + 8;
   uint16_t* xs = reinterpret_cast<uint16_t*>(vsm);
-  float* part = reinterpret_cast<float*>(vsm + (((size_t)(M + 1) * ld * 2 + 15) & ~(size_t)15));
+  float* part = reinterpret_cast<float*>(vsm + verify_xs_bytes(D));
   uint16_t* att = reinterpret_cast<uint16_t*>(part + 4 * NWAVE * 256);
-  uint8_t* amk = reinterpret_cast<uint8_t*>(att + 3 * FL_MAX_VERIFY * 64);
-  for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + M * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
+  uint8_t* amk = reinterpret_cast<uint8_t*>(att + (VH + 2 * FL_MAX_VERIFY) * 64);
+  uint16_t* hres = reinterpret_cast<uint16_t*>(amk + VH * FL_MAX_VERIFY);  // [FL_MAX_VERIFY][16]
+  for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + VH * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
   int slot = 0;  // optional timestamps, same slots as k_decode's
   stamp(p, slot);
 
@@ -1780,63 +1824,78 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     }
     return r;
   };
+  // this workgroup owns rows 16 wg .. 16 wg + 15 of h (its O tile and its down tile): their
+  // values for every token stay in LDS, starting from bf16(embed[token] * emb_mult) (model.py:138)
+  const bool owner = wg < D / 16;
+  if (owner)
+    for (int i = tid; i < M * 16; i += NT)
+      hres[i] = (uint16_t)f2bf(rbf(bf2f(p.w.embed[(size_t)token_at(i >> 4) * D + wg * 16 + (i & 15)]) * p.emb_mult));
 
+  int TPU, ngrp;
+  verify_units(NH, M, G, TPU, ngrp);
   for (int l = 0; l < params_here().NL; ++l) {
     const DecodeParams& p = params_here();
     const uint32_t e0 = p.epoch + 5u * (uint32_t)l;
     const uint32_t t_prev = tag_of(e0 - 1), t_qkv = tag_of(e0), t_attn = tag_of(e0 + 1),
                    t_h1 = tag_of(e0 + 2), t_act = tag_of(e0 + 3), t_h2 = tag_of(e0 + 4);
+    uint32_t* const vf = p.vflag;
     // ---------------- P1: RMSNorm + QKV + RoPE + KV append ----------------
     const uint32_t* const qkv_q = p.w.wqkv_q + (size_t)l * NQKV * (D >> 3);
     const uint32_t* const qkv_sz = p.w.wqkv_sz + (size_t)l * NQKV * (D >> 7);
     if (wg < NQKV / 16) {
-      TileW tw;
-      tile_load(qkv_q, qkv_sz, wg * 16, 16, D, 0, D >> 7, tw);
-      if (l == 0) {  // bf16(embed[token] * emb_mult)  (engine/model.py:138)
-        for (int i = tid; i < M * (D >> 1); i += NT) {
-          const int m = i / (D >> 1), c = i - m * (D >> 1);
-          const uint32_t e2 = reinterpret_cast<const uint32_t*>(p.w.embed + (size_t)token_at(m) * D)[c];
-          reinterpret_cast<uint32_t*>(xs + m * ld)[c] =
-              pack_bf16x2(rbf(bflo(e2) * p.emb_mult), rbf(bfhi(e2) * p.emb_mult));
-        }
-      } else {
-        stage_rows(p, p.h, D, M, 0, D, t_prev, xs, ld);
-      }
-      lds_barrier();
-      norm_rows(xs, ld, M, D, p.w.attn_norm + (size_t)l * D, p.eps, part);
-      lds_barrier();
-      stamp(p, slot);
-      for (int t = wg; t < NQKV / 16; t += G) {
-        const int n0 = t * 16;
-        const TileW cur = tw;
-        if (t + G < NQKV / 16) tile_load(qkv_q, qkv_sz, (t + G) * 16, 16, D, 0, D >> 7, tw);
-        fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        tile_mma(cur, D >> 7, xs, ld, M, acc);
-        tile_publish(part, acc);
-        if (tid < 128) {  // (token, NEOX pair) of the tile
-          const int m = tid >> 3, pp = tid & 7;
-          if (m < M) {
-            const float a = rbf(tile_sum(part, m * 16 + 2 * pp)), b = rbf(tile_sum(part, m * 16 + 2 * pp + 1));
-            const int srow = n0 + 2 * pp;
-            const int hh = srow >> 6, j = (srow & 63) >> 1;
-            float oa = a, ob = b;
-            if (hh < NH + NKV) {  // RoPE at pos + depth[m] (engine/model.py:257-269)
-              const uint32_t cs = reinterpret_cast<const uint32_t*>(p.w.rope)[rope_pos(m) * 32 + j];
-              const float cc = bflo(cs), sn = bfhi(cs);
-              oa = rbf(a * cc - b * sn);
-              ob = rbf(b * cc + a * sn);
-            }
-            st_coh_u64(p.qkv + (size_t)m * HALF + hh * 32 + j,
-                       (unsigned long long)pack_bf16x2(oa, ob) | ((unsigned long long)t_qkv << 32));
-            if (hh >= NH) {  // KV append at slot pos + m
-              const int g = (hh < NH + NKV) ? hh - NH : hh - NH - NKV;
-              uint16_t* dst = ((hh < NH + NKV) ? p.kc : p.vc) + ((size_t)(l * NKV + g) * p.S + pos + m) * 64;
-              dst[j] = (uint16_t)f2bf(oa);
-              dst[j + 32] = (uint16_t)f2bf(ob);
-            }
+      for (int h0 = 0; h0 < M; h0 += VH) {
+        const int mh = min(VH, M - h0);
+        TileW tw;
+        tile_load(qkv_q, qkv_sz, wg * 16, 16, D, 0, D >> 7, tw);
+        if (l == 0) {  // bf16(embed[token] * emb_mult)  (engine/model.py:138)
+          if (h0 > 0) lds_barrier();  // every wave is done with the previous pass's rows
+          for (int i = tid; i < mh * (D >> 1); i += NT) {
+            const int m = i / (D >> 1), c = i - m * (D >> 1);
+            const uint32_t e2 = reinterpret_cast<const uint32_t*>(p.w.embed + (size_t)token_at(h0 + m) * D)[c];
+            reinterpret_cast<uint32_t*>(xs + m * ld)[c] =
+                pack_bf16x2(rbf(bflo(e2) * p.emb_mult), rbf(bfhi(e2) * p.emb_mult));
           }
+        } else {
+          if (h0 == 0) wait_flags(p, vf + VF_H2, D / 16, t_prev);
+          else lds_barrier();
+          stage_bf16(p.vh, D, h0, mh, 0, D, xs, ld);
         }
         lds_barrier();
+        norm_rows(xs, ld, mh, D, p.w.attn_norm + (size_t)l * D, p.eps, part);
+        lds_barrier();
+        if (h0 == 0) stamp(p, slot);
+        for (int t = wg; t < NQKV / 16; t += G) {
+          const int n0 = t * 16;
+          const TileW cur = tw;
+          if (t + G < NQKV / 16) tile_load(qkv_q, qkv_sz, (t + G) * 16, 16, D, 0, D >> 7, tw);
+          fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+          tile_mma(cur, D >> 7, xs, ld, mh, acc);
+          tile_publish(part, acc);
+          if (tid < 128) {  // (token, NEOX pair) of the tile
+            const int ml = tid >> 3, pp = tid & 7, m = h0 + ml;
+            if (ml < mh) {
+              const float a = rbf(tile_sum(part, ml * 16 + 2 * pp)), b = rbf(tile_sum(part, ml * 16 + 2 * pp + 1));
+              const int srow = n0 + 2 * pp;
+              const int hh = srow >> 6, j = (srow & 63) >> 1;
+              float oa = a, ob = b;
+              if (hh < NH + NKV) {  // RoPE at pos + depth[m] (engine/model.py:257-269)
+                const uint32_t cs = reinterpret_cast<const uint32_t*>(p.w.rope)[rope_pos(m) * 32 + j];
+                const float cc = bflo(cs), sn = bfhi(cs);
+                oa = rbf(a * cc - b * sn);
+                ob = rbf(b * cc + a * sn);
+              }
+              st_coh_u64(p.qkv + (size_t)m * HALF + hh * 32 + j,
+                         (unsigned long long)pack_bf16x2(oa, ob) | ((unsigned long long)t_qkv << 32));
+              if (hh >= NH) {  // KV append at slot pos + m
+                const int g = (hh < NH + NKV) ? hh - NH : hh - NH - NKV;
+                uint16_t* dst = ((hh < NH + NKV) ? p.kc : p.vc) + ((size_t)(l * NKV + g) * p.S + pos + m) * 64;
+                dst[j] = (uint16_t)f2bf(oa);
+                dst[j + 32] = (uint16_t)f2bf(ob);
+              }
+            }
+          }
+          lds_barrier();
+        }
       }
     } else {
       stamp(p, slot);
@@ -1849,152 +1908,164 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     stamp(p, slot);
     stamp(p, slot);
     // ---------------- P3: O projection + residual ----------------
-    if (wg < D / 16) {
+    if (owner) {
       const uint32_t* const o_q = p.w.wo_q + (size_t)l * D * (D >> 3);
       const uint32_t* const o_sz = p.w.wo_sz + (size_t)l * D * (D >> 7);
-      TileW tw;
-      tile_load(o_q, o_sz, wg * 16, 16, D, 0, D >> 7, tw);
-      stage_rows(p, p.attn, D, M, 0, D, t_attn, xs, ld);
-      lds_barrier();
-      stamp(p, slot);
-      for (int t = wg; t < D / 16; t += G) {
-        const int n0 = t * 16;
-        const TileW cur = tw;
-        if (t + G < D / 16) tile_load(o_q, o_sz, (t + G) * 16, 16, D, 0, D >> 7, tw);
+      for (int h0 = 0; h0 < M; h0 += VH) {
+        const int mh = min(VH, M - h0);
+        TileW tw;
+        tile_load(o_q, o_sz, wg * 16, 16, D, 0, D >> 7, tw);
+        if (h0 == 0) wait_flags(p, vf + VF_ATTN, NH * ngrp, t_attn);
+        else lds_barrier();
+        stage_bf16(p.vattn, D, h0, mh, 0, D, xs, ld);
+        lds_barrier();
+        if (h0 == 0) stamp(p, slot);
         fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        tile_mma(cur, D >> 7, xs, ld, M, acc);
+        tile_mma(tw, D >> 7, xs, ld, mh, acc);
         tile_publish(part, acc);
         if (tid < 256) {
-          const int m = tid >> 4, n = tid & 15;
-          if (m < M) {
-            const int row = n0 + n;
-            float hold;
-            if (l == 0) {
-              hold = rbf(bf2f(p.w.embed[(size_t)token_at(m) * D + row]) * p.emb_mult);
-            } else {  // this thread wrote the word in the previous layer's down phase
-              hold = bflo(ld_coh_u32(p.h + (size_t)m * D + row));
-            }
+          const int ml = tid >> 4, n = tid & 15, m = h0 + ml;
+          if (ml < mh) {  // h1 = bf16(h + bf16(bf16(o) * rm))  (engine/model.py:162)
             const float o = rbf(rbf(tile_sum(part, tid)) * p.resid_mult);
-            st_coh_u32(p.h + (size_t)m * D + row, f2bf(hold + o) | (t_h1 << 16));
+            const uint32_t h1 = f2bf(bf2f(hres[m * 16 + n]) + o);
+            hres[m * 16 + n] = (uint16_t)h1;
+            st_coh_u16(p.vh + (size_t)m * D + wg * 16 + n, h1);
           }
         }
         lds_barrier();
       }
+      set_flag(vf + VF_H1 + wg, t_h1);
     }
     // ---------------- P4: RMSNorm + gate/up + SwiGLU ----------------
-    if (wg >= D / 16) stamp(p, slot);
+    if (!owner) stamp(p, slot);
     stamp(p, slot);
     if (wg < (2 * F) / 16) {
       const uint32_t* const gu_q = p.w.wgu_q + (size_t)l * 2 * F * (D >> 3);
       const uint32_t* const gu_sz = p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7);
       // this workgroup's tiles wg, wg+G, ... in rounds of up to 4: the round's MFMAs run back to
       // back into 4 accumulators, one publish and one epilogue per round. The first tile's
-      // weights are requested before the input wait, the rest once the inputs are in (requesting
-      // them after the norm instead was measured slower).
+      // weights are requested before the input wait, the rest once the inputs are in.
       const int nt = ((2 * F) / 16 - wg + G - 1) / G;
-      TileW tw[4] = {};
-      tile_load(gu_q, gu_sz, wg * 16, 16, D, 0, D >> 7, tw[0]);
-      stage_rows(p, p.h, D, M, 0, D, t_h1, xs, ld);
+      for (int h0 = 0; h0 < M; h0 += VH) {
+        const int mh = min(VH, M - h0);
+        const bool last = h0 + VH >= M;
+        TileW tw[4] = {};
+        tile_load(gu_q, gu_sz, wg * 16, 16, D, 0, D >> 7, tw[0]);
+        if (h0 == 0) wait_flags(p, vf + VF_H1, D / 16, t_h1);
+        else lds_barrier();
+        stage_bf16(p.vh, D, h0, mh, 0, D, xs, ld);
 #pragma unroll
-      for (int i = 1; i < 4; ++i)
-        if (i < nt) tile_load(gu_q, gu_sz, (wg + i * G) * 16, 16, D, 0, D >> 7, tw[i]);
-      lds_barrier();
-      norm_rows(xs, ld, M, D, p.w.ffn_norm + (size_t)l * D, p.eps, part);
-      lds_barrier();
-      stamp(p, slot);
-      for (int b4 = 0; b4 < nt; b4 += 4) {
-        fl_f32x4 acc[4] = {};
+        for (int i = 1; i < 4; ++i)
+          if (i < nt) tile_load(gu_q, gu_sz, (wg + i * G) * 16, 16, D, 0, D >> 7, tw[i]);
+        lds_barrier();
+        norm_rows(xs, ld, mh, D, p.w.ffn_norm + (size_t)l * D, p.eps, part);
+        lds_barrier();
+        if (h0 == 0) stamp(p, slot);
+        for (int b4 = 0; b4 < nt; b4 += 4) {
+          fl_f32x4 acc[4] = {};
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (b4 + i < nt) tile_mma(tw[i], D >> 7, xs, ld, M, acc[i]);
+          for (int i = 0; i < 4; ++i)
+            if (b4 + i < nt) tile_mma(tw[i], D >> 7, xs, ld, mh, acc[i]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (b4 + i + 4 < nt) tile_load(gu_q, gu_sz, (wg + (b4 + i + 4) * G) * 16, 16, D, 0, D >> 7, tw[i]);
-        tile_publish4(part, acc);
-        for (int it = tid; it < 4 * 128; it += NT) {
-          const int i = it >> 7, m = (it >> 3) & 15, pp = it & 7;
-          if (b4 + i < nt && m < M) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
-            const float* pt = part + i * NWAVE * 256;
-            const float gg = rbf(tile_sum(pt, m * 16 + 2 * pp)), uu = rbf(tile_sum(pt, m * 16 + 2 * pp + 1));
-            const int n0 = (wg + (b4 + i) * G) * 16;
-            st_coh_u32(p.act + (size_t)m * F + (n0 >> 1) + pp, f2bf(rbf(silu_f(gg)) * uu) | (t_act << 16));
+          for (int i = 0; i < 4; ++i)
+            if (b4 + i + 4 < nt) tile_load(gu_q, gu_sz, (wg + (b4 + i + 4) * G) * 16, 16, D, 0, D >> 7, tw[i]);
+          tile_publish4(part, acc);
+          for (int it = tid; it < 4 * 128; it += NT) {
+            const int i = it >> 7, ml = (it >> 3) & 15, pp = it & 7;
+            if (b4 + i < nt && ml < mh) {  // act = bf16(bf16(silu(g)) * u)  (engine/model.py:227-228)
+              const float* pt = part + i * NWAVE * 256;
+              const float gg = rbf(tile_sum(pt, ml * 16 + 2 * pp)), uu = rbf(tile_sum(pt, ml * 16 + 2 * pp + 1));
+              const int n0 = (wg + (b4 + i) * G) * 16;
+              st_coh_u16(p.vact + (size_t)(h0 + ml) * F + (n0 >> 1) + pp, f2bf(rbf(silu_f(gg)) * uu));
+            }
+          }
+          if (last) {  // the round's tiles are written for every token: their ready flags
+            release_rows();
+            if (tid < 4 && b4 + tid < nt) st_coh_u32(vf + VF_ACT + wg + (b4 + tid) * G, t_act << 16);
+          } else {
+            lds_barrier();
           }
         }
-        lds_barrier();
       }
     }
     if (wg >= (2 * F) / 16) stamp(p, slot);
     stamp(p, slot);
     // ---------------- P5: down projection + residual, K split over workgroups ----------------
     // The 8192-long K of each 16-row tile is cut into parts of 8 groups (1024 inputs; fewer when
-    // D < 1024, as a part is staged into one xs row), one group per wave. Workgroup w takes part k = w % KP of the tiles w / KP, w / KP + G / KP, ...: it
-    // stages only its part's 1024 inputs, runs one group per wave for each of its tiles (weights
-    // requested before the input wait), and publishes each tile's part sum (fp32, tagged) to
-    // p.part. The tile's owner (workgroup t % G) sums the parts in order and adds the residual.
+    // D < 1024, as a part is staged into one xs row), one group per wave. Workgroup w takes part
+    // k = w % KP of the tiles w / KP, w / KP + G / KP, ...: it stages only its part's inputs (those
+    // of the gate/up tiles behind them, by their ready flags), runs one group per wave for each of
+    // its tiles (weights requested before the input wait), and publishes each tile's part sum
+    // (fp32, tagged) to p.part. The tile's owner (workgroup t) sums the parts in order and adds
+    // the residual.
     int p5slot = slot;
     slot += 2;
     {
       const uint32_t* const d_q = p.w.wd_q + (size_t)l * D * (F >> 3);
       const uint32_t* const d_sz = p.w.wd_sz + (size_t)l * D * (F >> 7);
-      // groups per part: one per wave, and no more than an xs row holds (D inputs)
       const int ntile = D / 16, ng = F >> 7, GPP = min(NWAVE, D >> 7), KP = (ng + GPP - 1) / GPP, GK = G / KP;
       const int k = wg % KP, kg0 = k * GPP, kgn = min(GPP, ng - kg0);
       const int nmine = (wg < GK * KP) ? max(0, (ntile - wg / KP + GK - 1) / GK) : 0;
       unsigned long long* const dpart = p.part;  // [tile][part][FL_MAX_VERIFY][16]
       constexpr int TMAX = 8;  // tiles per workgroup whose weights are all requested up front
-      TileW1 tw[TMAX] = {};
+      for (int h0 = 0; h0 < M; h0 += VH) {
+        const int mh = min(VH, M - h0);
+        TileW1 tw[TMAX] = {};
 #pragma unroll
-      for (int i = 0; i < TMAX; ++i)
-        if (i < nmine) tile_load1(d_q, d_sz, (wg / KP + i * GK) * 16, F, kg0, kgn, tw[i]);
-      if (nmine > 0) {
-        stage_rows(p, p.act, F, M, kg0 * 128, kgn * 128, t_act, xs, ld);
-        lds_barrier();
-        stamp(p, p5slot);
-      }
-      for (int j0 = 0; j0 < nmine; j0 += 4) {
-        if (j0 >= TMAX) {  // more tiles than prefetched (few workgroups): one round at a time
+        for (int i = 0; i < TMAX; ++i)
+          if (i < nmine) tile_load1(d_q, d_sz, (wg / KP + i * GK) * 16, F, kg0, kgn, tw[i]);
+        if (nmine > 0) {
+          if (h0 == 0) wait_flags(p, vf + VF_ACT + 16 * kg0, 16 * kgn, t_act);  // gate/up tiles of this part
+          else lds_barrier();
+          stage_bf16(p.vact, F, h0, mh, kg0 * 128, kgn * 128, xs, ld);
+          lds_barrier();
+          if (h0 == 0) stamp(p, p5slot);
+        }
+        for (int j0 = 0; j0 < nmine; j0 += 4) {
+          if (j0 >= TMAX) {  // more tiles than prefetched (few workgroups): one round at a time
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (j0 + i < nmine) tile_load1(d_q, d_sz, (wg / KP + (j0 + i) * GK) * 16, F, kg0, kgn, tw[i]);
+          }
+          fl_f32x4 acc[4] = {};
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (j0 + i < nmine) tile_load1(d_q, d_sz, (wg / KP + (j0 + i) * GK) * 16, F, kg0, kgn, tw[i]);
-        }
-        fl_f32x4 acc[4] = {};
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (j0 + i < nmine) {
-            const TileW1& w = j0 >= TMAX ? tw[i] : (j0 == 0 ? tw[i] : tw[4 + i]);
-            tile_mma1(w, kgn, xs, ld, M, acc[i]);
+            if (j0 + i < nmine) {
+              const TileW1& w = j0 >= TMAX ? tw[i] : (j0 == 0 ? tw[i] : tw[4 + i]);
+              tile_mma1(w, kgn, xs, ld, mh, acc[i]);
+            }
+          tile_publish4(part, acc);
+          for (int it = tid; it < 4 * 256; it += NT) {
+            const int i = it >> 8, ml = (it >> 4) & 15, n = it & 15;
+            if (j0 + i < nmine && ml < mh) {
+              const int t = wg / KP + (j0 + i) * GK;
+              const float v = tile_sum(part + i * NWAVE * 256, ml * 16 + n);
+              st_coh_u64(dpart + (((size_t)t * KP + k) * FL_MAX_VERIFY + h0 + ml) * 16 + n,
+                         (unsigned long long)__float_as_uint(v) | ((unsigned long long)t_h2 << 32));
+            }
           }
-        tile_publish4(part, acc);
-        for (int it = tid; it < 4 * 256; it += NT) {
-          const int i = it >> 8, m = (it >> 4) & 15, n = it & 15;
-          if (j0 + i < nmine && m < M) {
-            const int t = wg / KP + (j0 + i) * GK;
-            const float v = tile_sum(part + i * NWAVE * 256, m * 16 + n);
-            st_coh_u64(dpart + (((size_t)t * KP + k) * FL_MAX_VERIFY + m) * 16 + n,
-                       (unsigned long long)__float_as_uint(v) | ((unsigned long long)t_h2 << 32));
-          }
+          lds_barrier();
         }
-        lds_barrier();
       }
       if (nmine == 0) stamp(p, p5slot);
-      // owner: tile t = wg, wg + G, ...; thread (m, n) sums its row's KP parts in order
-      for (int t = wg; t < ntile; t += G) {
+      // owner of tile wg: thread (m, n) sums its row's KP parts in order, h2 = h1 + bf16(bf16(d) * rm)
+      if (owner) {
         if (tid < 16 * M) {
-          const int m = tid >> 4, n = tid & 15, row = t * 16 + n;
+          const int m = tid >> 4, n = tid & 15;
           auto ok = [t_h2](unsigned long long v) { return (uint32_t)(v >> 32) == t_h2; };
           float sum = 0.0f;
           for (int kk = 0; kk < KP; ++kk) {
-            const unsigned long long* a = dpart + (((size_t)t * KP + kk) * FL_MAX_VERIFY + m) * 16 + n;
+            const unsigned long long* a = dpart + (((size_t)wg * KP + kk) * FL_MAX_VERIFY + m) * 16 + n;
             unsigned long long v = ld_coh_u64(a);
             if (!ok(v)) v = spin_until(p, v, ok, [a]() { return ld_coh_u64(a); });
             sum += __uint_as_float((uint32_t)v);
           }
-          uint32_t hw = ld_coh_u32(p.h + (size_t)m * D + row);  // h1 of this row (O phase)
-          auto ok1 = [t_h1](uint32_t v) { return (v >> 16) == t_h1; };
-          if (!ok1(hw)) hw = spin_until(p, hw, ok1, [&]() { return ld_coh_u32(p.h + (size_t)m * D + row); });
-          const float o = rbf(rbf(sum) * p.resid_mult);
-          st_coh_u32(p.h + (size_t)m * D + row, f2bf(bflo(hw) + o) | (t_h2 << 16));
+          const float o = rbf(rbf(sum) * p.resid_mult);  // engine/model.py:163
+          const uint32_t h2 = f2bf(bf2f(hres[m * 16 + n]) + o);
+          hres[m * 16 + n] = (uint16_t)h2;
+          st_coh_u16(p.vh + (size_t)m * D + wg * 16 + n, h2);
         }
+        set_flag(vf + VF_H2 + wg, t_h2);
       }
     }
     stamp(p, p5slot);
@@ -2002,75 +2073,81 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
 
   // ---------------- final norm + tied bf16 LM head + per-token argmax ----------------
   const int ntile = (p.V + 15) / 16;
-  unsigned long long best = 0ull;
-  if (wg < ntile || (p.feat && wg == 0)) {
-    stage_rows(p, p.h, D, M, 0, D, tag_of(p.epoch + 5u * (uint32_t)p.NL - 1u), xs, ld);
-    lds_barrier();
-    norm_rows(xs, ld, M, D, p.w.final_norm, p.eps, part);
-    lds_barrier();
-    stamp(p, slot);
-    if (p.feat && wg == 0)
-      for (int i = tid; i < M * D; i += NT) p.feat[i] = xs[(i / D) * ld + (i % D)];
-    const int lane = tid & 63, wave = tid >> 6, r = lane & 15, c = lane >> 4;
-    const int ksteps = D >> 5;
-    const uint16_t* xrow = xs + (r < M ? r : M) * ld + c * 8;
-    constexpr int SPW = 16;  // k-steps per wave (D <= 4096)
-    // double-buffered: the next tile's embedding rows are requested before this tile's MFMAs; a
-    // tile past the vocabulary requests nothing (empty range), so the loads stay branch-free
-    auto load_tile = [&](int t, uint4 (&bw)[SPW]) {
-      const int rows = max(0, min(16, p.V - t * 16));
-      const auto er = buf_rsrc(p.w.embed + (size_t)t * 16 * D, (uint32_t)rows * (uint32_t)D * 2u);
-#pragma unroll
-      for (int i = 0; i < SPW; ++i) {
-        const int st = wave + NWAVE * i;
-        bw[i] = buf_ld128(er, st < ksteps ? (uint32_t)(r * D + st * 32 + c * 8) * 2u : 0xFFFFFFF0u);
-      }
-    };
-    auto do_tile = [&](int t, const uint4 (&bw)[SPW]) {
-      const int n0 = t * 16, rows = min(16, p.V - n0);
-      fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int i = 0; i < SPW; ++i) {
-        const int st = wave + NWAVE * i;
-        if (st < ksteps) {
-          const uint4 xa = *reinterpret_cast<const uint4*>(xrow + st * 32);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(fl_bf16x8, xa),
-                                                        __builtin_bit_cast(fl_bf16x8, bw[i]), acc, 0, 0, 0);
-        }
-      }
-      tile_publish(part, acc);
-      if (tid < 256) {
-        const int m = tid >> 4, n = tid & 15;
-        if (m < M && n < rows) {
-          // logits = bf16(bf16(x . E^T) / logits_scaling)  (engine/model.py:144)
-          const float lg = rbf(rbf(tile_sum(part, tid)) / p.logits_scaling);
-          if (p.logits) p.logits[(size_t)m * p.V + n0 + n] = lg;
-          best = u64max(best, amax_key(lg, (uint32_t)(n0 + n)));
-        }
-      }
+  const uint32_t t_fin = tag_of(p.epoch + 5u * (uint32_t)p.NL - 1u);
+  for (int h0 = 0; h0 < M; h0 += VH) {
+    const int mh = min(VH, M - h0);
+    unsigned long long best = 0ull;
+    if (wg < ntile || (p.feat && wg == 0)) {
+      if (h0 == 0) wait_flags(p, p.vflag + VF_H2, D / 16, t_fin);
+      else lds_barrier();
+      stage_bf16(p.vh, D, h0, mh, 0, D, xs, ld);
       lds_barrier();
-    };
-    uint4 bwa[SPW], bwb[SPW];
-    load_tile(wg, bwa);
-    for (int t = wg; t < ntile; t += 2 * G) {
-      load_tile(t + G, bwb);
-      do_tile(t, bwa);
-      if (t + G >= ntile) break;
-      load_tile(t + 2 * G, bwa);
-      do_tile(t + G, bwb);
+      norm_rows(xs, ld, mh, D, p.w.final_norm, p.eps, part);
+      lds_barrier();
+      if (h0 == 0) stamp(p, slot);
+      if (p.feat && wg == 0)
+        for (int i = tid; i < mh * D; i += NT) p.feat[(size_t)h0 * D + i] = xs[(i / D) * ld + (i % D)];
+      const int lane = tid & 63, wave = tid >> 6, r = lane & 15, c = lane >> 4;
+      const int ksteps = D >> 5;
+      const uint16_t* xrow = xs + (r < mh ? r : VH) * ld + c * 8;
+      constexpr int SPW = 16;  // k-steps per wave (D <= 4096)
+      // double-buffered: the next tile's embedding rows are requested before this tile's MFMAs; a
+      // tile past the vocabulary requests nothing (empty range), so the loads stay branch-free
+      auto load_tile = [&](int t, uint4 (&bw)[SPW]) {
+        const int rows = max(0, min(16, p.V - t * 16));
+        const auto er = buf_rsrc(p.w.embed + (size_t)t * 16 * D, (uint32_t)rows * (uint32_t)D * 2u);
+#pragma unroll
+        for (int i = 0; i < SPW; ++i) {
+          const int st = wave + NWAVE * i;
+          bw[i] = buf_ld128(er, st < ksteps ? (uint32_t)(r * D + st * 32 + c * 8) * 2u : 0xFFFFFFF0u);
+        }
+      };
+      auto do_tile = [&](int t, const uint4 (&bw)[SPW]) {
+        const int n0 = t * 16, rows = min(16, p.V - n0);
+        fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < SPW; ++i) {
+          const int st = wave + NWAVE * i;
+          if (st < ksteps) {
+            const uint4 xa = *reinterpret_cast<const uint4*>(xrow + st * 32);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(fl_bf16x8, xa),
+                                                          __builtin_bit_cast(fl_bf16x8, bw[i]), acc, 0, 0, 0);
+          }
+        }
+        tile_publish(part, acc);
+        if (tid < 256) {
+          const int ml = tid >> 4, n = tid & 15;
+          if (ml < mh && n < rows) {
+            // logits = bf16(bf16(x . E^T) / logits_scaling)  (engine/model.py:144)
+            const float lg = rbf(rbf(tile_sum(part, tid)) / p.logits_scaling);
+            if (p.logits) p.logits[(size_t)(h0 + ml) * p.V + n0 + n] = lg;
+            best = u64max(best, amax_key(lg, (uint32_t)(n0 + n)));
+          }
+        }
+        lds_barrier();
+      };
+      uint4 bwa[SPW], bwb[SPW];
+      load_tile(wg, bwa);
+      for (int t = wg; t < ntile; t += 2 * G) {
+        load_tile(t + G, bwb);
+        do_tile(t, bwa);
+        if (t + G >= ntile) break;
+        load_tile(t + 2 * G, bwa);
+        do_tile(t + G, bwb);
+      }
+    } else if (h0 == 0) {
+      stamp(p, slot);
     }
-  } else {
-    stamp(p, slot);
+    // per-token argmax: the 16 threads of a token row are lanes 16k..16k+15 of one wave
+    if (tid < 256) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) best = u64max(best, (unsigned long long)__shfl_xor(best, o, 64));
+      const int ml = tid >> 4;
+      if ((tid & 15) == 0 && ml < mh && best != 0ull)
+        __hip_atomic_fetch_max(p.amax + h0 + ml, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   stamp(p, slot);
-  // per-token argmax: the 16 threads of a token row are lanes 16k..16k+15 of one wave
-  if (tid < 256) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) best = u64max(best, (unsigned long long)__shfl_xor(best, o, 64));
-    const int m = tid >> 4;
-    if ((tid & 15) == 0 && m < M && best != 0ull)
-      __hip_atomic_fetch_max(p.amax + m, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
   wait_mem();
   lds_barrier();
   if (tid == 0) {
@@ -2093,8 +2170,10 @@ struct KvMove {
   int32_t src[FL_MAX_VERIFY], dst[FL_MAX_VERIFY];
   int32_t n;
 };
-__global__ __launch_bounds__(256) void k_kv_move(uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-                                                 int S, KvMove mv) {
+// one workgroup per (layer, KV group); 16 threads per moved row (K and V, 8 x 16 bytes each)
+constexpr int KV_MOVE_THREADS = 16 * FL_MAX_VERIFY;
+__global__ __launch_bounds__(KV_MOVE_THREADS) void k_kv_move(uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                             int S, KvMove mv) {
   const int t = threadIdx.x;
   const size_t base = (size_t)blockIdx.x * S * 64;  // (layer, group) span: S rows of 64 bf16
   const int i = t >> 4, half = (t >> 3) & 1, part = t & 7;
@@ -2135,6 +2214,8 @@ struct fl_state {
   uint32_t *h, *attn, *act;
   unsigned long long* qkv;
   unsigned long long* part;
+  uint16_t* vrows;              // verify exchange rows: h [FL_MAX_VERIFY][D], attn [..][D], act [..][F]
+  uint32_t* vflag;              // verify ready flags
   uint32_t* shist;              // fused sampling exchange: per-workgroup histograms
   unsigned long long* sword;    // ... bin totals, maxima, partial sums
   int att_spw;
@@ -2149,8 +2230,8 @@ struct fl_state {
   int prof_slots;
   void* blocks[16];
   int nblocks;
-  void* uc[8];  // pooled uncached exchange buffers
-  size_t uc_bytes[8];
+  void* uc[12];  // pooled uncached exchange buffers
+  size_t uc_bytes[12];
   int nuc;
   // Tags are 16 bits (1..65535) and advance 5 per layer per launch, so a word left over from an
   // older launch could carry the tag a reader is waiting for once the tags have gone round. The
@@ -2264,6 +2345,10 @@ DecodeParams base_params(const fl_weights* w, fl_state* st, int pos) {
   p.attn = st->attn;
   p.act = st->act;
   p.part = st->part;
+  p.vh = st->vrows;
+  p.vattn = st->vrows + (size_t)FL_MAX_VERIFY * st->d.dim;
+  p.vact = st->vrows + (size_t)2 * FL_MAX_VERIFY * st->d.dim;
+  p.vflag = st->vflag;
   p.shist = st->shist;
   p.sword = st->sword;
   p.att_spw = st->att_spw;
@@ -2405,8 +2490,8 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   // speculative verify: its dynamic LDS (token rows staged for the matrix cores) must fit, and a
   // full grid of it must be co-resident
   st->verify_ok = 0;
-  if (D <= 4096) {
-    const size_t vl = verify_lds_bytes(FL_MAX_VERIFY, D);
+  if (D <= 4096 && 2 * F / 16 <= VF_WORDS - VF_ACT) {
+    const size_t vl = verify_lds_bytes(D);
     int vocc = 0;
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_verify),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)vl) == hipSuccess &&
@@ -2421,8 +2506,14 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   if (rc == FL_OK) rc = uc_alloc(st, &st->qkv, (size_t)(NQKV / 2) * FL_MAX_VERIFY);
   if (rc == FL_OK) rc = uc_alloc(st, &st->attn, (size_t)D * FL_MAX_VERIFY);
   if (rc == FL_OK) rc = uc_alloc(st, &st->act, (size_t)F * FL_MAX_VERIFY);
-  if (rc == FL_OK)
-    rc = uc_alloc(st, &st->part, (size_t)d->n_head * MAX_SLICES * 66 * FL_MAX_VERIFY);
+  {
+    // decode: attention slice partials; verify: down-projection part sums [D/16][KP][FL_MAX_VERIFY][16]
+    const int gpp = std::max(1, std::min(NWAVE, D >> 7)), kp = ((F >> 7) + gpp - 1) / gpp;
+    const size_t dec = (size_t)d->n_head * MAX_SLICES * 66, ver = (size_t)(D / 16) * kp * FL_MAX_VERIFY * 16;
+    if (rc == FL_OK) rc = uc_alloc(st, &st->part, std::max(dec, ver));
+  }
+  if (rc == FL_OK) rc = uc_alloc(st, &st->vrows, (size_t)FL_MAX_VERIFY * (2 * D + F));
+  if (rc == FL_OK) rc = uc_alloc(st, &st->vflag, (size_t)VF_WORDS);
   if (rc == FL_OK) rc = uc_alloc(st, &st->shist, (size_t)G * 256);
   if (rc == FL_OK) rc = uc_alloc(st, &st->sword, (size_t)256 + 2 * G);
   if (rc == FL_OK) rc = dev_alloc(st, &st->amax, FL_MAX_VERIFY);
@@ -2490,7 +2581,7 @@ int fl_kv_move(fl_state* st, const int32_t* src, const int32_t* dst, int32_t n, 
     mv.dst[i] = dst[i];
   }
   if (n == 0) return FL_OK;
-  hipLaunchKernelGGL(k_kv_move, dim3(st->d.n_layer * st->d.n_kv_head), dim3(256), 0,
+  hipLaunchKernelGGL(k_kv_move, dim3(st->d.n_layer * st->d.n_kv_head), dim3(KV_MOVE_THREADS), 0,
                      as_stream(stream), st->kc, st->vc, st->max_seq, mv);
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
@@ -2531,10 +2622,11 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
   if (m < 1 || m > FL_MAX_VERIFY) return FL_E_M;
   if (pos < 0 || pos + m > st->max_seq) return FL_E_POS;
   if (!st->verify_ok) return FL_E_ARG;
-  // the down projection splits K into parts of 8 groups, each needing a workgroup of its own
+  // the down projection splits K into parts of 8 groups, each needing a workgroup of its own,
+  // and each 16-row tile of h has an owning workgroup that keeps its rows in LDS
   {
     const int gpp = std::min(NWAVE, st->d.dim >> 7);
-    if (st->vgrid < ((st->d.inter >> 7) + gpp - 1) / gpp) return FL_E_ARG;
+    if (st->vgrid < ((st->d.inter >> 7) + gpp - 1) / gpp || st->vgrid < st->d.dim / 16) return FL_E_ARG;
   }
   if (maybe_clear(st, as_stream(stream)) != FL_OK) return FL_E_LAUNCH;
   DecodeParams p = base_params(w, st, pos);
@@ -2548,7 +2640,7 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
   p.prof = st->prof;
   p.prof_slots = st->prof_slots;
   void* args[] = {&p};
-  const unsigned lds = (unsigned)verify_lds_bytes(m, st->d.dim);
+  const unsigned lds = (unsigned)verify_lds_bytes(st->d.dim);
   const hipError_t e =
       st->coop ? hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_verify),
                                             dim3(st->vgrid), dim3(NT), args, lds, as_stream(stream))

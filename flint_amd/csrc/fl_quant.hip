@@ -146,18 +146,20 @@ __global__ __launch_bounds__(64 * kGemmWaves) void k_gemm(const uint32_t* __rest
                                                           const uint16_t* __restrict__ x,
                                                           uint16_t* __restrict__ y, int m, int n,
                                                           int k) {
-  __shared__ float part[kGemmWaves][256];
+  __shared__ float part[kGemmWaves][2][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, c = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int rows = min(16, n - n0);
   const int groups = k >> 7;
+  const bool two = m > 16;  // a second 16-row block of activations (tokens 16..31)
   const auto wr = buf_rsrc(q + (size_t)n0 * (k >> 3), (uint32_t)rows * (uint32_t)(k >> 1));
   const auto sr = buf_rsrc(sz + (size_t)n0 * groups, (uint32_t)rows * (uint32_t)groups * 4u);
   const auto xr = buf_rsrc(x, (uint32_t)m * (uint32_t)k * 2u);
   const uint32_t woff = (uint32_t)r * (uint32_t)(k >> 1) + (uint32_t)c * 16u;   // bytes
   const uint32_t xoff = (uint32_t)r * (uint32_t)k * 2u + (uint32_t)c * 64u;     // bytes
-  fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t xoff2 = xoff + 16u * (uint32_t)k * 2u;
+  fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int u = wave; u < groups; u += kGemmWaves) {
     const uint4 w = buf_ld128(wr, woff + (uint32_t)u * 64u);
     const uint32_t s = buf_ld32(sr, ((uint32_t)r * (uint32_t)groups + (uint32_t)u) * 4u);
@@ -167,16 +169,23 @@ __global__ __launch_bounds__(64 * kGemmWaves) void k_gemm(const uint32_t* __rest
     uint32_t d[4][4];
     dq32(w, dq_const(s), d);
     mfma_chunk(d, xa, acc);
+    if (two) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xa[e] = buf_ld128(xr, xoff2 + (uint32_t)u * 256u + (uint32_t)e * 16u);
+      mfma_chunk(d, xa, acc2);
+    }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) part[wave][(c * 4 + i) * 16 + r] = acc[i];
+  for (int i = 0; i < 4; ++i) {
+    part[wave][0][(c * 4 + i) * 16 + r] = acc[i];
+    part[wave][1][(c * 4 + i) * 16 + r] = acc2[i];
+  }
   __syncthreads();
-  const int t = threadIdx.x;
-  if (t < 256) {
+  for (int t = threadIdx.x; t < (two ? 512 : 256); t += 64 * kGemmWaves) {
     const int row = t >> 4, col = t & 15;  // activation row (token), weight row in the tile
     float v = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kGemmWaves; ++w) v += part[w][t];
+    for (int w = 0; w < kGemmWaves; ++w) v += part[w][t >> 8][t & 255];
     if (row < m && col < rows) y[(size_t)row * n + n0 + col] = (uint16_t)f2bf(v);
   }
 }

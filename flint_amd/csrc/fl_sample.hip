@@ -225,10 +225,14 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float* __restrict__ logi
 
 namespace {
 
-// Scratch of fl_sample_noalloc: a fixed block per device for FL_MAX_VERIFY rows (2.1 MB), part of
+// Rows per cooperative launch, and rows of each scratch block: 16 rows of up to SP_C chunks fill
+// the chip's 256 CUs once.
+constexpr int SAMPLE_ROWS = 16;
+
+// Scratch of fl_sample_noalloc: a fixed block per device for SAMPLE_ROWS rows (2.1 MB), part of
 // the code object, so no call allocates. Host code must not pass `scratch` itself to a kernel (it
 // names a host-side stand-in): its device address comes from hipGetSymbolAddress, once per device.
-static __device__ __align__(256) SampleWs scratch[FL_MAX_VERIFY];
+static __device__ __align__(256) SampleWs scratch[SAMPLE_ROWS];
 
 std::mutex g_scratch_mu;
 SampleWs* g_scratch_ptr[64] = {};
@@ -242,8 +246,8 @@ int sample_launch(const float* logits, int32_t rows, int32_t vocab, float temper
   int v = vocab, ci = C, tk = top_k;
   uint32_t slo = (uint32_t)seed, shi = (uint32_t)(seed >> 32), olo = (uint32_t)offset, ohi = (uint32_t)(offset >> 32);
   float td = tdiv;
-  for (int r0 = 0; r0 < rows; r0 += FL_MAX_VERIFY) {  // FL_MAX_VERIFY rows per launch (the scratch's rows)
-    const int n = std::min(FL_MAX_VERIFY, rows - r0);
+  for (int r0 = 0; r0 < rows; r0 += SAMPLE_ROWS) {  // SAMPLE_ROWS rows per launch (the scratch's rows)
+    const int n = std::min(SAMPLE_ROWS, rows - r0);
     const float* lg = logits + (size_t)r0 * vocab;
     const float* nz = noise ? noise + (size_t)r0 * vocab : nullptr;
     int32_t* to = tokens_out + r0;
@@ -278,8 +282,8 @@ int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperatur
   static SampleWs* ws[64] = {};
   if (!ws[dev]) {
     SampleWs* w = nullptr;
-    if (hipMalloc(&w, sizeof(SampleWs) * FL_MAX_VERIFY) != hipSuccess) return FL_E_HIP;
-    if (hipMemset(w, 0, sizeof(SampleWs) * FL_MAX_VERIFY) != hipSuccess) return FL_E_HIP;
+    if (hipMalloc(&w, sizeof(SampleWs) * SAMPLE_ROWS) != hipSuccess) return FL_E_HIP;
+    if (hipMemset(w, 0, sizeof(SampleWs) * SAMPLE_ROWS) != hipSuccess) return FL_E_HIP;
     ws[dev] = w;
   }
   return sample_launch(logits, rows, vocab, temperature, top_k, seed, offset, noise, tokens_out,

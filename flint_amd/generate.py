@@ -4,15 +4,15 @@ Mirrors reference engine/generate.py:57-81,137-206 (prefill / decode_one_token /
 generate) for greedy sampling and chat.py:71-96 (logits_at / pick / respond). Tokens stay on
 the device between steps: step i reads the token step i-1 wrote, so the loop issues launches
 back-to-back with no host synchronisation (gpt-fast's decode loop has none either). The prompt
-is prefilled through the speculative-verify kernel, up to 16 tokens per launch.
+is prefilled through the speculative-verify kernel, up to 32 tokens per launch.
 """
 import torch
 
 
-def prefill(model, x, input_pos, chunk=16):
+def prefill(model, x, input_pos, chunk=32):
     """Feed prompt tokens x (int32 device [T]) at positions input_pos[0]..; returns the greedy next
     token (int32 device [1]) after the last one (reference engine/generate.py:57-60, which runs
-    the prompt through one forward). The prompt goes through the verify kernel `chunk` (<= 16)
+    the prompt through one forward). The prompt goes through the verify kernel `chunk` (<= 32)
     tokens per launch with a causal mask: each launch reads every weight once for the whole
     chunk and appends the chunk's K/V rows."""
     from . import _lib

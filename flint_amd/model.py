@@ -260,7 +260,7 @@ class Transformer:
 
     def kv_move(self, src, dst):
         """Move the K/V rows of cache slots src[i] to dst[i] in every layer (host int lists, at most
-        16): the KV compaction after a tree verify (reference spec_tree.py:124-127). All rows are
+        32): the KV compaction after a tree verify (reference spec_tree.py:124-127). All rows are
         read before any is written."""
         if self._state is None:
             raise RuntimeError("call setup_caches first")

@@ -36,7 +36,7 @@ enum {
                            a workgroup was not resident because other work held its CU)        */
 };
 
-#define FL_MAX_VERIFY 16
+#define FL_MAX_VERIFY 32
 #define FL_HEAD_DIM 64
 #define FL_GROUP 128
 
@@ -88,7 +88,7 @@ int fl_dequant_int4(const uint32_t* q, const uint32_t* sz, uint16_t* out,
 int fl_gemv_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint16_t* y,
                  int32_t n, int32_t k, void* stream);
 
-/* Y[M,N] = bf16( X[M,K] . dq[N,K]^T ), M <= FL_MAX_VERIFY, weight read once for all M rows.
+/* Y[M,N] = bf16( X[M,K] . dq[N,K]^T ), M <= FL_MAX_VERIFY (32), weight read once for all M rows.
  * Replaces reference kernels/int4_gemv_mk.cu:11-57 gemv_mk<M> and kernels/int4_gemm_tc.cu:12-70. */
 int fl_gemm_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint16_t* y,
                  int32_t m, int32_t n, int32_t k, void* stream);
@@ -177,7 +177,7 @@ int fl_kv_move(fl_state* st, const int32_t* src, const int32_t* dst, int32_t n, 
  * largest is dropped (ties with it stay); p = bf16(softmax(x)); the token is the first index of
  * the largest bf16(p / q). q is noise[rows, vocab] when given, else bf16(-log u) with u from
  * Philox4x32-10, key = seed, counter = (index, row, offset low, offset high). probs_out
- * [rows, vocab] (optional) receives p. top_k = 0 means no top-k. Up to FL_MAX_VERIFY rows per
+ * [rows, vocab] (optional) receives p. top_k = 0 means no top-k. Up to 16 rows per
  * cooperative launch (more rows: several launches); the library keeps one scratch block per device
  * (allocated on the first call), so calls on one device must be stream-ordered.
  * Replaces reference engine/generate.py:36-55 (multinomial_sample_one_no_sync, logits_to_probs,
@@ -188,7 +188,7 @@ int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperatur
 
 /* fl_sample that allocates nothing: the same arguments, results and limits (vocab <= 65536,
  * FL_E_ARG beyond), bit-identical output, but its scratch (per-row histograms, partial sums, the
- * argmax word: 2.1 MB for FL_MAX_VERIFY rows) is a fixed device array of the library, one per GPU,
+ * argmax word: 2.1 MB for 16 rows) is a fixed device array of the library, one per GPU,
  * held until the process ends. No hipMalloc, hipFree or allocating library call. Calls on one GPU
  * share that array: calls that overlap on one GPU (other streams or threads) race; keep them
  * stream-ordered. The first call on a device looks the array's address up (no allocation).

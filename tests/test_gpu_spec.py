@@ -26,7 +26,8 @@ def test_kv_move_equals_in_order_copies(dev):
     eng.v_cache.copy_(torch.randn(eng.v_cache.shape, generator=g).to(torch.bfloat16))
     for pos, path in ((40, [0, 2, 5, 6, 9]), (0, [0, 1, 3]), (100, list(range(16))),
                       (7, [0, 15]),
-                      (60, [0, 3, 4, 8, 12, 13, 14, 15])):
+                      (60, [0, 3, 4, 8, 12, 13, 14, 15]),
+                      (20, [0] + list(range(2, 33)))):  # 31 moves
         src = [pos + p for s, p in enumerate(path) if s and p != s]
         dst = [pos + s for s, p in enumerate(path) if s and p != s]
         log(f"kv_move pos={pos} path={path} moves={len(src)}")
@@ -37,8 +38,8 @@ def test_kv_move_equals_in_order_copies(dev):
         eng.kv_move(src, dst)
         torch.cuda.synchronize()
         assert torch.equal(eng.k_cache, k_ref) and torch.equal(eng.v_cache, v_ref)
-    # sixteen arbitrary disjoint moves (no source is another move's destination)
-    src, dst = list(range(64, 80)), list(range(16))
+    # thirty-two arbitrary disjoint moves (no source is another move's destination)
+    src, dst = list(range(64, 96)), list(range(32))
     k_ref, v_ref = eng.k_cache.clone(), eng.v_cache.clone()
     k_ref[:, :, dst] = k_ref[:, :, src]
     v_ref[:, :, dst] = v_ref[:, :, src]
@@ -48,7 +49,7 @@ def test_kv_move_equals_in_order_copies(dev):
     before = eng.k_cache.clone()
     eng.kv_move([], [])
     with pytest.raises(_lib.FlError):
-        eng.kv_move(list(range(17)), list(range(17)))
+        eng.kv_move(list(range(_lib.MAX_VERIFY + 1)), list(range(_lib.MAX_VERIFY + 1)))
     with pytest.raises(_lib.FlError):
         eng.kv_move([eng.max_seq_length], [0])
     with pytest.raises(_lib.FlError):

@@ -5,33 +5,24 @@ Reference semantics (kernels/verify_mega.cu:106-283, spec_mega.py:51-57, spec_tr
 101-104): token m sits at cache slot pos+m, takes RoPE position pos+depth[m] and attends to the
 cache [0, pos) plus the new tokens j with amask[m][j]. Known-answer structure of the reference's
 own test (bench/verify_mega_test.py:43-59): a causal chain verified in one pass equals M
-sequential decode steps. Tolerance as for decode: logits within logit_bar(config) (twice the
-oracle's own fp32-order floor), argmax equal except where the oracle's top-2 margin is within it.
+sequential decode steps. Tolerance (tests/helpers.py check_rows): each row's max and mean |dlogit|,
+and the mean over the rows, within twice the oracle's own floor (the larger of the configuration's
+recorded floor and the distance of the oracle's second implementation on the same input), argmax
+equal except where the oracle's top-2 margin is within the max bar.
 """
 import pytest
 import torch
 
-from tests.helpers import compare_logits, fill_kv_random, log, logit_bar, make_pair, near_tie
+from tests.helpers import (check_rows, compare_logits, fill_kv_random, log, make_pair,
+                           oracle_pair)
 
 pytestmark = pytest.mark.gpu
 
 
-def _check_rows(lg, lo, label, name):
-    bar = logit_bar(name)
-    ties = 0
-    for m in range(lo.shape[0]):
-        ok, d, within, same = compare_logits(lg[m], lo[m], name)
-        am_e, am_o = int(torch.argmax(lg[m])), int(torch.argmax(lo[m]))
-        log(f"{label} row {m}: max|dlogit|={d:.3e} ({within:.1%} within 2e-2) argmax {am_e}/{am_o}")
-        assert ok, (label, m, d)
-        if am_e != am_o:
-            assert near_tie(lo[m], bar), (label, m)
-            ties += 1
-    return ties
-
-
 @pytest.mark.parametrize("name,pos,m", [("tiny", 0, 5), ("tiny", 77, 8), ("small", 130, 5),
-                                        ("small", 200, 16), ("tiny", 300, 1)])
+                                        ("small", 200, 16), ("tiny", 300, 1), ("tiny", 3, 32),
+                                        ("small", 60, 17), ("small", 250, 20), ("small", 90, 24),
+                                        ("flint-3b-l1", 130, 28), ("flint-3b-l1", 300, 32)])
 def test_verify_chain_matches_oracle(dev, name, pos, m):
     args, sd, eng, orc = make_pair(name, seed=11)
     eng.setup_caches(1, 512)
@@ -41,9 +32,9 @@ def test_verify_chain_matches_oracle(dev, name, pos, m):
     toks = torch.randint(0, args.vocab_size, (m,), generator=g, dtype=torch.int32)
     tout, lg, feat = eng.verify(toks.to(dev), pos)
     eng.check()
-    lo, ho = orc.forward(toks, pos)
-    ties = _check_rows(lg.cpu(), lo, f"{name} chain pos={pos} M={m}", name)
-    assert ties <= 1
+    (alt, _), (lo, ho) = oracle_pair(orc, lambda: orc.forward(toks, pos))
+    ties = check_rows(lg.cpu(), lo.float(), alt.float(), name, f"{name} chain pos={pos} M={m}")
+    assert ties <= max(1, m // 8)
     assert torch.equal(tout.cpu(), torch.argmax(lg.cpu(), dim=-1).int())
     assert float((feat.cpu().float() - ho.float()).abs().max()) <= 0.25
     # the M new K / V rows were appended at slots pos .. pos+M-1
@@ -53,14 +44,23 @@ def test_verify_chain_matches_oracle(dev, name, pos, m):
         assert float(torch.maximum(kd, vd).max()) <= 0.25, l
 
 
-def test_verify_tree_matches_oracle(dev):
-    """An 8-node draft tree (spec_tree.py:46-51): depth = node depth, amask = ancestors + self."""
-    args, sd, eng, orc = make_pair("small", seed=12)
+def _random_tree(n, seed):
+    """Parent list of an n-node tree in topological order: node i > 0 hangs off a node before it."""
+    g = torch.Generator().manual_seed(seed)
+    return [-1] + [int(torch.randint(0, i, (1,), generator=g)) for i in range(1, n)]
+
+
+@pytest.mark.parametrize("name,pos,parent", [
+    ("small", 150, [-1, 0, 0, 1, 1, 2, 3, 5]),
+    ("small", 180, _random_tree(24, 3)),
+    ("flint-3b-l1", 220, _random_tree(32, 4))])
+def test_verify_tree_matches_oracle(dev, name, pos, parent):
+    """Draft trees (spec_tree.py:46-51) of 8, 24 and 32 nodes: depth = node depth, amask =
+    ancestors + self. Widths above 16 run the GEMM phases in two passes of 16 token rows."""
+    args, sd, eng, orc = make_pair(name, seed=12)
     eng.setup_caches(1, 512)
     orc.setup_caches(eng.max_seq_length)
-    pos = 150
     fill_kv_random(eng, orc, pos, seed=21)
-    parent = [-1, 0, 0, 1, 1, 2, 3, 5]
     m = len(parent)
     depth = torch.zeros(m, dtype=torch.int32)
     amask = torch.zeros(m, m, dtype=torch.uint8)
@@ -74,16 +74,17 @@ def test_verify_tree_matches_oracle(dev):
                          dtype=torch.int32)
     tout, lg, feat = eng.verify(toks.to(dev), pos, depth=depth.to(dev), amask=amask.to(dev))
     eng.check()
-    lo, ho = orc.forward(toks, pos, depth=depth, amask=amask)
-    ties = _check_rows(lg.cpu(), lo, "tree", "small")
-    assert ties <= 1
+    alt, lo = oracle_pair(orc, lambda: orc.forward(toks, pos, depth=depth, amask=amask)[0].float())
+    ties = check_rows(lg.cpu(), lo, alt, name, f"{name} tree M={m}")
+    assert ties <= max(1, m // 8)
 
 
-def test_verify_chain_equals_sequential_decode(dev):
+@pytest.mark.parametrize("m", [6, 32])
+def test_verify_chain_equals_sequential_decode(dev, m):
     """Reference bench/verify_mega_test.py:43-59: verify of a causal chain == M decode steps."""
     args, sd, eng, _ = make_pair("tiny", seed=13)
     eng.setup_caches(1, 256)
-    pos, m = 40, 6
+    pos = 40
     g = torch.Generator().manual_seed(9)
     prefix = torch.randint(0, args.vocab_size, (pos,), generator=g, dtype=torch.int32).to(dev)
     toks = torch.randint(0, args.vocab_size, (m,), generator=g, dtype=torch.int32).to(dev)
@@ -104,7 +105,7 @@ def test_verify_rejects_bad_arguments(dev):
     from flint_amd import _lib
     args, sd, eng, _ = make_pair("tiny", seed=1)
     eng.setup_caches(1, 64)
-    toks = torch.zeros(17, dtype=torch.int32, device=dev)
+    toks = torch.zeros(33, dtype=torch.int32, device=dev)
     with pytest.raises(_lib.FlError) as e:
         eng.verify(toks, 0)
     assert e.value.code == -3

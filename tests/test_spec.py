@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 import torch
 
+from flint_amd import _lib
 from flint_amd.spec import (LookupDraft, SpecDecoder, accept_chain, accept_tree, compaction_moves,
                             tree_depths, tree_mask)
 
@@ -211,7 +212,7 @@ class StandInModel:
     def verify(self, tokens, pos, depth=None, amask=None, logits=None, feat=None, tokens_out=None):
         toks = [int(t) for t in tokens.reshape(-1).tolist()]
         m = len(toks)
-        assert 1 <= m <= 16 and pos + m <= len(self.slots)
+        assert 1 <= m <= _lib.MAX_VERIFY and pos + m <= len(self.slots)
         depth = depth.tolist()
         amask = amask.reshape(m, m).tolist()
         prefix = self._prefix(pos)
@@ -237,7 +238,7 @@ class StandInModel:
         return tout
 
     def kv_move(self, src, dst):
-        assert len(src) == len(dst) <= 16
+        assert len(src) == len(dst) <= _lib.MAX_VERIFY
         rows = [self.slots[s] for s in src]
         for d, r in zip(dst, rows):
             self.slots[d] = r
@@ -359,7 +360,7 @@ def test_spec_loop_rejects_bad_drafts():
     with pytest.raises(ValueError):
         SpecDecoder(StandInModel(), Bad([1, 2], [-1, 5])).generate([1, 2], 4, mode="tree")
     with pytest.raises(ValueError):
-        SpecDecoder(StandInModel(), k=16)
+        SpecDecoder(StandInModel(), k=_lib.MAX_VERIFY)
     with pytest.raises(ValueError):
         SpecDecoder(StandInModel()).generate([], 4)
 
