@@ -26,7 +26,8 @@ GROUP = 128
 EXPORTS = [
     "fl_version", "fl_device_info", "fl_quantize_int4", "fl_dequant_int4", "fl_gemv_int4",
     "fl_gemm_int4", "fl_state_create", "fl_state_destroy", "fl_state_reset", "fl_state_check",
-    "fl_state_profile", "fl_state_buffers",
+    "fl_state_profile", "fl_state_buffers", "fl_state_set_wait_limit",
+    "fl_state_force_timeout",
     "fl_decode_step", "fl_decode_sample", "fl_decode_hidden", "fl_verify", "fl_kv_move", "fl_sample",
     "fl_sample_noalloc",
 ]
@@ -82,6 +83,8 @@ def load(path=LIB_PATH):
         "fl_state_destroy": ([vp], i32),
         "fl_state_reset": ([vp, vp], i32),
         "fl_state_check": ([vp, vp], i32),
+        "fl_state_set_wait_limit": ([vp, ctypes.c_uint64], i32),
+        "fl_state_force_timeout": ([vp, i32], i32),
         "fl_state_profile": ([vp, vp, i32, vp], i32),
         "fl_state_buffers": ([vp, vp, vp, vp, vp], i32),
         "fl_decode_step": ([ctypes.POINTER(Weights), vp, vp, i32, vp, vp, vp, vp], i32),

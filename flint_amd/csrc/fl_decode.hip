@@ -64,7 +64,7 @@ constexpr int ROWS_MAX = 256;        // max rows per workgroup in one GEMV phase
 constexpr int LM_MAXC = 6;           // max 16-byte chunks per lane of one LM-head row (D <= 3072)
 constexpr int LM_RB = 2;             // LM-head rows per wave per batch
 constexpr int MAX_SLICES = 64;       // attention key slices per kv group
-constexpr unsigned long long SPIN_TICKS = 200000000ull;  // 2 s of the 100 MHz realtime clock
+constexpr unsigned long long SPIN_TICKS = 200000000ull;  // default wait bound: 2 s of the 100 MHz realtime clock
 // attention LDS (floats): bf16 q / new k / new v rows, then per-wave partials
 constexpr int ATT_FLOATS = 96 + NWAVE * 66;
 constexpr int WS_FLOATS = (MAXC * NT > ATT_FLOATS) ? MAXC * NT : ATT_FLOATS;
@@ -91,6 +91,8 @@ struct DecodeParams {
   uint32_t epoch;              // epoch of this launch's first phase (5 per layer)
   unsigned long long* prof;    // optional per-workgroup phase timestamps (100 MHz clock)
   int prof_slots;
+  unsigned long long spin_ticks;  // bound of every inter-workgroup wait (100 MHz ticks)
+  const uint32_t* stall;       // tests: when set, workgroup 0 first waits on this never-written word
   // decode only, fused sampling: samp_tdiv > 0 samples the token (temperature divisor
   // max(T, 1e-5), top-k when 0 < samp_topk < V, Philox4x32-10 noise keyed by seed at counter
   // (index, 0, offset)); samp_tdiv = 0 takes the greedy argmax
@@ -148,8 +150,9 @@ __device__ __forceinline__ void stamp(const DecodeParams& p, int& slot) {
   ++slot;
 }
 
-// Slow path of a tag wait: sleep-poll with a 2 s limit; a timeout (or an earlier error) is
-// recorded in p.err and the wait gives up, so a broken producer can never hang the GPU.
+// Slow path of a tag wait: sleep-poll with a limit of p.spin_ticks (2 s by default); a timeout (or
+// an earlier error) is recorded in p.err and the wait gives up, so a broken producer can never
+// hang the GPU. After an error every later wait of the launch gives up within 64 polls.
 template <typename T, typename Ok, typename Ld>
 __device__ __forceinline__ T spin_until(const DecodeParams& p, T v, Ok ok, Ld ld) {
   const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
@@ -159,7 +162,7 @@ __device__ __forceinline__ T spin_until(const DecodeParams& p, T v, Ok ok, Ld ld
     v = ld();
     if ((++it & 63u) == 0) {
       if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-      if (__builtin_amdgcn_s_memrealtime() - t0 > SPIN_TICKS) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > p.spin_ticks) {
         __hip_atomic_store(p.err, (int32_t)FL_E_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
@@ -1073,6 +1076,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
   const int pos = p.pos;
   int slot = 0;
   stamp(p, slot);
+  if (p.stall && wg == 0 && tid == 0) (void)wait_u32(p, p.stall, 1u);  // forced timeout (tests)
   // the layer-0 input: bf16(embed[token] * emb_mult), or the caller's hidden state h_io as it is
   // (reference kernels/megakernel_decode.cu:204-208 takes h; chat.py:72 forms it on the host)
   const uint16_t* erow;
@@ -1805,6 +1809,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
   for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + VH * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
   int slot = 0;  // optional timestamps, same slots as k_decode's
   stamp(p, slot);
+  if (p.stall && wg == 0 && tid == 0) (void)wait_u32(p, p.stall, 1u);  // forced timeout (tests)
 
   auto token_at = [&](int m) {
     int t = p.tokens[m];
@@ -2228,6 +2233,9 @@ struct fl_state {
   uint32_t epoch;
   unsigned long long* prof;
   int prof_slots;
+  unsigned long long spin_ticks;  // wait bound passed to every launch
+  uint32_t* stall;                // zero word, never written: forced-timeout wait (tests)
+  int force_timeout;
   void* blocks[16];
   int nblocks;
   void* uc[12];  // pooled uncached exchange buffers
@@ -2369,6 +2377,8 @@ DecodeParams base_params(const fl_weights* w, fl_state* st, int pos) {
   p.resid_mult = st->d.resid_mult;
   p.logits_scaling = st->d.logits_scaling;
   p.epoch = st->epoch;
+  p.spin_ticks = st->spin_ticks;
+  p.stall = st->force_timeout ? st->stall : nullptr;
   p.M = 1;
   return p;
 }
@@ -2476,6 +2486,7 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
     st->since_clear = 0;
   }
   st->att_spw = 8;
+  st->spin_ticks = SPIN_TICKS;
   // Plain launches by default: one workgroup per CU is all that fits (LDS), the grid is one per
   // CU, and on a device not shared with concurrent work every workgroup is resident at once. A
   // plain launch starts right after the previous one on the stream; a cooperative launch, which
@@ -2519,6 +2530,7 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   if (rc == FL_OK) rc = dev_alloc(st, &st->amax, FL_MAX_VERIFY);
   if (rc == FL_OK) rc = dev_alloc(st, &st->done, 1);
   if (rc == FL_OK) rc = dev_alloc(st, &st->err, 1);
+  if (rc == FL_OK) rc = dev_alloc(st, &st->stall, 1);
   if (rc != FL_OK) {
     fl_state_destroy(st);
     return rc;
@@ -2560,6 +2572,18 @@ int fl_state_buffers(fl_state* st, uint16_t** h, uint16_t** qkv, uint16_t** attn
   if (qkv) *qkv = reinterpret_cast<uint16_t*>(st->qkv);
   if (attn) *attn = reinterpret_cast<uint16_t*>(st->attn);
   if (act) *act = reinterpret_cast<uint16_t*>(st->act);
+  return FL_OK;
+}
+
+int fl_state_set_wait_limit(fl_state* st, uint64_t ticks) {
+  if (!st) return FL_E_ARG;
+  st->spin_ticks = ticks ? (unsigned long long)ticks : SPIN_TICKS;
+  return FL_OK;
+}
+
+int fl_state_force_timeout(fl_state* st, int32_t on) {
+  if (!st) return FL_E_ARG;
+  st->force_timeout = on != 0;
   return FL_OK;
 }
 

@@ -178,6 +178,18 @@ class Transformer:
         """Raise if a kernel recorded an error (synchronises)."""
         _lib.call("fl_state_check", self._state, _lib.stream_ptr())
 
+    def reset_state(self):
+        """Clear the decode state's error flag, counters and exchange buffers (not the KV cache)."""
+        _lib.call("fl_state_reset", self._state, _lib.stream_ptr())
+
+    def set_wait_limit(self, ticks=0):
+        """Bound of the kernels' inter-workgroup waits in 100 MHz ticks (0: the default 2 s)."""
+        _lib.call("fl_state_set_wait_limit", self._state, int(ticks))
+
+    def force_timeout(self, on=True):
+        """Tests: later launches start with a wait that is never satisfied (the timeout path)."""
+        _lib.call("fl_state_force_timeout", self._state, 1 if on else 0)
+
     def decode_step(self, token, pos, token_out=None, logits=None, feat=None):
         """One decode step: token (int32 device tensor, 1 element) at position pos. Writes the greedy
         argmax to token_out (int32 device, 1 element; default: an internal buffer) and returns it."""

@@ -118,6 +118,17 @@ int fl_state_profile(fl_state* st, uint64_t* buf, int32_t slots_per_wg, int32_t*
  * uint32 words (bf16 bits | phase tag << 16), and this step's q/k/v as uint64 words [(NH+2*NKV)*32]
  * (bf16 bits of dim i | bf16 bits of dim i+32 << 16 | tag << 32; word hh*32+i, heads [q|k|v]). */
 int fl_state_buffers(fl_state* st, uint16_t** h, uint16_t** qkv, uint16_t** attn, uint16_t** act);
+/* Bound of every inter-workgroup wait inside later decode / verify launches, in ticks of the
+ * 100 MHz real-time clock (0: the default, 2 s). A wait that reaches it records FL_E_TIMEOUT and
+ * gives up, and so do the launch's later waits; the launch still ends normally, its outputs are
+ * then meaningless, and fl_state_check reports the error until fl_state_reset. A tiny bound
+ * forces that path from the host (tests of the timeout handling). No counterpart in the
+ * reference, whose grid barriers have no bound. */
+int fl_state_set_wait_limit(fl_state* st, uint64_t ticks);
+/* Tests of the timeout path, no counterpart in the reference: while on != 0, every later decode /
+ * verify launch starts (in workgroup 0) with a wait on a word that is never written, so it takes
+ * the timeout path once the wait bound is reached, deterministically, and still ends normally. */
+int fl_state_force_timeout(fl_state* st, int32_t on);
 /* Last error recorded by a kernel (FL_OK or FL_E_TIMEOUT); synchronises the stream. */
 int fl_state_check(fl_state* st, void* stream);
 

@@ -147,7 +147,7 @@ def test_order_floor(name):
 
 @pytest.mark.slow
 def test_order_floor_40_layers():
-    """The 40-layer model: the floor grows to about 0.3 (a quarter to a third of the logits within
+    """The 40-layer model: the floor grows to about 0.37 (a fifth to a third of the logits within
     2e-2), so the north star's 2e-2 cannot be met even by the reference against itself; the GPU
     bars at 40 layers are twice this. Opt in with FLINT_AMD_SLOW=1 (builds a 6.5 GB oracle)."""
     worst_max, worst_mean, worst_agg, min_within = measure_floor("flint-3b")
