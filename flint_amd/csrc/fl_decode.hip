@@ -75,6 +75,7 @@ struct DecodeParams {
   uint32_t *h, *attn, *act;    // tagged words: bf16 value | tag << 16
   unsigned long long* qkv;     // tagged NEOX pairs: dim i | dim i+32 << 16 | tag << 32
   unsigned long long* part;    // attention slice partials / verify down-projection parts (tagged fp32)
+  unsigned long long* vpart;   // verify attention unit partials (tagged fp32)
   uint16_t *vh, *vattn, *vact; // verify: bf16 [FL_MAX_VERIFY][D | D | F] rows, ready by vflag
   uint32_t* vflag;             // verify: ready flags (tag << 16)
   unsigned long long* amax;    // argmax key
@@ -87,6 +88,8 @@ struct DecodeParams {
   uint16_t* feat;
   int D, NH, NKV, F, V, NL, S, pos;
   int att_spw;                 // attention: target 8-key steps per wave per slice
+  int vkps;                    // verify attention: cached keys per slice (a multiple of 16)
+  int vtok_work;               // verify attention by tokens while tokens per unit x keys <= this
   float eps, emb_mult, attn_scale, resid_mult, logits_scaling;
   uint32_t epoch;              // epoch of this launch's first phase (5 per layer)
   unsigned long long* prof;    // optional per-workgroup phase timestamps (100 MHz clock)
@@ -178,6 +181,36 @@ __device__ __forceinline__ unsigned long long wait_pair(const DecodeParams& p,
   unsigned long long v = ld();
   if (!ok(v)) v = spin_until(p, v, ok, ld);
   return v;
+}
+
+// Poll tagged 64-bit words until every valid one carries `tag`: v[i] holds the last value read of
+// word addr(i); the words still missing are re-read together, so each poll costs one round trip
+// however many words are missing (a word-by-word wait would pay one per word). Bounded like
+// spin_until.
+template <int B, typename Addr, typename Valid>
+__device__ __forceinline__ void poll_tagged(const DecodeParams& p, unsigned long long (&v)[B],
+                                            uint32_t tag, Addr addr, Valid valid) {
+  auto ok = [tag](unsigned long long w) { return (uint32_t)(w >> 32) == tag; };
+  unsigned long long t0 = 0;
+  for (unsigned it = 0;; ++it) {
+    bool done = true;
+#pragma unroll
+    for (int i = 0; i < B; ++i)
+      if (valid(i) && !ok(v[i])) done = false;
+    if (done) return;
+    if (it == 0) t0 = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+    for (int i = 0; i < B; ++i)
+      if (valid(i) && !ok(v[i])) v[i] = ld_coh_u64(addr(i));
+    if ((it & 63u) == 63u) {
+      if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > p.spin_ticks) {
+        __hip_atomic_store(p.err, (int32_t)FL_E_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+    }
+  }
 }
 
 __device__ __forceinline__ void wave_sync() {
@@ -1408,26 +1441,56 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
 // launch, as k_decode keeps them in registers.
 constexpr int VH = 16;  // token rows per pass through a GEMM phase (one MFMA row block)
 
-// dynamic LDS of k_verify: staged token rows [VH + 1][D + 8] bf16 (row VH stays zero), per-wave
-// tile partials [4][8][256] floats, attention staging (q [VH][64], new k and v [32][64] bf16, the
-// unit's mask rows [VH][32]) and this workgroup's rows of the residual h [32][16] (bf16)
-__host__ __device__ inline size_t verify_xs_bytes(int D) { return ((size_t)(VH + 1) * (D + 8) * 2 + 15) & ~(size_t)15; }
+// Verify attention (see attention_verify): keys per load round VRK; LDS regions of a unit, in
+// bytes from the region's start.
+constexpr int VRK = 256;
+constexpr int VT_LD = VRK + 8;  // V^T row pitch (bf16)
+constexpr int VA_Q = 0;                                   // q rows [32][64] bf16
+constexpr int VA_K = VA_Q + FL_MAX_VERIFY * 128;          // key rows [VRK][64] bf16
+constexpr int VA_VT = VA_K + VRK * 128;                   // values, transposed [64][VT_LD] bf16
+constexpr int VA_MASK = VA_VT + 64 * VT_LD * 2;           // tree mask rows [32][32] u8
+constexpr int VA_WP = VA_MASK + FL_MAX_VERIFY * FL_MAX_VERIFY;  // per-wave partials [NWAVE][16][66] fp32
+constexpr int VA_BYTES = VA_WP + NWAVE * 16 * 66 * 4;
+
+// dynamic LDS of k_verify: a region shared by the staged token rows of the GEMM phases
+// ([VH + 1][D + 8] bf16, row VH stays zero) and the attention unit (VA_BYTES), the current
+// RMSNorm weight vector [D] bf16, per-wave tile partials [4][8][256] floats and this workgroup's
+// rows of the residual h [32][16] (bf16)
+__host__ __device__ inline size_t verify_xs_bytes(int D) {
+  const size_t xs = ((size_t)(VH + 1) * (D + 8) * 2 + 15) & ~(size_t)15;
+  return xs > (size_t)VA_BYTES ? xs : (size_t)VA_BYTES;
+}
+__host__ __device__ inline size_t verify_nw_bytes(int D) { return ((size_t)D * 2 + 15) & ~(size_t)15; }
 inline size_t verify_lds_bytes(int D) {
-  return verify_xs_bytes(D) + 4 * NWAVE * 256 * 4 + (size_t)(VH + 2 * FL_MAX_VERIFY) * 64 * 2 +
-         VH * FL_MAX_VERIFY + FL_MAX_VERIFY * 16 * 2;
+  return verify_xs_bytes(D) + verify_nw_bytes(D) + 4 * NWAVE * 256 * 4 + FL_MAX_VERIFY * 16 * 2;
 }
 
-// verify's ready flags (uint32 words, tag << 16): per O tile (h1), per down tile (h2), per
-// attention unit (token group * NH + head), per gate/up tile (SwiGLU output)
-constexpr int VF_H1 = 0, VF_H2 = 256, VF_ATTN = 512, VF_ACT = VF_ATTN + 64 * FL_MAX_VERIFY;
+// A norm weight vector (bf16 [D], D % 8 == 0) into LDS. Called before a phase's input wait: its
+// loads complete while the workgroup waits, so the norm after the wait reads no global memory
+// (a global load there would queue behind the weight tiles requested before the wait and wait
+// for all of them: loads complete in order).
+__device__ __forceinline__ void stage_norm_w(const uint16_t* __restrict__ nw, int D, uint16_t* nws) {
+  for (int i = tid_here(); i < (D >> 3); i += NT)
+    reinterpret_cast<uint4*>(nws)[i] = reinterpret_cast<const uint4*>(nw)[i];
+}
+
+// verify's ready flags (uint32 words, tag << 16): per O tile (h1), per down tile (h2), per query
+// head (attention output), per gate/up tile (SwiGLU output)
+constexpr int VF_H1 = 0, VF_H2 = 256, VF_ATTN = 512, VF_ACT = VF_ATTN + 256;
 constexpr int VF_WORDS = VF_ACT + 2048;
 
-// tokens per attention unit and units per head: the fewest tokens per unit (at most VH) that give
-// every workgroup at most one unit, where such a count exists
-__device__ __forceinline__ void verify_units(int NH, int M, int G, int& tpu, int& ngrp) {
-  tpu = min(VH, (NH * M + G - 1) / G);
-  while (tpu < min(VH, M) && NH * ((M + tpu - 1) / tpu) > G) ++tpu;
-  ngrp = (M + tpu - 1) / tpu;
+// Key slices of verify attention per query head: nsl units, one per p.vkps cached keys (default 128)
+// but at most VNS
+// and G / NH (so all units of a launch fit the grid, one each), unit s covering the cached keys
+// [s kps, min(pos, (s+1) kps)) (kps a multiple of 16); the last unit also takes the new keys.
+// With pos <= p.vkps there is one unit per head and no merge.
+constexpr int VNS = 16;
+__device__ __forceinline__ void verify_slices(const DecodeParams& p, int pos, int NH, int G, int& nsl, int& kps) {
+  const int ch = (pos + 15) >> 4;
+  const int cap = max(1, min(VNS, G / NH));
+  nsl = max(1, min(cap, (pos + p.vkps - 1) / p.vkps));  // a slice per vkps keys, while units last
+  kps = ((ch + nsl - 1) / nsl) * 16;
+  nsl = kps ? max(1, (pos + kps - 1) / kps) : 1;
 }
 
 // Ready flags order the bf16 rows without fences (which on gfx950 write back / invalidate a whole
@@ -1438,7 +1501,39 @@ __device__ __forceinline__ void verify_units(int NH, int M, int G, int& tpu, int
 // reads are the ones written before the flag. The empty asm statements keep the compiler from
 // moving memory accesses across the hand-off.
 __device__ __forceinline__ void wait_flags(const DecodeParams& p, const uint32_t* flags, int n, uint32_t tag) {
-  for (int i = tid_here(); i < n; i += NT) (void)wait_u32(p, flags + i, tag);
+  // wave 0 polls the flags four to a lane, one 16-byte load per lane per poll (flags 16-byte
+  // aligned): a workgroup that waits puts at most 64 loads per poll on the flags' few memory
+  // lines instead of one per flag and thread
+  if (tid_here() < 64) {
+    const int lane = tid_here();
+    for (int b = 0; b < n; b += 256) {
+      const auto rs = buf_rsrc(flags + b, (uint32_t)min(256, n - b) * 4u);
+      auto mine_ok = [&](uint4 v) {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        bool ok = true;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (b + 4 * lane + e < n && (w[e] >> 16) != tag) ok = false;
+        return ok;
+      };
+      uint4 v = buf_ld128_coh(rs, (uint32_t)lane * 16u);
+      unsigned long long t0 = 0;
+      for (unsigned it = 0;; ++it) {
+        const bool ok = mine_ok(v);
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+        if (it == 0) t0 = __builtin_amdgcn_s_memrealtime();
+        __builtin_amdgcn_s_sleep(2);
+        if (!ok) v = buf_ld128_coh(rs, (uint32_t)lane * 16u);
+        if ((it & 63u) == 63u) {
+          if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+          if (__builtin_amdgcn_s_memrealtime() - t0 > p.spin_ticks) {
+            __hip_atomic_store(p.err, (int32_t)FL_E_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+        }
+      }
+    }
+  }
   asm volatile("" ::: "memory");
   lds_barrier();
   asm volatile("" ::: "memory");
@@ -1486,8 +1581,8 @@ __device__ void stage_bf16(const uint16_t* src, int stride, int m0, int mh, int 
 // A row is shared by NWAVE / M waves (all 8 for one token), whose partial sums of squares meet
 // in red (NWAVE floats of LDS); the row loop has the same trip count in every wave, so the
 // barriers are uniform.
-__device__ void norm_rows(uint16_t* xs, int ld, int M, int D, const uint16_t* __restrict__ nw,
-                          float eps, float* red) {
+__device__ __forceinline__ void norm_rows(uint16_t* xs, int ld, int M, int D, const uint16_t* nw,
+                                          float eps, float* red) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
   int wpr = 1;                                  // waves per row: a power of two, wpr * M <= NWAVE
   while (wpr * 2 * M <= NWAVE) wpr *= 2;
@@ -1636,15 +1731,29 @@ __device__ __forceinline__ float tile_sum(const float* part, int t) {
   return v;
 }
 
-// Attention (engine/model.py:171-179 over the verify key set). A unit is one query head and a
+// tokens per attention unit and units per head (attention by tokens): the fewest tokens per unit
+// (at most VH) that give every workgroup at most one unit, where such a count exists
+__device__ __forceinline__ void verify_units(int NH, int M, int G, int& tpu, int& ngrp) {
+  tpu = min(VH, (NH * M + G - 1) / G);
+  while (tpu < min(VH, M) && NH * ((M + tpu - 1) / tpu) > G) ++tpu;
+  ngrp = (M + tpu - 1) / tpu;
+}
+
+// Verify attention by tokens (engine/model.py:171-179 over the verify key set), for few tokens
+// at short and medium contexts, where it needs no merge across workgroups. A unit is one query head and a
 // group of TPU consecutive tokens (verify_units: the fewest that give every workgroup at most one
 // unit); the unit requests the head's cached keys and values once and runs its tokens one after
 // another. While the cache fits one round of registers (pos <= 8 * NWAVE * RB) the later tokens
 // reuse it. LDS att: q of the unit's tokens [VH][64], then the new k and v of the group
 // [FL_MAX_VERIFY][64] each; amk: the unit's amask rows [TPU][M]. The outputs go to the bf16
 // buffer vattn, then the unit's ready flag (VF_ATTN + group * NH + head).
-__device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
-                                 uint16_t* att, uint8_t* amk, float* wpart) {
+__device__ void attention_verify_tokens(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
+                                        unsigned char* ua, int& slot) {
+  uint16_t* const att = reinterpret_cast<uint16_t*>(ua);                        // q [VH][64], new k, v [32][64]
+  uint8_t* const amk = ua + (VH + 2 * FL_MAX_VERIFY) * 64 * 2;                  // [VH][32]
+  float* const wpart = reinterpret_cast<float*>(amk + VH * FL_MAX_VERIFY);      // [NWAVE][66]
+  stamp(p, slot);
+  stamp(p, slot);
   constexpr int RB = 12;
   const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
   const int kk = lane >> 3, ds = lane & 7;
@@ -1791,6 +1900,358 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
     }
     set_flag(p.vflag + VF_ATTN + grp * NH + hq, otag);
   }
+  stamp(p, slot);
+  stamp(p, slot);
+}
+
+// Verify attention (engine/model.py:171-179 over the verify key set; q.k^T * scale, softmax and
+// p.v in fp32, bf16 output). Token m's query attends to the cached keys [0, pos) and to the new
+// keys t (this launch's tokens, from the q/k/v exchange) with amask[m][t].
+//
+// Unit (head hq, slice s) takes all M tokens of one query head against one key slice
+// (verify_slices); units are numbered u = (j * nsl + s) * NKV + g for head j of KV group g, so
+// with workgroups dealt round-robin over the 8 XCDs the units of one group read its K / V rows
+// through one L2. The unit's cached K / V rows are requested before the wait for q. Per 16-key
+// chunk and 16-token row tile a wave forms S^T = K Q^T with two 16x16x32 bf16 MFMAs (lane (r, c)
+// then holds the scores of token r for keys 4c .. 4c+3), updates the rows' running max and sum
+// (exp2 domain), and accumulates O^T = V^T P^T with 16x16x16 bf16 MFMAs, P split into three bf16
+// terms p = hi + mid + lo (each product with a bf16 value exact in fp32, so the accumulation is
+// fp32 p.v up to summation order). The waves that split one row tile's chunks merge through LDS.
+// With one unit per head it writes bf16(o / sum) to vattn itself; otherwise every unit publishes
+// each token's (max, sum, o[64]) as tagged fp32 words, then merges the tokens m = s, s + nsl, ...
+// over the head's units in unit order and writes them. Each unit then sets its ready flag
+// (VF_ATTN + hq * nsl + s). Timestamps (slot, 4 per call): q staged, keys done, partials
+// published (or output written), flag set.
+__device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
+                                 unsigned char* ua, int& slot) {
+  const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, c = lane >> 4;
+  const int M = p.M, pos = p.pos, NH = p.NH, NKV = p.NKV, QPG = p.NH / p.NKV, G = grid_here();
+  const int HALF = (NH + 2 * NKV) * 32;  // tagged pairs per token
+  const int RT = (M + 15) >> 4;          // token row tiles (1 or 2)
+  int nsl, kps;
+  verify_slices(p, pos, NH, G, nsl, kps);
+  const float sc = p.attn_scale * 1.4426950408889634f;
+  uint16_t* const qs = reinterpret_cast<uint16_t*>(ua + VA_Q);
+  uint16_t* const ks = reinterpret_cast<uint16_t*>(ua + VA_K);
+  uint16_t* const vt = reinterpret_cast<uint16_t*>(ua + VA_VT);
+  uint8_t* const amk = ua + VA_MASK;
+  float* const wp = reinterpret_cast<float*>(ua + VA_WP);
+  unsigned long long* const vpart = p.vpart;  // [NH][VNS][32][66] tagged fp32
+  int WPR = 1;  // waves per row tile
+  while (RT * WPR * 2 <= NWAVE) WPR *= 2;
+  const int myrt = wave % RT, kp = wave / RT;  // this wave's row tile and chunk phase
+  const int nunits = NH * nsl;
+  if ((int)blockIdx.x >= nunits) {
+    stamp(p, slot);
+    stamp(p, slot);
+    stamp(p, slot);
+  }
+  for (int unit = blockIdx.x; unit < nunits; unit += G) {
+    const int g = unit % NKV, rest = unit / NKV, sl = rest % nsl, jh = rest / nsl;
+    const int hq = g * QPG + jh;
+    const bool last = sl == nsl - 1;  // also takes the new keys
+    const int k0 = sl * kps, nc = max(0, min(pos, k0 + kps) - k0);  // cached keys of the unit
+    const int nk = nc + (last ? M : 0);
+    const size_t cbase = (size_t)(l * NKV + g) * p.S * 64;
+    // cached keys [k0 + kb, k0 + kb + n) into rows 0 .. n-1 of ks and columns 0 .. n-1 of vt
+    auto load_round = [&](int kb, int n) {
+      const auto kr = buf_rsrc(p.kc + cbase + (size_t)(k0 + kb) * 64, (uint32_t)n * 128u);
+      const auto vr = buf_rsrc(p.vc + cbase + (size_t)(k0 + kb) * 64, (uint32_t)n * 128u);
+      uint4 kv[4], vv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {  // VRK * 8 = 2048 16-byte chunks each of K and V: 4 per thread
+        const int ci = tid + NT * i;
+        kv[i] = buf_ld128(kr, (uint32_t)ci * 16u);
+        vv[i] = buf_ld128(vr, (uint32_t)ci * 16u);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ci = tid + NT * i, key = ci >> 3, d0 = (ci & 7) * 8;
+        if (key >= n) continue;  // rows past the round: the new keys may be staged there
+        *reinterpret_cast<uint4*>(ks + key * 64 + d0) = kv[i];
+        const uint32_t w4[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vt[(d0 + 2 * e) * VT_LD + key] = (uint16_t)w4[e];
+          vt[(d0 + 2 * e + 1) * VT_LD + key] = (uint16_t)(w4[e] >> 16);
+        }
+      }
+    };
+    if (nc > 0) load_round(0, min(nc, VRK));  // cached keys: requested before the q wait
+    // q of the head for every token (zero rows up to the tile edge); for the last slice the new
+    // keys' K / V rows (after the round's cached keys, if they fit, else in a round of their own)
+    // and the mask
+    const int nb0 = (nc + M <= VRK) ? nc : 0;  // where the new keys go in ks / vt
+    {
+      const int nq = M * 32, nkv = last && nb0 == nc ? 64 * M : 0, total = nq + nkv;
+      constexpr int B = 4;
+      auto word = [&](int idx) {  // tagged pair of item idx: q pairs, then new k, then new v
+        if (idx < nq) return p.qkv + (size_t)(idx >> 5) * HALF + hq * 32 + (idx & 31);
+        const int i2 = idx - nq, which = i2 / (32 * M), r2 = i2 - which * 32 * M;
+        return p.qkv + (size_t)(r2 >> 5) * HALF + (which ? NH + NKV + g : NH + g) * 32 + (r2 & 31);
+      };
+      for (int base = 0; base < total; base += B * NT) {
+        unsigned long long v[B];
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          const int idx = base + tid + i * NT;
+          v[i] = idx < total ? ld_coh_u64(word(idx)) : 0ull;
+        }
+        poll_tagged<B>(p, v, qtag, [&](int i) { return word(base + tid + i * NT); },
+                       [&](int i) { return base + tid + i * NT < total; });
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          const int idx = base + tid + i * NT;
+          if (idx < total) {
+            const uint16_t lo = (uint16_t)v[i], hi = (uint16_t)(v[i] >> 16);
+            if (idx < nq) {
+              const int m = idx >> 5, dp = idx & 31;
+              qs[m * 64 + dp] = lo;
+              qs[m * 64 + dp + 32] = hi;
+            } else {
+              const int i2 = idx - nq, which = i2 / (32 * M), r2 = i2 - which * 32 * M;
+              const int t = nb0 + (r2 >> 5), dp = r2 & 31;
+              if (which == 0) {
+                ks[t * 64 + dp] = lo;
+                ks[t * 64 + dp + 32] = hi;
+              } else {
+                vt[dp * VT_LD + t] = lo;
+                vt[(dp + 32) * VT_LD + t] = hi;
+              }
+            }
+          }
+        }
+      }
+      for (int i = tid; i < (RT * 16 - M) * 32; i += NT) reinterpret_cast<uint32_t*>(qs + M * 64)[i] = 0u;
+      if (last)
+        for (int i = tid; i < M * M; i += NT) amk[i] = p.amask[i];
+    }
+    lds_barrier();
+    stamp(p, slot);
+    // ---- S, online softmax and P.V, one round of keys at a time: ncr cached keys (rows 0 ..
+    // ncr-1 of ks / vt), then, in the round that holds them, the M new keys (rows ncr .. ncr+M-1)
+    float mrun = -INFINITY, lrun = 0.0f;
+    fl_f32x4 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = fl_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const bool active = wave < RT * WPR;
+    const uint16_t* qrow = qs + (myrt * 16 + r) * 64 + c * 8;
+    const int mrow = min(myrt * 16 + r, M - 1);  // this lane's token (rows past M are padding)
+    // value columns past the round's keys up to the chunk edge must be finite (p = 0 there)
+    auto zero_tail = [&](int nr) {
+      for (int i = tid; i < 64 * 16; i += NT) {
+        const int col = nr + (i & 15);
+        if (col < ((nr + 15) & ~15)) vt[(i >> 4) * VT_LD + col] = 0;
+      }
+    };
+    int kb = 0, ncr = min(VRK, nc);
+    bool new_in = last && nb0 == nc, new_done = !last || nb0 == nc;
+    zero_tail(ncr + (new_in ? M : 0));
+    lds_barrier();
+    for (;;) {
+      const int nr = ncr + (new_in ? M : 0);
+      if (active && nr > 0) {
+        const uint4 qa = *reinterpret_cast<const uint4*>(qrow);
+        const uint4 qb = *reinterpret_cast<const uint4*>(qrow + 32);
+        for (int ch = kp; ch * 16 < nr; ch += WPR) {
+          const uint16_t* krow = ks + (ch * 16 + r) * 64 + c * 8;
+          fl_f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+          st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(fl_bf16x8, *reinterpret_cast<const uint4*>(krow)),
+              __builtin_bit_cast(fl_bf16x8, qa), st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(fl_bf16x8, *reinterpret_cast<const uint4*>(krow + 32)),
+              __builtin_bit_cast(fl_bf16x8, qb), st, 0, 0, 0);
+          // st[i]: score of token row r, round key ch * 16 + 4c + i
+          float sv[4], mx = -INFINITY;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kl = ch * 16 + 4 * c + i;
+            bool ok = kl < nr;
+            if (kl >= ncr) ok = ok && amk[mrow * M + min(kl - ncr, M - 1)] != 0;  // a new key
+            sv[i] = ok ? st[i] * sc : -INFINITY;
+            mx = fmaxf(mx, sv[i]);
+          }
+          mx = xor32_max(xor16_max(mx));
+          const float mn = fmaxf(mrun, mx);
+          const float mu = (mn == -INFINITY) ? 0.0f : mn;
+          const float corr = __builtin_amdgcn_exp2f(mrun - mu);
+          float pv[4];
+          float ps = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pv[i] = __builtin_amdgcn_exp2f(sv[i] - mu);
+            ps += pv[i];
+          }
+          ps = xor32_sum(xor16_sum(ps));
+          lrun = lrun * corr + ps;
+          mrun = mn;
+          uint32_t ph[2], pm[2], pl[2];  // p = hi + mid + lo, three bf16 terms
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float a0 = pv[2 * e], a1 = pv[2 * e + 1];
+            ph[e] = pack_bf16x2(a0, a1);
+            const float r0 = a0 - bflo(ph[e]), r1 = a1 - bfhi(ph[e]);
+            pm[e] = pack_bf16x2(r0, r1);
+            pl[e] = pack_bf16x2(r0 - bflo(pm[e]), r1 - bfhi(pm[e]));
+          }
+          typedef short fl_s16x4 __attribute__((ext_vector_type(4)));
+          const fl_s16x4 bh = __builtin_bit_cast(fl_s16x4, make_uint2(ph[0], ph[1]));
+          const fl_s16x4 bm = __builtin_bit_cast(fl_s16x4, make_uint2(pm[0], pm[1]));
+          const fl_s16x4 bl = __builtin_bit_cast(fl_s16x4, make_uint2(pl[0], pl[1]));
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            fl_f32x4 acc = o[dt];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] *= corr;
+            const fl_s16x4 va = __builtin_bit_cast(
+                fl_s16x4, *reinterpret_cast<const uint2*>(vt + (dt * 16 + r) * VT_LD + ch * 16 + 4 * c));
+            acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, bm, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, bl, acc, 0, 0, 0);
+            o[dt] = acc;
+          }
+        }
+      }
+      if (kb + VRK < nc) {  // the next round of cached keys
+        lds_barrier();      // every wave is done with this one
+        kb += VRK;
+        ncr = min(VRK, nc - kb);
+        load_round(kb, ncr);
+        zero_tail(ncr);
+        lds_barrier();
+      } else if (!new_done) {  // the new keys in a round of their own (rows 0 .. M-1)
+        lds_barrier();
+        for (int i = tid; i < 64 * M; i += NT) {
+          const int which = i / (32 * M), r2 = i - which * 32 * M, t = r2 >> 5, dp = r2 & 31;
+          const unsigned long long w =
+              wait_pair(p, p.qkv + (size_t)t * HALF + (which ? NH + NKV + g : NH + g) * 32 + dp, qtag);
+          if (which == 0) {
+            ks[t * 64 + dp] = (uint16_t)w;
+            ks[t * 64 + dp + 32] = (uint16_t)(w >> 16);
+          } else {
+            vt[dp * VT_LD + t] = (uint16_t)w;
+            vt[(dp + 32) * VT_LD + t] = (uint16_t)(w >> 16);
+          }
+        }
+        ncr = 0;
+        new_in = new_done = true;
+        zero_tail(M);
+        lds_barrier();
+      } else {
+        break;
+      }
+    }
+    stamp(p, slot);
+    // ---- the unit's (max, sum, o) per token: the WPR waves of each row tile merge through LDS
+    // (o[dt][i] at lane (r, c): token row r, dim 16 dt + 4 c + i)
+    lds_barrier();
+    if (active) {
+      float* w = wp + (wave * 16 + r) * 66;
+      if (c == 0) {
+        w[0] = mrun;
+        w[1] = lrun;
+      }
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[2 + dt * 16 + 4 * c + i] = o[dt][i];
+    }
+    lds_barrier();
+    // thread (token m, word wd): the unit's value of that word, waves of the row tile in order
+    auto unit_word = [&](int m, int wd) {
+      const int rt = m >> 4, rr = m & 15;
+      float mm = -INFINITY;
+      for (int q = 0; q < WPR; ++q) mm = fmaxf(mm, wp[((rt + q * RT) * 16 + rr) * 66]);
+      if (wd == 0) return mm;
+      float val = 0.0f;
+      for (int q = 0; q < WPR; ++q) {
+        const float* w = wp + ((rt + q * RT) * 16 + rr) * 66;
+        const float e = (w[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(w[0] - mm);
+        val += w[wd] * e;
+      }
+      return val;
+    };
+    unsigned long long* const hp = vpart + (size_t)hq * VNS * FL_MAX_VERIFY * 66;
+    uint32_t* const flag = p.vflag + VF_ATTN + hq * nsl + sl;
+    if (nsl == 1) {  // the unit saw every key: its rows are the output
+      for (int it = tid; it < M * 64; it += NT) {
+        const int m = it >> 6, d = it & 63;
+        st_coh_u16(p.vattn + (size_t)m * p.D + hq * 64 + d, f2bf(unit_word(m, 2 + d) / unit_word(m, 1)));
+      }
+      stamp(p, slot);
+      set_flag(flag, otag);
+    } else {
+      // publish every token's (max, sum, o), then merge the tokens m = sl, sl + nsl, ... over the
+      // head's nsl units: thread (token of pass q and wave, dim d), words of the units in order
+      for (int it = tid; it < M * 66; it += NT) {
+        const int m = it / 66, wd = it - m * 66;
+        st_coh_u64(hp + ((size_t)sl * FL_MAX_VERIFY + m) * 66 + wd,
+                   (unsigned long long)__float_as_uint(unit_word(m, wd)) | ((unsigned long long)otag << 32));
+      }
+      stamp(p, slot);
+      const int ntok = (M - sl + nsl - 1) / nsl, npass = (ntok + NWAVE - 1) / NWAVE;  // <= 4
+      const int d = lane;
+      auto tok = [&](int q) { return sl + (q * NWAVE + wave) * nsl; };
+      // words 0 .. VNS-1: o[d] of (pass i / nsl, unit i % nsl), npass * nsl <= VNS; VNS + q: (d < 2 nsl)
+      // max / sum of unit d / 2 for pass q
+      unsigned long long wv[VNS + 4];
+      auto valid = [&](int i) {
+        if (i < VNS) return i < npass * nsl && tok(i / nsl) < M;
+        return i - VNS < npass && tok(i - VNS) < M && d < 2 * nsl;
+      };
+      auto addr = [&](int i) {
+        return i < VNS ? hp + ((size_t)(i % nsl) * FL_MAX_VERIFY + tok(i / nsl)) * 66 + 2 + d
+                       : hp + ((size_t)(d >> 1) * FL_MAX_VERIFY + tok(i - VNS)) * 66 + (d & 1);
+      };
+#pragma unroll
+      for (int i = 0; i < VNS + 4; ++i) wv[i] = valid(i) ? ld_coh_u64(addr(i)) : 0ull;
+      poll_tagged<VNS + 4>(p, wv, otag, addr, valid);
+      float* const mlw = reinterpret_cast<float*>(ks);  // [4][NWAVE][VNS][2] max, sum
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (valid(VNS + q)) mlw[((q * NWAVE + wave) * VNS + (d >> 1)) * 2 + (d & 1)] = __uint_as_float((uint32_t)wv[VNS + q]);
+      lds_barrier();
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (q < npass && tok(q) < M) {
+          const float* ml = mlw + (q * NWAVE + wave) * VNS * 2;
+          float mm = -INFINITY;
+          for (int u = 0; u < nsl; ++u) mm = fmaxf(mm, ml[2 * u]);
+          float L = 0.0f, O = 0.0f;
+#pragma unroll
+          for (int i = 0; i < VNS; ++i) {
+            if (i / nsl == q && i < npass * nsl) {
+              const int u = i % nsl;
+              const float e = (ml[2 * u] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml[2 * u] - mm);
+              L += ml[2 * u + 1] * e;
+              O += __uint_as_float((uint32_t)wv[i]) * e;
+            }
+          }
+          st_coh_u16(p.vattn + (size_t)tok(q) * p.D + hq * 64 + d, f2bf(O / L));
+        }
+      }
+      set_flag(flag, otag);
+    }
+    lds_barrier();
+  }
+  stamp(p, slot);
+}
+
+// Which verify attention runs: by tokens (no merge across workgroups; each unit runs its tokens
+// one after another over every key of its head) while tokens per unit x keys is at most
+// p.vtok_work, else by key slices (matrix cores, merged over the slices). Measured on the 3B
+// shape (40 heads, 256 workgroups) the two meet near 2 tokens per unit at 1024 keys. Returns the
+// number of ready flags its units set.
+__device__ __forceinline__ int verify_attn_flags(const DecodeParams& p, bool& by_tokens) {
+  const int G = grid_here();
+  int tpu, ngrp, nsl, kps;
+  verify_units(p.NH, p.M, G, tpu, ngrp);
+  by_tokens = tpu * max(p.pos, 1) <= p.vtok_work && p.NH * ngrp <= VF_ACT - VF_ATTN;
+  if (by_tokens) return p.NH * ngrp;
+  verify_slices(p, p.pos, p.NH, G, nsl, kps);
+  return p.NH * nsl;
 }
 
 __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
@@ -1801,11 +2262,10 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
   const int D = p.D, F = p.F, NH = p.NH, NKV = p.NKV, M = p.M, pos = p.pos;
   const int NQKV = (NH + 2 * NKV) * 64, HALF = NQKV / 2;
   const int ld = D + 8;
-  uint16_t* xs = reinterpret_cast<uint16_t*>(vsm);
-  float* part = reinterpret_cast<float*>(vsm + verify_xs_bytes(D));
-  uint16_t* att = reinterpret_cast<uint16_t*>(part + 4 * NWAVE * 256);
-  uint8_t* amk = reinterpret_cast<uint8_t*>(att + (VH + 2 * FL_MAX_VERIFY) * 64);
-  uint16_t* hres = reinterpret_cast<uint16_t*>(amk + VH * FL_MAX_VERIFY);  // [FL_MAX_VERIFY][16]
+  uint16_t* xs = reinterpret_cast<uint16_t*>(vsm);  // also the attention unit's region
+  uint16_t* nws = reinterpret_cast<uint16_t*>(vsm + verify_xs_bytes(D));  // RMSNorm weights [D]
+  float* part = reinterpret_cast<float*>(vsm + verify_xs_bytes(D) + verify_nw_bytes(D));
+  uint16_t* hres = reinterpret_cast<uint16_t*>(part + 4 * NWAVE * 256);  // [FL_MAX_VERIFY][16]
   for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + VH * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
   int slot = 0;  // optional timestamps, same slots as k_decode's
   stamp(p, slot);
@@ -1836,8 +2296,6 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     for (int i = tid; i < M * 16; i += NT)
       hres[i] = (uint16_t)f2bf(rbf(bf2f(p.w.embed[(size_t)token_at(i >> 4) * D + wg * 16 + (i & 15)]) * p.emb_mult));
 
-  int TPU, ngrp;
-  verify_units(NH, M, G, TPU, ngrp);
   for (int l = 0; l < params_here().NL; ++l) {
     const DecodeParams& p = params_here();
     const uint32_t e0 = p.epoch + 5u * (uint32_t)l;
@@ -1848,6 +2306,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     const uint32_t* const qkv_q = p.w.wqkv_q + (size_t)l * NQKV * (D >> 3);
     const uint32_t* const qkv_sz = p.w.wqkv_sz + (size_t)l * NQKV * (D >> 7);
     if (wg < NQKV / 16) {
+      stage_norm_w(p.w.attn_norm + (size_t)l * D, D, nws);
       for (int h0 = 0; h0 < M; h0 += VH) {
         const int mh = min(VH, M - h0);
         TileW tw;
@@ -1866,7 +2325,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
           stage_bf16(p.vh, D, h0, mh, 0, D, xs, ld);
         }
         lds_barrier();
-        norm_rows(xs, ld, mh, D, p.w.attn_norm + (size_t)l * D, p.eps, part);
+        norm_rows(xs, ld, mh, D, nws, p.eps, part);
         lds_barrier();
         if (h0 == 0) stamp(p, slot);
         for (int t = wg; t < NQKV / 16; t += G) {
@@ -1907,11 +2366,12 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     }
     stamp(p, slot);
     // ---------------- P2: attention ----------------
-    stamp(p, slot);
-    stamp(p, slot);
-    attention_verify(p, l, t_qkv, t_attn, att, amk, part);
-    stamp(p, slot);
-    stamp(p, slot);
+    bool by_tokens;
+    (void)verify_attn_flags(p, by_tokens);
+    if (by_tokens) attention_verify_tokens(p, l, t_qkv, t_attn, vsm, slot);
+    else attention_verify(p, l, t_qkv, t_attn, vsm, slot);
+    // the attention unit used the staged-rows region: the zero row again
+    for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + VH * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
     // ---------------- P3: O projection + residual ----------------
     if (owner) {
       const uint32_t* const o_q = p.w.wo_q + (size_t)l * D * (D >> 3);
@@ -1920,8 +2380,12 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
         const int mh = min(VH, M - h0);
         TileW tw;
         tile_load(o_q, o_sz, wg * 16, 16, D, 0, D >> 7, tw);
-        if (h0 == 0) wait_flags(p, vf + VF_ATTN, NH * ngrp, t_attn);
-        else lds_barrier();
+        if (h0 == 0) {
+          bool by_tokens;
+          wait_flags(p, vf + VF_ATTN, verify_attn_flags(p, by_tokens), t_attn);
+        } else {
+          lds_barrier();
+        }
         stage_bf16(p.vattn, D, h0, mh, 0, D, xs, ld);
         lds_barrier();
         if (h0 == 0) stamp(p, slot);
@@ -1948,22 +2412,22 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
       const uint32_t* const gu_q = p.w.wgu_q + (size_t)l * 2 * F * (D >> 3);
       const uint32_t* const gu_sz = p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7);
       // this workgroup's tiles wg, wg+G, ... in rounds of up to 4: the round's MFMAs run back to
-      // back into 4 accumulators, one publish and one epilogue per round. The first tile's
-      // weights are requested before the input wait, the rest once the inputs are in.
+      // back into 4 accumulators, one publish and one epilogue per round. The first round's
+      // weights are requested before the input wait, each later round's during the one before.
       const int nt = ((2 * F) / 16 - wg + G - 1) / G;
+      stage_norm_w(p.w.ffn_norm + (size_t)l * D, D, nws);
       for (int h0 = 0; h0 < M; h0 += VH) {
         const int mh = min(VH, M - h0);
         const bool last = h0 + VH >= M;
-        TileW tw[4] = {};
-        tile_load(gu_q, gu_sz, wg * 16, 16, D, 0, D >> 7, tw[0]);
+        TileW tw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)  // tiles past nt: an empty range, no memory access
+          tile_load(gu_q, gu_sz, (wg + i * G) * 16, i < nt ? 16 : 0, D, 0, D >> 7, tw[i]);
         if (h0 == 0) wait_flags(p, vf + VF_H1, D / 16, t_h1);
         else lds_barrier();
         stage_bf16(p.vh, D, h0, mh, 0, D, xs, ld);
-#pragma unroll
-        for (int i = 1; i < 4; ++i)
-          if (i < nt) tile_load(gu_q, gu_sz, (wg + i * G) * 16, 16, D, 0, D >> 7, tw[i]);
         lds_barrier();
-        norm_rows(xs, ld, mh, D, p.w.ffn_norm + (size_t)l * D, p.eps, part);
+        norm_rows(xs, ld, mh, D, nws, p.eps, part);
         lds_barrier();
         if (h0 == 0) stamp(p, slot);
         for (int b4 = 0; b4 < nt; b4 += 4) {
@@ -2083,15 +2547,6 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     const int mh = min(VH, M - h0);
     unsigned long long best = 0ull;
     if (wg < ntile || (p.feat && wg == 0)) {
-      if (h0 == 0) wait_flags(p, p.vflag + VF_H2, D / 16, t_fin);
-      else lds_barrier();
-      stage_bf16(p.vh, D, h0, mh, 0, D, xs, ld);
-      lds_barrier();
-      norm_rows(xs, ld, mh, D, p.w.final_norm, p.eps, part);
-      lds_barrier();
-      if (h0 == 0) stamp(p, slot);
-      if (p.feat && wg == 0)
-        for (int i = tid; i < mh * D; i += NT) p.feat[(size_t)h0 * D + i] = xs[(i / D) * ld + (i % D)];
       const int lane = tid & 63, wave = tid >> 6, r = lane & 15, c = lane >> 4;
       const int ksteps = D >> 5;
       const uint16_t* xrow = xs + (r < mh ? r : VH) * ld + c * 8;
@@ -2132,7 +2587,20 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
         lds_barrier();
       };
       uint4 bwa[SPW], bwb[SPW];
-      load_tile(wg, bwa);
+      load_tile(wg, bwa);  // the first tile's rows are requested before the input wait
+      if (h0 == 0) {
+        stage_norm_w(p.w.final_norm, D, nws);
+        wait_flags(p, p.vflag + VF_H2, D / 16, t_fin);
+      } else {
+        lds_barrier();
+      }
+      stage_bf16(p.vh, D, h0, mh, 0, D, xs, ld);
+      lds_barrier();
+      norm_rows(xs, ld, mh, D, nws, p.eps, part);
+      lds_barrier();
+      if (h0 == 0) stamp(p, slot);
+      if (p.feat && wg == 0)
+        for (int i = tid; i < mh * D; i += NT) p.feat[(size_t)h0 * D + i] = xs[(i / D) * ld + (i % D)];
       for (int t = wg; t < ntile; t += 2 * G) {
         load_tile(t + G, bwb);
         do_tile(t, bwa);
@@ -2220,10 +2688,12 @@ struct fl_state {
   unsigned long long* qkv;
   unsigned long long* part;
   uint16_t* vrows;              // verify exchange rows: h [FL_MAX_VERIFY][D], attn [..][D], act [..][F]
+  unsigned long long* vpart;    // verify attention slice partials [NH][VNS][FL_MAX_VERIFY][66]
   uint32_t* vflag;              // verify ready flags
   uint32_t* shist;              // fused sampling exchange: per-workgroup histograms
   unsigned long long* sword;    // ... bin totals, maxima, partial sums
   int att_spw;
+  int vkps, vtok_work;
   int coop;       // launch with hipLaunchCooperativeKernel (else a plain launch, the default)
   const void* kdec;  // the k_decode instantiation whose chunk budget fits the model
   int verify_ok;  // k_verify's dynamic LDS fits and a grid of it is co-resident
@@ -2357,9 +2827,12 @@ DecodeParams base_params(const fl_weights* w, fl_state* st, int pos) {
   p.vattn = st->vrows + (size_t)FL_MAX_VERIFY * st->d.dim;
   p.vact = st->vrows + (size_t)2 * FL_MAX_VERIFY * st->d.dim;
   p.vflag = st->vflag;
+  p.vpart = st->vpart;
   p.shist = st->shist;
   p.sword = st->sword;
   p.att_spw = st->att_spw;
+  p.vkps = st->vkps;
+  p.vtok_work = st->vtok_work;
   p.amax = st->amax;
   p.done = st->done;
   p.err = st->err;
@@ -2486,6 +2959,8 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
     st->since_clear = 0;
   }
   st->att_spw = 8;
+  st->vkps = 128;
+  st->vtok_work = 2048;
   st->spin_ticks = SPIN_TICKS;
   // Plain launches by default: one workgroup per CU is all that fits (LDS), the grid is one per
   // CU, and on a device not shared with concurrent work every workgroup is resident at once. A
@@ -2498,10 +2973,19 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
     const int v = atoi(e);
     if (v >= 1 && v <= 64) st->att_spw = v;
   }
+  if (const char* e = getenv("FLINT_AMD_VERIFY_SLICE_KEYS")) {  // tuning knob: keys per verify slice
+    const int v = atoi(e);
+    if (v >= 16 && v <= 65536) st->vkps = v & ~15;
+  }
+  if (const char* e = getenv("FLINT_AMD_VERIFY_TOKEN_WORK")) {  // tuning knob (0: always by slices)
+    const int v = atoi(e);
+    if (v >= 0) st->vtok_work = v;
+  }
   // speculative verify: its dynamic LDS (token rows staged for the matrix cores) must fit, and a
   // full grid of it must be co-resident
   st->verify_ok = 0;
-  if (D <= 4096 && 2 * F / 16 <= VF_WORDS - VF_ACT) {
+  // (one attention unit per workgroup: at least one per query head; one ready flag per head)
+  if (D <= 4096 && 2 * F / 16 <= VF_WORDS - VF_ACT && d->n_head <= cu && d->n_head <= VF_ACT - VF_ATTN) {
     const size_t vl = verify_lds_bytes(D);
     int vocc = 0;
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_verify),
@@ -2525,6 +3009,8 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   }
   if (rc == FL_OK) rc = uc_alloc(st, &st->vrows, (size_t)FL_MAX_VERIFY * (2 * D + F));
   if (rc == FL_OK) rc = uc_alloc(st, &st->vflag, (size_t)VF_WORDS);
+  if (rc == FL_OK && st->verify_ok)
+    rc = uc_alloc(st, &st->vpart, (size_t)d->n_head * VNS * FL_MAX_VERIFY * 66);
   if (rc == FL_OK) rc = uc_alloc(st, &st->shist, (size_t)G * 256);
   if (rc == FL_OK) rc = uc_alloc(st, &st->sword, (size_t)256 + 2 * G);
   if (rc == FL_OK) rc = dev_alloc(st, &st->amax, FL_MAX_VERIFY);

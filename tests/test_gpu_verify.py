@@ -18,12 +18,23 @@ from tests.helpers import (check_rows, compare_logits, fill_kv_random, log, make
 
 pytestmark = pytest.mark.gpu
 
+# The attention of a verify launch runs by tokens (a unit per query head and token group, every key
+# in turn) or by key slices (a unit per query head and key slice on the matrix cores, partials
+# merged), chosen by the launch's shape; FLINT_AMD_VERIFY_TOKEN_WORK at state creation forces one.
+MODES = {"tokens": "1000000000", "slices": "0"}
+
+
+@pytest.fixture(params=list(MODES))
+def attn_mode(request, monkeypatch):
+    monkeypatch.setenv("FLINT_AMD_VERIFY_TOKEN_WORK", MODES[request.param])
+    return request.param
+
 
 @pytest.mark.parametrize("name,pos,m", [("tiny", 0, 5), ("tiny", 77, 8), ("small", 130, 5),
                                         ("small", 200, 16), ("tiny", 300, 1), ("tiny", 3, 32),
                                         ("small", 60, 17), ("small", 250, 20), ("small", 90, 24),
                                         ("flint-3b-l1", 130, 28), ("flint-3b-l1", 300, 32)])
-def test_verify_chain_matches_oracle(dev, name, pos, m):
+def test_verify_chain_matches_oracle(dev, attn_mode, name, pos, m):
     args, sd, eng, orc = make_pair(name, seed=11)
     eng.setup_caches(1, 512)
     orc.setup_caches(eng.max_seq_length)
@@ -33,7 +44,7 @@ def test_verify_chain_matches_oracle(dev, name, pos, m):
     tout, lg, feat = eng.verify(toks.to(dev), pos)
     eng.check()
     (alt, _), (lo, ho) = oracle_pair(orc, lambda: orc.forward(toks, pos))
-    ties = check_rows(lg.cpu(), lo.float(), alt.float(), name, f"{name} chain pos={pos} M={m}")
+    ties = check_rows(lg.cpu(), lo.float(), alt.float(), name, f"{name} {attn_mode} chain pos={pos} M={m}")
     assert ties <= max(1, m // 8)
     assert torch.equal(tout.cpu(), torch.argmax(lg.cpu(), dim=-1).int())
     assert float((feat.cpu().float() - ho.float()).abs().max()) <= 0.25
@@ -54,7 +65,7 @@ def _random_tree(n, seed):
     ("small", 150, [-1, 0, 0, 1, 1, 2, 3, 5]),
     ("small", 180, _random_tree(24, 3)),
     ("flint-3b-l1", 220, _random_tree(32, 4))])
-def test_verify_tree_matches_oracle(dev, name, pos, parent):
+def test_verify_tree_matches_oracle(dev, attn_mode, name, pos, parent):
     """Draft trees (spec_tree.py:46-51) of 8, 24 and 32 nodes: depth = node depth, amask =
     ancestors + self. Widths above 16 run the GEMM phases in two passes of 16 token rows."""
     args, sd, eng, orc = make_pair(name, seed=12)
@@ -75,7 +86,7 @@ def test_verify_tree_matches_oracle(dev, name, pos, parent):
     tout, lg, feat = eng.verify(toks.to(dev), pos, depth=depth.to(dev), amask=amask.to(dev))
     eng.check()
     alt, lo = oracle_pair(orc, lambda: orc.forward(toks, pos, depth=depth, amask=amask)[0].float())
-    ties = check_rows(lg.cpu(), lo, alt, name, f"{name} tree M={m}")
+    ties = check_rows(lg.cpu(), lo, alt, name, f"{name} {attn_mode} tree M={m}")
     assert ties <= max(1, m // 8)
 
 
@@ -112,3 +123,27 @@ def test_verify_rejects_bad_arguments(dev):
     with pytest.raises(_lib.FlError) as e:
         eng.verify(toks[:4], 62)
     assert e.value.code == -2
+
+
+@pytest.mark.parametrize("name,pos", [("small", 40), ("small", 300), ("flint-3b-l1", 700)])
+def test_verify_rows_do_not_depend_on_width(dev, attn_mode, name, pos):
+    """A chain's first rows are computed the same way whatever the width (the GEMM rows are
+    independent, token m attends to the same keys, the attention mode and key slicing depend on
+    the context and the head count, here forced to one mode): verify of the first
+    five tokens equals rows 0..4 of verify of all eight bit for bit, and a repeated launch equals
+    the first (no dependence on workgroup timing)."""
+    args, sd, eng, orc = make_pair(name, seed=31)
+    eng.setup_caches(1, 1024)
+    orc.setup_caches(eng.max_seq_length)
+    fill_kv_random(eng, orc, pos, seed=pos)
+    g = torch.Generator().manual_seed(pos)
+    toks = torch.randint(0, args.vocab_size, (8,), generator=g, dtype=torch.int32).to(dev)
+    _, l8, f8 = eng.verify(toks, pos)
+    l8, f8 = l8.clone(), f8.clone()
+    _, l8b, _ = eng.verify(toks, pos)
+    _, l5, f5 = eng.verify(toks[:5], pos)
+    eng.check()
+    assert torch.equal(l8, l8b)
+    d = (l5.float() - l8[:5].float()).abs().max().item()
+    log(f"{name} pos={pos}: rows 0..4 at width 5 vs 8: max|d|={d:.3e}")
+    assert torch.equal(l5, l8[:5]) and torch.equal(f5, f8[:5])
