@@ -351,6 +351,8 @@ def main():
                     help="skip the speculative-verify latency (k = 4, 7 at context 1024)")
     ap.add_argument("--no-spec", action="store_true",
                     help="skip the speculative-loop timing (chain / tree with a known draft)")
+    ap.add_argument("--no-sampling", action="store_true",
+                    help="skip the sampler timings (standalone and fused into the decode launch)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="after timing, run one device-to-device copy of this many MiB (the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -369,14 +371,14 @@ def main():
     sd = synth_weights(args, seed=0, device=dev)
     model = Transformer.from_weights(args, sd, dev)
     torch.cuda.synchronize()
-    total = max(a.ctx + a.warmup + a.steps + 8, 1024 + 32,  # + the verify timing's context
-                0 if a.no_long else 8192 + 128 + 16)                # + config 3's
-    model.setup_caches(1, total)
+    # the cache holds the prompt and the generated tokens, as gpt-fast sizes it (generate.py:
+    # max_seq_length = T + max_new_tokens); the later legs re-size it for their own contexts
+    model.setup_caches(1, a.ctx + a.warmup + a.steps + 8)
     g = torch.Generator().manual_seed(1234)
     prompt = torch.randint(0, args.vocab_size, (a.ctx,), generator=g, dtype=torch.int32).to(dev)
     seq = torch.empty(a.ctx + a.warmup + a.steps, dtype=torch.int32, device=dev)
     seq[:a.ctx] = prompt
-    log(f"prefill {a.ctx} tokens (verify kernel, 16 tokens per launch)")
+    log(f"prefill {a.ctx} tokens (verify kernel, 32 tokens per launch)")
     from flint_amd.generate import prefill
     t0 = time.perf_counter()
     prefill(model, seq[:a.ctx - 1], 0)
@@ -442,9 +444,11 @@ def main():
         gemv = gemv_sweep(args, dev)
         log(f"config 1 (fl_gemv_int4, {gemv['rotation_bytes'] / 1e9:.2f} GB rotation): {gemv['shapes']}")
 
-    sampling = sampling_latency(args, dev)
-    sampling.update(fused_sampling(model, args, dev, a.ctx))
-    log(f"sampling over {args.vocab_size} logits: {sampling}")
+    sampling = None
+    if not a.no_sampling:
+        sampling = sampling_latency(args, dev)
+        sampling.update(fused_sampling(model, args, dev, a.ctx))
+        log(f"sampling over {args.vocab_size} logits: {sampling}")
 
     if a.copy_probe_mb > 0:
         n = a.copy_probe_mb * (1 << 20)

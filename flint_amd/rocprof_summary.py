@@ -1,6 +1,6 @@
 """Condense rocprofv3 CSV output into the short text kept under profiles/.
 
-    python -m flint_amd.rocprof_summary <dir> [--kernel k_decode] [--last N] [--skip-last S]
+    python -m flint_amd.rocprof_summary <dir> [--kernel k_decode] [--last N] [--skip-last S] [--by-grid]
         from `rocprofv3 --kernel-trace --stats -f csv`: the per-kernel stats table and, for the
         named kernel, the average duration of its last N dispatches (the timed window of a
         bench run, whose earlier dispatches are prefill / warmup at other context lengths);
@@ -31,7 +31,7 @@ def _short(name, width=60):
     return name if len(name) <= width else name[: width - 3] + "..."
 
 
-def summarise(d, kernel="k_decode", last=0, top=8, skip_last=0):
+def summarise(d, kernel="k_decode", last=0, top=8, skip_last=0, by_grid=False):
     out = []
     stats = _find(d, "kernel_stats.csv")
     with open(stats) as f:
@@ -62,6 +62,14 @@ def summarise(d, kernel="k_decode", last=0, top=8, skip_last=0):
             if gaps:
                 out.append(f"{kernel}: idle gap between consecutive timed dispatches: avg "
                            f"{sum(gaps) / len(gaps):.2f} us")
+        if by_grid:  # one line per launch shape (grid size) in the window
+            groups = {}
+            for r, dur in zip(disp[-len(win):], win):
+                groups.setdefault(int(r["Grid_Size_X"]), []).append(dur)
+            for gx in sorted(groups):
+                v = groups[gx]
+                out.append(f"{kernel}: grid {gx}: {len(v)} dispatches, avg {sum(v) / len(v):.2f} us, "
+                           f"min {min(v):.2f} us, max {max(v):.2f} us")
     return "\n".join(out)
 
 
@@ -132,6 +140,7 @@ def main(argv=None):
     ap.add_argument("--kernel", default="k_decode")
     ap.add_argument("--last", type=int, default=0)
     ap.add_argument("--skip-last", type=int, default=0)
+    ap.add_argument("--by-grid", action="store_true", help="also one line per grid size")
     ap.add_argument("--traffic", action="store_true")
     ap.add_argument("--pmc", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0)
@@ -142,7 +151,7 @@ def main(argv=None):
     elif a.traffic:
         print(traffic(a.dir[0], a.dir[1], a.kernel, a.last, a.copy_bytes, a.config))
     else:
-        print(summarise(a.dir[0], a.kernel, a.last, skip_last=a.skip_last))
+        print(summarise(a.dir[0], a.kernel, a.last, skip_last=a.skip_last, by_grid=a.by_grid))
 
 
 if __name__ == "__main__":
