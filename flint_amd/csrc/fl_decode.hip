@@ -1580,29 +1580,40 @@ __device__ void stage_bf16(const uint16_t* src, int stride, int m0, int mh, int 
 // rows m < M of xs: x <- bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)  (engine/model.py:237-242).
 // A row is shared by NWAVE / M waves (all 8 for one token), whose partial sums of squares meet
 // in red (NWAVE floats of LDS); the row loop has the same trip count in every wave, so the
-// barriers are uniform.
+// barriers are uniform. A lane's chunks are read four at a time (independent LDS reads in flight
+// instead of one round trip per chunk); nw is the weight vector in LDS.
 __device__ __forceinline__ void norm_rows(uint16_t* xs, int ld, int M, int D, const uint16_t* nw,
                                           float eps, float* red) {
+  constexpr int CB = 4;  // chunks per batch
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
   int wpr = 1;                                  // waves per row: a power of two, wpr * M <= NWAVE
   while (wpr * 2 * M <= NWAVE) wpr *= 2;
   const int rpp = NWAVE / wpr;                  // rows per pass
   const int sub = wave % wpr, nch = D >> 3;     // this wave's share of a row; 8-value chunks per row
+  const int step = wpr * 64;                    // chunk stride of a lane
+  const uint4* const nw4 = reinterpret_cast<const uint4*>(nw);
   for (int m0 = 0; m0 < M; m0 += rpp) {
     const int m = m0 + wave / wpr;
     const bool on = m < M;
     uint4* row = reinterpret_cast<uint4*>(xs + (on ? m : 0) * ld);
     float ss = 0.0f;
-    if (on)
-      for (int i = sub * 64 + lane; i < nch; i += wpr * 64) {
-        const uint4 v = row[i];
-        const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+    for (int c0 = sub * 64 + lane; c0 < nch; c0 += CB * step) {
+      uint4 v[CB];
+#pragma unroll
+      for (int b = 0; b < CB; ++b) {
+        const int i = c0 + b * step;
+        v[b] = (on && i < nch) ? row[i] : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int b = 0; b < CB; ++b) {
+        const uint32_t in[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           ss += bflo(in[j]) * bflo(in[j]);
           ss += bfhi(in[j]) * bfhi(in[j]);
         }
       }
+    }
     ss = wave_sum(ss);
     if (wpr > 1) {
       if (lane == 0) red[wave] = ss;
@@ -1612,18 +1623,28 @@ __device__ __forceinline__ void norm_rows(uint16_t* xs, int ld, int M, int D, co
     }
     const float r = 1.0f / sqrtf(ss / (float)D + eps);
     if (on)
-      for (int i = sub * 64 + lane; i < nch; i += wpr * 64) {
-        const uint4 v = row[i];
-        const uint4 g = reinterpret_cast<const uint4*>(nw)[i];
-        const uint32_t in[4] = {v.x, v.y, v.z, v.w};
-        const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
-        uint32_t o[4];
+      for (int c0 = sub * 64 + lane; c0 < nch; c0 += CB * step) {
+        uint4 v[CB], g[CB];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float na = rbf(bflo(in[j]) * r), nb = rbf(bfhi(in[j]) * r);
-          o[j] = pack_bf16x2(na * bflo(gw[j]), nb * bfhi(gw[j]));
+        for (int b = 0; b < CB; ++b) {
+          const int i = min(c0 + b * step, nch - 1);
+          v[b] = row[i];
+          g[b] = nw4[i];
         }
-        row[i] = make_uint4(o[0], o[1], o[2], o[3]);
+#pragma unroll
+        for (int b = 0; b < CB; ++b) {
+          if (c0 + b * step < nch) {
+            const uint32_t in[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+            const uint32_t gw[4] = {g[b].x, g[b].y, g[b].z, g[b].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float na = rbf(bflo(in[j]) * r), nb = rbf(bfhi(in[j]) * r);
+              o[j] = pack_bf16x2(na * bflo(gw[j]), nb * bfhi(gw[j]));
+            }
+            row[c0 + b * step] = make_uint4(o[0], o[1], o[2], o[3]);
+          }
+        }
       }
     if (wpr > 1) lds_barrier();  // red is reused by the next pass
   }
