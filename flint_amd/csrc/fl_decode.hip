@@ -1760,28 +1760,169 @@ __device__ __forceinline__ void verify_units(int NH, int M, int G, int& tpu, int
   ngrp = (M + tpu - 1) / tpu;
 }
 
+// One pass of the by-tokens attention over tokens m0 + mi0 .. m0 + mi0 + nt - 1 (nt <= TT) of
+// head hq: the waves take interleaved 8-key steps over the cached keys [0, pos), RB steps per
+// round of registers, each K / V step used for all TT queries (lane (kk = lane / 8, ds = lane % 8)
+// holds dims 8ds..8ds+7 of key kk: q.k is 4 dot2 plus a 3-step DPP sum, p.v 8 FMAs per query);
+// wave 0 folds in the new keys under the tree mask; the waves merge through LDS and the pass
+// writes bf16(o / sum) of its tokens to vattn. Query slots past nt compute on token m0 + mi0 and
+// are not written.
+template <int TT, int RB>
+__device__ __forceinline__ void attn_tokens_pass(const DecodeParams& p, int pos, int M, int m0,
+                                                 int mi0, int nt, int hq, int l, int g, float sc,
+                                                 const uint32_t* att32, const uint16_t* katt,
+                                                 const uint16_t* vatt, const uint8_t* amk,
+                                                 float* wpart) {
+  const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+  const int kk = lane >> 3, ds = lane & 7;
+  const int NKV = p.NKV;
+  const int ns = (pos + 7) >> 3;  // 8-key steps over the cached keys [0, pos)
+  const int nrounds = (ns + NWAVE * RB - 1) / (NWAVE * RB);
+  const size_t cbase = (size_t)(l * NKV + g) * p.S * 64;
+  const auto kb = buf_rsrc(p.kc + cbase, (uint32_t)pos * 128u);
+  const auto vb = buf_rsrc(p.vc + cbase, (uint32_t)pos * 128u);
+  uint4 kr[RB], vr[RB];
+  auto issue = [&](int r) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const uint32_t off = (uint32_t)(((r * NWAVE * RB + wave + NWAVE * i) * 8 + kk) * 128 + ds * 16);
+      kr[i] = buf_ld128(kb, off);
+      vr[i] = buf_ld128(vb, off);
+    }
+  };
+  if (nrounds > 0) issue(0);
+  uint32_t qv[TT][4];
+  float mx[TT], lsum[TT], o[TT][8];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int mi = mi0 + (t < nt ? t : 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[t][e] = att32[mi * 32 + ds * 4 + e];
+    mx[t] = -INFINITY;
+    lsum[t] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[t][e] = 0.0f;
+  }
+  for (int r = 0; r < nrounds; ++r) {
+    if (r > 0) issue(r);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      if (t >= nt) break;  // uniform: a pass with fewer tokens skips the unused query slots
+      float s[RB];
+      float rmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int st = r * NWAVE * RB + wave + NWAVE * i;
+        float a = dot2_bf16(kr[i].x, qv[t][0], 0.0f);
+        a = dot2_bf16(kr[i].y, qv[t][1], a);
+        a = dot2_bf16(kr[i].z, qv[t][2], a);
+        a = dot2_bf16(kr[i].w, qv[t][3], a);
+        a = sum8(a);
+        s[i] = (st * 8 + kk < pos) ? a * sc : -INFINITY;
+        rmax = fmaxf(rmax, s[i]);
+      }
+      const float mn = fmaxf(mx[t], max_stride8(rmax));
+      const float mu = (mn == -INFINITY) ? 0.0f : mn;
+      const float corr = __builtin_amdgcn_exp2f(mx[t] - mu);
+      lsum[t] *= corr;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[t][e] *= corr;
+      mx[t] = mn;
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const float pw = __builtin_amdgcn_exp2f(s[i] - mu);
+        lsum[t] += pw;
+        o[t][0] = __builtin_fmaf(pw, bflo(vr[i].x), o[t][0]);
+        o[t][1] = __builtin_fmaf(pw, bfhi(vr[i].x), o[t][1]);
+        o[t][2] = __builtin_fmaf(pw, bflo(vr[i].y), o[t][2]);
+        o[t][3] = __builtin_fmaf(pw, bfhi(vr[i].y), o[t][3]);
+        o[t][4] = __builtin_fmaf(pw, bflo(vr[i].z), o[t][4]);
+        o[t][5] = __builtin_fmaf(pw, bfhi(vr[i].z), o[t][5]);
+        o[t][6] = __builtin_fmaf(pw, bflo(vr[i].w), o[t][6]);
+        o[t][7] = __builtin_fmaf(pw, bfhi(vr[i].w), o[t][7]);
+      }
+    }
+  }
+  if (wave == 0) {  // the new tokens' keys, 8 per step, masked by amask[m][.]
+    for (int s0 = 0; s0 < M; s0 += 8) {
+      const int jn = s0 + kk;
+      const int js = min(jn, M - 1);
+      const uint32_t* kw = reinterpret_cast<const uint32_t*>(katt) + js * 32 + ds * 4;
+      const uint32_t* vw = reinterpret_cast<const uint32_t*>(vatt) + js * 32 + ds * 4;
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        if (t >= nt) break;
+        const int mi = mi0 + t;
+        const bool valid = jn < M && amk[mi * M + js] != 0;
+        float a = dot2_bf16(kw[0], qv[t][0], 0.0f);
+        a = dot2_bf16(kw[1], qv[t][1], a);
+        a = dot2_bf16(kw[2], qv[t][2], a);
+        a = dot2_bf16(kw[3], qv[t][3], a);
+        a = sum8(a);
+        const float sn = valid ? a * sc : -INFINITY;
+        const float mn = fmaxf(mx[t], max_stride8(sn));
+        const float mu = (mn == -INFINITY) ? 0.0f : mn;
+        const float corr = __builtin_amdgcn_exp2f(mx[t] - mu);
+        const float pw = __builtin_amdgcn_exp2f(sn - mu);
+        lsum[t] = lsum[t] * corr + pw;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[t][2 * e] = __builtin_fmaf(pw, bflo(vw[e]), o[t][2 * e] * corr);
+          o[t][2 * e + 1] = __builtin_fmaf(pw, bfhi(vw[e]), o[t][2 * e + 1] * corr);
+        }
+        mx[t] = mn;
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    lsum[t] = sum_stride8(lsum[t]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[t][e] = sum_stride8(o[t][e]);
+    float* mywp = wpart + (t * NWAVE + wave) * 66;
+    if (kk == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mywp[2 + ds * 8 + e] = o[t][e];
+    }
+    if (lane == 0) {
+      mywp[0] = mx[t];
+      mywp[1] = lsum[t];
+    }
+  }
+  lds_barrier();
+  if (tid < 64 * nt) {  // thread (token t, dim d): the waves merged in a fixed order
+    const int t = tid >> 6, d = tid & 63;
+    const float* wt = wpart + t * NWAVE * 66;
+    float M_ = -INFINITY, Ls = 0.0f, O = 0.0f;
+    for (int w = 0; w < NWAVE; ++w) M_ = fmaxf(M_, wt[w * 66]);
+    for (int w = 0; w < NWAVE; ++w) {
+      const float* wp = wt + w * 66;
+      const float e = (wp[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wp[0] - M_);
+      Ls += wp[1] * e;
+      O += wp[2 + d] * e;
+    }
+    st_coh_u16(p.vattn + (size_t)(m0 + mi0 + t) * p.D + hq * 64 + d, f2bf(O / Ls));
+  }
+  lds_barrier();
+}
+
 // Verify attention by tokens (engine/model.py:171-179 over the verify key set), for few tokens
 // at short and medium contexts, where it needs no merge across workgroups. A unit is one query head and a
 // group of TPU consecutive tokens (verify_units: the fewest that give every workgroup at most one
-// unit); the unit requests the head's cached keys and values once and runs its tokens one after
-// another. While the cache fits one round of registers (pos <= 8 * NWAVE * RB) the later tokens
-// reuse it. LDS att: q of the unit's tokens [VH][64], then the new k and v of the group
+// unit); the unit runs its tokens two at a time over the head's cached keys (attn_tokens_pass),
+// each key's K / V registers serving both queries. LDS att: q of the unit's tokens [VH][64], then the new k and v of the group
 // [FL_MAX_VERIFY][64] each; amk: the unit's amask rows [TPU][M]. The outputs go to the bf16
 // buffer vattn, then the unit's ready flag (VF_ATTN + group * NH + head).
 __device__ void attention_verify_tokens(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
                                         unsigned char* ua, int& slot) {
   uint16_t* const att = reinterpret_cast<uint16_t*>(ua);                        // q [VH][64], new k, v [32][64]
   uint8_t* const amk = ua + (VH + 2 * FL_MAX_VERIFY) * 64 * 2;                  // [VH][32]
-  float* const wpart = reinterpret_cast<float*>(amk + VH * FL_MAX_VERIFY);      // [NWAVE][66]
+  float* const wpart = reinterpret_cast<float*>(amk + VH * FL_MAX_VERIFY);      // [2][NWAVE][66]
   stamp(p, slot);
   stamp(p, slot);
-  constexpr int RB = 12;
-  const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
-  const int kk = lane >> 3, ds = lane & 7;
+  const int tid = tid_here();
   const int M = p.M, pos = p.pos, NH = p.NH, NKV = p.NKV, QPG = p.NH / p.NKV;
   const int HALF = (NH + 2 * NKV) * 32;  // tagged pairs per token
-  const int ns = (pos + 7) >> 3;         // 8-key steps over the cached keys [0, pos)
-  const int nrounds = (ns + NWAVE * RB - 1) / (NWAVE * RB);
   int TPU, ngrp;
   verify_units(NH, M, (int)gridDim.x, TPU, ngrp);
   const float sc = p.attn_scale * 1.4426950408889634f;
@@ -1791,19 +1932,6 @@ __device__ void attention_verify_tokens(const DecodeParams& p, int l, uint32_t q
   for (int u = blockIdx.x; u < NH * ngrp; u += gridDim.x) {
     const int g = u % NKV, rest = u / NKV, j = rest % QPG, grp = rest / QPG;
     const int hq = g * QPG + j, m0 = grp * TPU, mt = min(M, m0 + TPU) - m0;
-    const size_t cbase = (size_t)(l * NKV + g) * p.S * 64;
-    const auto kb = buf_rsrc(p.kc + cbase, (uint32_t)pos * 128u);
-    const auto vb = buf_rsrc(p.vc + cbase, (uint32_t)pos * 128u);
-    uint4 kr[RB], vr[RB];
-    auto issue = [&](int r) {
-#pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const uint32_t off = (uint32_t)(((r * NWAVE * RB + wave + NWAVE * i) * 8 + kk) * 128 + ds * 16);
-        kr[i] = buf_ld128(kb, off);
-        vr[i] = buf_ld128(vb, off);
-      }
-    };
-    if (nrounds > 0) issue(0);
     const int nq = 32 * mt;
     for (int i = tid; i < nq + 64 * M; i += NT) {
       int hh, tok, d;
@@ -1822,103 +1950,9 @@ __device__ void attention_verify_tokens(const DecodeParams& p, int l, uint32_t q
     }
     for (int i = tid; i < mt * M; i += NT) amk[i] = p.amask[m0 * M + i];
     lds_barrier();
-    for (int mi = 0; mi < mt; ++mi) {
-      const int m = m0 + mi;
-      uint32_t qv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) qv[e] = att32[mi * 32 + ds * 4 + e];
-      float mx = -INFINITY, lsum = 0.0f, o[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = 0.0f;
-      if (mi > 0 && nrounds > 1) issue(0);  // the registers hold the last round
-      for (int r = 0; r < nrounds; ++r) {
-        if (r > 0) issue(r);
-        float s[RB];
-        float rmax = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < RB; ++i) {
-          const int st = r * NWAVE * RB + wave + NWAVE * i;
-          float a = dot2_bf16(kr[i].x, qv[0], 0.0f);
-          a = dot2_bf16(kr[i].y, qv[1], a);
-          a = dot2_bf16(kr[i].z, qv[2], a);
-          a = dot2_bf16(kr[i].w, qv[3], a);
-          a = sum8(a);
-          s[i] = (st * 8 + kk < pos) ? a * sc : -INFINITY;
-          rmax = fmaxf(rmax, s[i]);
-        }
-        const float mn = fmaxf(mx, max_stride8(rmax));
-        const float mu = (mn == -INFINITY) ? 0.0f : mn;
-        const float corr = __builtin_amdgcn_exp2f(mx - mu);
-        lsum *= corr;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] *= corr;
-        mx = mn;
-#pragma unroll
-        for (int i = 0; i < RB; ++i) {
-          const float pw = __builtin_amdgcn_exp2f(s[i] - mu);
-          lsum += pw;
-          o[0] = __builtin_fmaf(pw, bflo(vr[i].x), o[0]);
-          o[1] = __builtin_fmaf(pw, bfhi(vr[i].x), o[1]);
-          o[2] = __builtin_fmaf(pw, bflo(vr[i].y), o[2]);
-          o[3] = __builtin_fmaf(pw, bfhi(vr[i].y), o[3]);
-          o[4] = __builtin_fmaf(pw, bflo(vr[i].z), o[4]);
-          o[5] = __builtin_fmaf(pw, bfhi(vr[i].z), o[5]);
-          o[6] = __builtin_fmaf(pw, bflo(vr[i].w), o[6]);
-          o[7] = __builtin_fmaf(pw, bfhi(vr[i].w), o[7]);
-        }
-      }
-      if (wave == 0) {  // the new tokens' keys, 8 per step, masked by amask[m][.]
-        for (int s0 = 0; s0 < M; s0 += 8) {
-          const int jn = s0 + kk;
-          const bool valid = jn < M && amk[mi * M + min(jn, M - 1)] != 0;
-          const int js = min(jn, M - 1);
-          const uint32_t* kw = reinterpret_cast<const uint32_t*>(katt) + js * 32 + ds * 4;
-          const uint32_t* vw = reinterpret_cast<const uint32_t*>(vatt) + js * 32 + ds * 4;
-          float a = dot2_bf16(kw[0], qv[0], 0.0f);
-          a = dot2_bf16(kw[1], qv[1], a);
-          a = dot2_bf16(kw[2], qv[2], a);
-          a = dot2_bf16(kw[3], qv[3], a);
-          a = sum8(a);
-          const float sn = valid ? a * sc : -INFINITY;
-          const float mn = fmaxf(mx, max_stride8(sn));
-          const float mu = (mn == -INFINITY) ? 0.0f : mn;
-          const float corr = __builtin_amdgcn_exp2f(mx - mu);
-          const float pw = __builtin_amdgcn_exp2f(sn - mu);
-          lsum = lsum * corr + pw;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            o[2 * e] = __builtin_fmaf(pw, bflo(vw[e]), o[2 * e] * corr);
-            o[2 * e + 1] = __builtin_fmaf(pw, bfhi(vw[e]), o[2 * e + 1] * corr);
-          }
-          mx = mn;
-        }
-      }
-      lsum = sum_stride8(lsum);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = sum_stride8(o[e]);
-      float* mywp = wpart + wave * 66;
-      if (kk == 0) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) mywp[2 + ds * 8 + e] = o[e];
-      }
-      if (lane == 0) {
-        mywp[0] = mx;
-        mywp[1] = lsum;
-      }
-      lds_barrier();
-      if (tid < 64) {
-        float M_ = -INFINITY, Ls = 0.0f, O = 0.0f;
-        for (int w = 0; w < NWAVE; ++w) M_ = fmaxf(M_, wpart[w * 66]);
-        for (int w = 0; w < NWAVE; ++w) {
-          const float* wp = wpart + w * 66;
-          const float e = (wp[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wp[0] - M_);
-          Ls += wp[1] * e;
-          O += wp[2 + tid] * e;
-        }
-        st_coh_u16(p.vattn + (size_t)m * p.D + hq * 64 + tid, f2bf(O / Ls));
-      }
-      lds_barrier();
-    }
+    // the unit's tokens, TT at a time: each key step's K / V registers serve all TT queries
+    for (int mi0 = 0; mi0 < mt; mi0 += 2)
+      attn_tokens_pass<2, 8>(p, pos, M, m0, mi0, min(2, mt - mi0), hq, l, g, sc, att32, katt, vatt, amk, wpart);
     set_flag(p.vflag + VF_ATTN + grp * NH + hq, otag);
   }
   stamp(p, slot);
