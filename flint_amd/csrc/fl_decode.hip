@@ -1652,8 +1652,10 @@ __device__ __forceinline__ void norm_rows(uint16_t* xs, int ld, int M, int D, co
 
 // The weights of one 16-row tile of an [N, K] int4 matrix over the K groups g0 .. g0+ng-1
 // (ng <= 32): this wave's groups g0 + wave + 8i, one 16-byte quarter-group per lane. Loading
-// does not depend on the token rows, so a phase requests its first tile before it waits for its
-// inputs and the next tile before it computes the current one.
+// does not depend on the token rows, so QKV and gate/up request tiles before they wait for their
+// inputs, and every phase requests the next tile before it computes the current one. Loads
+// complete in order: rows staged after a tile's request arrive only after that tile, so O and the
+// down projection (whose wait is short) request theirs once the rows are in.
 struct TileW {
   uint4 w[4];
   uint32_t s[4];
@@ -2434,7 +2436,6 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
       for (int h0 = 0; h0 < M; h0 += VH) {
         const int mh = min(VH, M - h0);
         TileW tw;
-        tile_load(o_q, o_sz, wg * 16, 16, D, 0, D >> 7, tw);
         if (h0 == 0) {
           bool by_tokens;
           wait_flags(p, vf + VF_ATTN, verify_attn_flags(p, by_tokens), t_attn);
@@ -2442,6 +2443,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
           lds_barrier();
         }
         stage_bf16(p.vattn, D, h0, mh, 0, D, xs, ld);
+        tile_load(o_q, o_sz, wg * 16, 16, D, 0, D >> 7, tw);  // after the rows, as in P5
         lds_barrier();
         if (h0 == 0) stamp(p, slot);
         fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -2474,13 +2476,18 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
       for (int h0 = 0; h0 < M; h0 += VH) {
         const int mh = min(VH, M - h0);
         const bool last = h0 + VH >= M;
+        // two tiles' weights requested before the input wait, two once the rows are in: loads
+        // complete in order, and the rows queued behind all four tiles arrived later (measured)
         TileW tw[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)  // tiles past nt: an empty range, no memory access
+        for (int i = 0; i < 2; ++i)  // tiles past nt: an empty range, no memory access
           tile_load(gu_q, gu_sz, (wg + i * G) * 16, i < nt ? 16 : 0, D, 0, D >> 7, tw[i]);
         if (h0 == 0) wait_flags(p, vf + VF_H1, D / 16, t_h1);
         else lds_barrier();
         stage_bf16(p.vh, D, h0, mh, 0, D, xs, ld);
+#pragma unroll
+        for (int i = 2; i < 4; ++i)
+          tile_load(gu_q, gu_sz, (wg + i * G) * 16, i < nt ? 16 : 0, D, 0, D >> 7, tw[i]);
         lds_barrier();
         norm_rows(xs, ld, mh, D, nws, p.eps, part);
         lds_barrier();
@@ -2519,7 +2526,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     // D < 1024, as a part is staged into one xs row), one group per wave. Workgroup w takes part
     // k = w % KP of the tiles w / KP, w / KP + G / KP, ...: it stages only its part's inputs (those
     // of the gate/up tiles behind them, by their ready flags), runs one group per wave for each of
-    // its tiles (weights requested before the input wait), and publishes each tile's part sum
+    // its tiles (weights requested once its inputs are in), and publishes each tile's part sum
     // (fp32, tagged) to p.part. The tile's owner (workgroup t) sums the parts in order and adds
     // the residual.
     int p5slot = slot;
@@ -2531,17 +2538,19 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
       const int k = wg % KP, kg0 = k * GPP, kgn = min(GPP, ng - kg0);
       const int nmine = (wg < GK * KP) ? max(0, (ntile - wg / KP + GK - 1) / GK) : 0;
       unsigned long long* const dpart = p.part;  // [tile][part][FL_MAX_VERIFY][16]
-      constexpr int TMAX = 8;  // tiles per workgroup whose weights are all requested up front
+      constexpr int TMAX = 8;  // tiles per workgroup whose weights are requested together
       for (int h0 = 0; h0 < M; h0 += VH) {
         const int mh = min(VH, M - h0);
         TileW1 tw[TMAX] = {};
-#pragma unroll
-        for (int i = 0; i < TMAX; ++i)
-          if (i < nmine) tile_load1(d_q, d_sz, (wg / KP + i * GK) * 16, F, kg0, kgn, tw[i]);
         if (nmine > 0) {
           if (h0 == 0) wait_flags(p, vf + VF_ACT + 16 * kg0, 16 * kgn, t_act);  // gate/up tiles of this part
           else lds_barrier();
           stage_bf16(p.vact, F, h0, mh, kg0 * 128, kgn * 128, xs, ld);
+          // the tiles' weights once the inputs are in (requested before the wait, the staged
+          // rows queued behind them: measured slower)
+#pragma unroll
+          for (int i = 0; i < TMAX; ++i)
+            if (i < nmine) tile_load1(d_q, d_sz, (wg / KP + i * GK) * 16, F, kg0, kgn, tw[i]);
           lds_barrier();
           if (h0 == 0) stamp(p, p5slot);
         }
