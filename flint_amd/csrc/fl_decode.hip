@@ -1454,24 +1454,32 @@ constexpr int VA_BYTES = VA_WP + NWAVE * 16 * 66 * 4;
 
 // dynamic LDS of k_verify: a region shared by the staged token rows of the GEMM phases
 // ([VH + 1][D + 8] bf16, row VH stays zero) and the attention unit (VA_BYTES), the current
-// RMSNorm weight vector [D] bf16, per-wave tile partials [4][8][256] floats and this workgroup's
-// rows of the residual h [32][16] (bf16)
+// RMSNorm weight vector as two masked copies (stage_norm_w: 2 x [D] bf16), per-wave tile partials
+// [4][8][256] floats and this workgroup's rows of the residual h [32][16] (bf16)
 __host__ __device__ inline size_t verify_xs_bytes(int D) {
   const size_t xs = ((size_t)(VH + 1) * (D + 8) * 2 + 15) & ~(size_t)15;
   return xs > (size_t)VA_BYTES ? xs : (size_t)VA_BYTES;
 }
-__host__ __device__ inline size_t verify_nw_bytes(int D) { return ((size_t)D * 2 + 15) & ~(size_t)15; }
+__host__ __device__ inline size_t verify_nw_bytes(int D) { return ((size_t)D * 4 + 15) & ~(size_t)15; }
 inline size_t verify_lds_bytes(int D) {
   return verify_xs_bytes(D) + verify_nw_bytes(D) + 4 * NWAVE * 256 * 4 + FL_MAX_VERIFY * 16 * 2;
 }
 
-// A norm weight vector (bf16 [D], D % 8 == 0) into LDS. Called before a phase's input wait: its
-// loads complete while the workgroup waits, so the norm after the wait reads no global memory
-// (a global load there would queue behind the weight tiles requested before the wait and wait
-// for all of them: loads complete in order).
+// A norm weight vector (bf16 [D], D % 8 == 0) into LDS as two copies of its bf16 pairs, one with
+// the high half cleared (w_2k, 0) and one with the low half cleared (0, w_2k+1): a v_dot2 of a
+// packed pair with them is the one product x_2k * w_2k (or x_2k+1 * w_2k+1), exact in fp32, with
+// no unpacking (norm_rows). Called before a phase's input wait: its loads complete while the
+// workgroup waits, so the norm after the wait reads no global memory (a global load there would
+// queue behind the weight tiles requested before the wait and wait for all of them: loads
+// complete in order).
 __device__ __forceinline__ void stage_norm_w(const uint16_t* __restrict__ nw, int D, uint16_t* nws) {
-  for (int i = tid_here(); i < (D >> 3); i += NT)
-    reinterpret_cast<uint4*>(nws)[i] = reinterpret_cast<const uint4*>(nw)[i];
+  uint4* const lo = reinterpret_cast<uint4*>(nws);
+  uint4* const hi = lo + (D >> 3);
+  for (int i = tid_here(); i < (D >> 3); i += NT) {
+    const uint4 w = reinterpret_cast<const uint4*>(nw)[i];
+    lo[i] = make_uint4(w.x & 0xFFFFu, w.y & 0xFFFFu, w.z & 0xFFFFu, w.w & 0xFFFFu);
+    hi[i] = make_uint4(w.x & 0xFFFF0000u, w.y & 0xFFFF0000u, w.z & 0xFFFF0000u, w.w & 0xFFFF0000u);
+  }
 }
 
 // verify's ready flags (uint32 words, tag << 16): per O tile (h1), per down tile (h2), per query
@@ -1581,7 +1589,11 @@ __device__ void stage_bf16(const uint16_t* src, int stride, int m0, int mh, int 
 // A row is shared by NWAVE / M waves (all 8 for one token), whose partial sums of squares meet
 // in red (NWAVE floats of LDS); the row loop has the same trip count in every wave, so the
 // barriers are uniform. A lane's chunks are read four at a time (independent LDS reads in flight
-// instead of one round trip per chunk); nw is the weight vector in LDS.
+// instead of one round trip per chunk); nw is the weight vector in LDS as stage_norm_w leaves it.
+// The squares are summed two per v_dot2 (fp32, in a different order than torch's reduction);
+// x * r is an fp32 multiply, rounded to bf16 by v_cvt_pk_bf16_f32, and its product with w one
+// v_dot2 against the masked weight pair (the bf16 product is exact in fp32, so the result is the
+// reference's bf16(bf16(x * r) * w); an exact zero product may come out as +0 where torch gives -0).
 __device__ __forceinline__ void norm_rows(uint16_t* xs, int ld, int M, int D, const uint16_t* nw,
                                           float eps, float* red) {
   constexpr int CB = 4;  // chunks per batch
@@ -1591,7 +1603,8 @@ __device__ __forceinline__ void norm_rows(uint16_t* xs, int ld, int M, int D, co
   const int rpp = NWAVE / wpr;                  // rows per pass
   const int sub = wave % wpr, nch = D >> 3;     // this wave's share of a row; 8-value chunks per row
   const int step = wpr * 64;                    // chunk stride of a lane
-  const uint4* const nw4 = reinterpret_cast<const uint4*>(nw);
+  const uint4* const nwlo = reinterpret_cast<const uint4*>(nw);
+  const uint4* const nwhi = nwlo + nch;
   for (int m0 = 0; m0 < M; m0 += rpp) {
     const int m = m0 + wave / wpr;
     const bool on = m < M;
@@ -1608,10 +1621,7 @@ __device__ __forceinline__ void norm_rows(uint16_t* xs, int ld, int M, int D, co
       for (int b = 0; b < CB; ++b) {
         const uint32_t in[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          ss += bflo(in[j]) * bflo(in[j]);
-          ss += bfhi(in[j]) * bfhi(in[j]);
-        }
+        for (int j = 0; j < 4; ++j) ss = dot2_bf16(in[j], in[j], ss);
       }
     }
     ss = wave_sum(ss);
@@ -1624,23 +1634,25 @@ __device__ __forceinline__ void norm_rows(uint16_t* xs, int ld, int M, int D, co
     const float r = 1.0f / sqrtf(ss / (float)D + eps);
     if (on)
       for (int c0 = sub * 64 + lane; c0 < nch; c0 += CB * step) {
-        uint4 v[CB], g[CB];
+        uint4 v[CB], gl[CB], gh[CB];
 #pragma unroll
         for (int b = 0; b < CB; ++b) {
           const int i = min(c0 + b * step, nch - 1);
           v[b] = row[i];
-          g[b] = nw4[i];
+          gl[b] = nwlo[i];
+          gh[b] = nwhi[i];
         }
 #pragma unroll
         for (int b = 0; b < CB; ++b) {
           if (c0 + b * step < nch) {
             const uint32_t in[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
-            const uint32_t gw[4] = {g[b].x, g[b].y, g[b].z, g[b].w};
+            const uint32_t wl[4] = {gl[b].x, gl[b].y, gl[b].z, gl[b].w};
+            const uint32_t wh[4] = {gh[b].x, gh[b].y, gh[b].z, gh[b].w};
             uint32_t o[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              const float na = rbf(bflo(in[j]) * r), nb = rbf(bfhi(in[j]) * r);
-              o[j] = pack_bf16x2(na * bflo(gw[j]), nb * bfhi(gw[j]));
+              const uint32_t n2 = pack_bf16x2(bflo(in[j]) * r, bfhi(in[j]) * r);  // bf16(x * r) pair
+              o[j] = pack_bf16x2(dot2_bf16(n2, wl[j], -0.0f), dot2_bf16(n2, wh[j], -0.0f));
             }
             row[c0 + b * step] = make_uint4(o[0], o[1], o[2], o[3]);
           }
