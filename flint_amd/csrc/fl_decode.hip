@@ -761,9 +761,59 @@ __device__ __forceinline__ void attn_slices(int pos, int NH, int G, int spw, int
 // (position pos, appended to the cache by this same launch) comes from the tagged q/k/v words
 // and is folded in by wave 0 of slice 0 as one extra key. Softmax uses the exact max of each
 // round of steps with an online rescale between rounds and for the new key. Waves merge through
-// LDS; slices > 0 publish (m, l, o) as tagged 64-bit words and slice 0 merges them in order.
+// LDS; slices > 0 publish (m, l, o) as tagged 64-bit words and slice 0 merges them in order (with
+// DEFER_MERGE_SLICES or more slices it returns its own (m, l, o) in mg and merges in the O phase).
+// With this many key slices or more, slice 0 leaves its merge to the O phase, after its own O
+// chunks are dequantised (it waits longest for the other slices, and its workgroup would otherwise
+// start that work last and be the last O producer). Measured against merging in the attention
+// phase: ctx 2048 / 3072 / 4096 / 8192 (4, 6, 6, 6 slices): -24, -66, -40, -48 us per step; with 2
+// or 3 slices the merge itself then waits behind the O phase's requests: +30 us (2), +5 us (3).
+constexpr int DEFER_MERGE_SLICES = 4;
+// A key-slice merge left to the caller: slice 0's (max, sum, o) after its own keys (wave 0, lane d)
+struct SliceMerge {
+  bool pend = false;  // workgroup-uniform
+  float M, Ls, O;
+  int hq, nsl;
+};
+// slice 0 of head hq folds in slices 1 .. nsl-1 in order (online rescale), four slices per batch,
+// and writes the head's output; run by wave 0 (lane d: output dim d)
+__device__ __forceinline__ void slice_merge(const DecodeParams& p, const SliceMerge& mg, uint32_t otag,
+                                            uint32_t ptag) {
+  const int d = tid_here();
+  float M = mg.M, Ls = mg.Ls, O = mg.O;
+  const int nsl = mg.nsl;
+  const unsigned long long* hpart = p.part + (size_t)mg.hq * MAX_SLICES * 66;
+  for (int c0 = 1; c0 < nsl; c0 += 4) {
+    unsigned long long wm[4], wl[4], wo[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const unsigned long long* cp = hpart + (size_t)min(c0 + b, nsl - 1) * 66;
+      wm[b] = ld_coh_u64(cp);
+      wl[b] = ld_coh_u64(cp + 1);
+      wo[b] = ld_coh_u64(cp + 2 + d);
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (c0 + b >= nsl) break;
+      const unsigned long long* cp = hpart + (size_t)(c0 + b) * 66;
+      auto ok = [ptag](unsigned long long v) { return (uint32_t)(v >> 32) == ptag; };
+      if (!ok(wm[b])) wm[b] = spin_until(p, wm[b], ok, [cp]() { return ld_coh_u64(cp); });
+      if (!ok(wl[b])) wl[b] = spin_until(p, wl[b], ok, [cp]() { return ld_coh_u64(cp + 1); });
+      if (!ok(wo[b]))
+        wo[b] = spin_until(p, wo[b], ok, [cp, d]() { return ld_coh_u64(cp + 2 + d); });
+      const float mc = __uint_as_float((uint32_t)wm[b]);
+      const float Mn = fmaxf(M, mc);
+      const float ea = __builtin_amdgcn_exp2f(M - Mn), eb = __builtin_amdgcn_exp2f(mc - Mn);
+      Ls = Ls * ea + __uint_as_float((uint32_t)wl[b]) * eb;
+      O = O * ea + __uint_as_float((uint32_t)wo[b]) * eb;
+      M = Mn;
+    }
+  }
+  st_coh_u32(p.attn + mg.hq * 64 + d, f2bf(O / Ls) | (otag << 16));
+}
+
 __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
-                                uint32_t ptag, float* ws, int& slot) {
+                                uint32_t ptag, float* ws, int& slot, SliceMerge& mg) {
   constexpr int RG = 4, NG = 2, RB = RG * NG;  // steps per wave per round, in groups of RG
   const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
   const int kk = lane >> 3, ds = lane & 7;
@@ -929,36 +979,15 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
       }
       st_coh_u64(pp + 2 + d, (unsigned long long)__float_as_uint(O) | tg);
     } else {
-      // slice 0 folds in slices 1 .. nsl-1 in order (online rescale), four slices per batch
-      for (int c0 = 1; c0 < nsl; c0 += 4) {
-        unsigned long long wm[4], wl[4], wo[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const unsigned long long* cp = hpart + (size_t)min(c0 + b, nsl - 1) * 66;
-          wm[b] = ld_coh_u64(cp);
-          wl[b] = ld_coh_u64(cp + 1);
-          wo[b] = ld_coh_u64(cp + 2 + d);
-        }
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          if (c0 + b >= nsl) break;
-          const unsigned long long* cp = hpart + (size_t)(c0 + b) * 66;
-          auto ok = [ptag](unsigned long long v) { return (uint32_t)(v >> 32) == ptag; };
-          if (!ok(wm[b])) wm[b] = spin_until(p, wm[b], ok, [cp]() { return ld_coh_u64(cp); });
-          if (!ok(wl[b])) wl[b] = spin_until(p, wl[b], ok, [cp]() { return ld_coh_u64(cp + 1); });
-          if (!ok(wo[b]))
-            wo[b] = spin_until(p, wo[b], ok, [cp, d]() { return ld_coh_u64(cp + 2 + d); });
-          const float mc = __uint_as_float((uint32_t)wm[b]);
-          const float Mn = fmaxf(M, mc);
-          const float ea = __builtin_amdgcn_exp2f(M - Mn), eb = __builtin_amdgcn_exp2f(mc - Mn);
-          Ls = Ls * ea + __uint_as_float((uint32_t)wl[b]) * eb;
-          O = O * ea + __uint_as_float((uint32_t)wo[b]) * eb;
-          M = Mn;
-        }
-      }
-      st_coh_u32(p.attn + hq * 64 + d, f2bf(O / Ls) | (otag << 16));
+      mg.M = M;
+      mg.Ls = Ls;
+      mg.O = O;
+      mg.hq = hq;
+      mg.nsl = nsl;
+      if (nsl < DEFER_MERGE_SLICES) slice_merge(p, mg, otag, ptag);
     }
   }
+  mg.pend = sl == 0 && nsl >= DEFER_MERGE_SLICES;
   __builtin_amdgcn_s_setprio(0);
   stamp(p, slot);
 }
@@ -1221,8 +1250,16 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
     stamp(p, slot);
 
     // ---------------- P2: GQA flash-decode attention ----------------
-    attention_phase(p, l, t_qkv, t_attn, e0 + 1u, ws, slot);
+    SliceMerge mg;
+    attention_phase(p, l, t_qkv, t_attn, e0 + 1u, ws, slot, mg);
     stamp(p, slot);
+    auto finish_merge = [&] {  // a deferred slice merge (wave 0, raised priority)
+      if (mg.pend && tid < 64) {
+        __builtin_amdgcn_s_setprio(1);
+        slice_merge(p, mg, t_attn, e0 + 1u);
+        __builtin_amdgcn_s_setprio(0);
+      }
+    };
 
     // ---------------- P3: O projection + residual ----------------
     row_range(D, wg, grid_here(), r0, rows);
@@ -1244,13 +1281,21 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
     };
     if (rows > 0) {
       stage_tagged<POLL_D>(p, p.attn, D, t_attn, xs, [&](auto refresh) {
-        if constexpr (C::G3 > 0) next_load_range<0, C::G3>(nx_gu, w_gu, s_gu);
-        gemv_predq<C::O, PD_O>(w_o, s_o, dql, [&](int i) {
-          if (i == PD_O - 1) refresh();
-        });
+        if (mg.pend) {  // this workgroup's O chunks first, then the merge, then the gate/up chunks
+          gemv_predq<C::O, PD_O>(w_o, s_o, dql, [&](int i) {});
+          finish_merge();
+          if constexpr (C::G3 > 0) next_load_range<0, C::G3>(nx_gu, w_gu, s_gu);
+          refresh();
+        } else {
+          if constexpr (C::G3 > 0) next_load_range<0, C::G3>(nx_gu, w_gu, s_gu);
+          gemv_predq<C::O, PD_O>(w_o, s_o, dql, [&](int i) {
+            if (i == PD_O - 1) refresh();
+          });
+        }
         if constexpr (C::G3 > 0) gemv_predq_reg<C::GU, C::G3, 0>(w_gu, s_gu, dqe, [](int) {});
       });
     } else {
+      finish_merge();
       early_gu();
     }
     stamp(p, slot);
