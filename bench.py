@@ -419,6 +419,12 @@ def main():
     spec = None
     if not a.no_spec:
         n = a.spec_tokens
+        # the cache holds the prompt, the n tokens and a pass's draft beyond them (at most
+        # MAX_VERIFY slots)
+        from flint_amd._lib import MAX_VERIFY
+        need = a.ctx + n + MAX_VERIFY + 8
+        if model.max_seq_length < need:
+            model.setup_caches(1, need)
         # the known continuation: plain greedy decode of n tokens after the prompt
         ref = torch.empty(a.ctx + n, dtype=torch.int32, device=dev)
         ref[:a.ctx] = prompt
