@@ -88,6 +88,8 @@ struct DecodeParams {
   uint16_t* feat;
   int D, NH, NKV, F, V, NL, S, pos;
   int att_spw;                 // attention: target 8-key steps per wave per slice
+  int gq_min;                  // attention on the matrix cores by KV group from this many cached keys
+  int gq_kps;                  // ... with at least this many keys per slice
   int vkps;                    // verify attention: cached keys per slice (a multiple of 16)
   int vtok_work;               // verify attention by tokens while tokens per unit x keys <= this
   float eps, emb_mult, attn_scale, resid_mult, logits_scaling;
@@ -995,6 +997,333 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
   stamp(p, slot);
 }
 
+// ---- long-context decode attention on the matrix cores, by KV group ----------------------------
+// One unit per (KV group g, key slice): the group's QPG query heads are the rows of the MFMA
+// tiles (engine/model.py:210-212 repeats the group's K / V for them; here the K / V rows are read
+// once for all QPG heads). Per 16-key chunk S^T = K Q^T with two 16x16x32 bf16 MFMAs, an online
+// softmax per head (exp2 domain), O^T = V^T P^T with 16x16x16 bf16 MFMAs and P split into three
+// bf16 terms (each product with a bf16 value exact in fp32): the same arithmetic as the verify
+// kernel's slice units, for one token. K rows and V^T go through LDS in rounds of GQ_VRK keys
+// (the first requested before the q wait); the last slice also takes the new key at pos. The 8
+// waves take interleaved chunks and merge through LDS. With one slice per group a unit writes
+// its heads' outputs; otherwise every unit publishes each head's (max, sum, o) as tagged fp32
+// words and the unit of slice s merges the heads j = s (mod nsl) over the slices (gqa_merge: in
+// a fixed order, so the result is deterministic). Units are numbered u = s * NKV + g, so a
+// group's slices run on workgroups of one XCD. Taken from p.gq_min cached keys on (4096: measured
+// against the per-head units, -18 / -15 / -35 us per step at ctx 4096 / 6144 / 8192, +40 to +55 at
+// 2048-3072), with slices of at least p.gq_kps = 128 keys (at most 32 per group).
+constexpr int GQ_VRK = 256;                      // keys per LDS round
+constexpr int GQ_VT_LD = GQ_VRK + 8;             // V^T row pitch (bf16)
+constexpr int GQ_ROWS = 8;                       // query heads per KV group this path takes
+constexpr int GQ_MAXSL = 32;                     // slices per group (4 per wave in the merge)
+constexpr int GQ_KS = 0, GQ_VT = GQ_KS + GQ_VRK * 128, GQ_WP = GQ_VT + 64 * GQ_VT_LD * 2;
+constexpr int GQ_BYTES = GQ_WP + NWAVE * GQ_ROWS * 66 * 4;
+static_assert(GQ_BYTES <= PD_MAX * 4 * NT * 16, "the GQA attention's LDS lives in the dequantised-chunk slots");
+static_assert((16 + 2) * 64 * 2 <= WS_FLOATS * 4, "q rows and the new key in ws");
+
+__device__ __forceinline__ void gqa_slices(int pos, int NKV, int G, int kps, int& nsl, int& spk) {
+  nsl = max(1, min(min(GQ_MAXSL, G / NKV), (pos + kps - 1) / kps));
+  spk = (pos + nsl - 1) / nsl;
+  nsl = max(1, (pos + spk - 1) / spk);
+}
+__device__ __forceinline__ bool use_gqa(const DecodeParams& p) {
+  return p.pos >= p.gq_min && p.NH / p.NKV <= GQ_ROWS && p.NKV <= grid_here();
+}
+
+// The unit of slice sl of KV group g merges the group's heads j = sl, sl + nsl, ... over the nsl
+// slices' published (max, sum, o): wave w takes slices w, w + 8, w + 16, w + 24 (lane d: their max,
+// sum and o[d], one batch), the waves' results meet in wp (NWAVE x 66 floats of LDS) and wave 0
+// combines them in wave order. Every thread of the workgroup calls it (it has barriers).
+__device__ void gqa_merge(const DecodeParams& p, int g, int sl, int nsl, float* wp, uint32_t otag,
+                        uint32_t ptag) {
+  const int lane = tid_here() & 63, wave = tid_here() >> 6;
+  const int QPG = p.NH / p.NKV;
+  for (int j = sl; j < QPG; j += nsl) {
+    const int d = lane;
+    const unsigned long long* hp = p.part + (size_t)(g * QPG + j) * MAX_SLICES * 66;
+    constexpr int SPW = GQ_MAXSL / NWAVE;
+    unsigned long long wv[3 * SPW];
+    auto valid = [&](int i) { return wave + NWAVE * (i / 3) < nsl; };
+    auto addr = [&](int i) {
+      const int sidx = min(wave + NWAVE * (i / 3), nsl - 1), k = i % 3;
+      return hp + (size_t)sidx * 66 + (k == 2 ? 2 + d : k);
+    };
+#pragma unroll
+    for (int i = 0; i < 3 * SPW; ++i) wv[i] = valid(i) ? ld_coh_u64(addr(i)) : 0ull;
+    poll_tagged<3 * SPW>(p, wv, ptag, addr, valid);
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {  // this wave's slices in order (online rescale)
+      if (wave + NWAVE * k < nsl) {
+        const float mc = __uint_as_float((uint32_t)wv[3 * k]);
+        const float Mn = fmaxf(M, mc);
+        const float ea = (M == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
+        const float eb = (mc == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mc - Mn);
+        L = L * ea + __uint_as_float((uint32_t)wv[3 * k + 1]) * eb;
+        O = O * ea + __uint_as_float((uint32_t)wv[3 * k + 2]) * eb;
+        M = Mn;
+      }
+    }
+    float* w = wp + wave * 66;
+    if (d == 0) {
+      w[0] = M;
+      w[1] = L;
+    }
+    w[2 + d] = O;
+    lds_barrier();
+    if (wave == 0) {
+      float MM = -INFINITY, LL = 0.0f, OO = 0.0f;
+      for (int q = 0; q < NWAVE; ++q) MM = fmaxf(MM, wp[q * 66]);
+      for (int q = 0; q < NWAVE; ++q) {
+        const float* x = wp + q * 66;
+        const float e = (x[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(x[0] - MM);
+        LL += x[1] * e;
+        OO += x[2 + d] * e;
+      }
+      st_coh_u32(p.attn + (g * QPG + j) * 64 + d, f2bf(OO / LL) | (otag << 16));
+    }
+    lds_barrier();  // wp is free again
+  }
+}
+
+__device__ void attention_gqa(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
+                              uint32_t ptag, float* ws, unsigned char* ua, int& slot) {
+  const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, c = lane >> 4;
+  const int pos = p.pos, NH = p.NH, NKV = p.NKV, QPG = NH / NKV;
+  int nsl, spk;
+  gqa_slices(pos, NKV, grid_here(), p.gq_kps, nsl, spk);
+  const int u = blockIdx.x;
+  if (u >= NKV * nsl) {
+    stamp(p, slot);
+    stamp(p, slot);
+    stamp(p, slot);
+    return;
+  }
+  const int g = u % NKV, sl = u / NKV;
+  const bool last = sl == nsl - 1;  // also takes the new key
+  const int k0 = sl * spk, nc = max(0, min(pos, k0 + spk) - k0);
+  const size_t cbase = (size_t)(l * NKV + g) * p.S * 64;
+  uint16_t* const ks = reinterpret_cast<uint16_t*>(ua + GQ_KS);
+  uint16_t* const vt = reinterpret_cast<uint16_t*>(ua + GQ_VT);
+  float* const wp = reinterpret_cast<float*>(ua + GQ_WP);
+  uint16_t* const qs = reinterpret_cast<uint16_t*>(ws);  // [16][64] q rows, then new k, new v
+  uint16_t* const kn = qs + 16 * 64;
+  uint16_t* const vn = kn + 64;
+  // cached keys [k0 + kb, k0 + kb + n) into rows 0 .. n-1 of ks and columns 0 .. n-1 of vt
+  auto load_round = [&](int kb, int n) {
+    const auto kr = buf_rsrc(p.kc + cbase + (size_t)(k0 + kb) * 64, (uint32_t)n * 128u);
+    const auto vr = buf_rsrc(p.vc + cbase + (size_t)(k0 + kb) * 64, (uint32_t)n * 128u);
+    uint4 kv[4], vv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // GQ_VRK * 8 = 2048 16-byte chunks each of K and V: 4 per thread
+      const int ci = tid + NT * i;
+      kv[i] = buf_ld128(kr, (uint32_t)ci * 16u);
+      vv[i] = buf_ld128(vr, (uint32_t)ci * 16u);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ci = tid + NT * i, key = ci >> 3, d0 = (ci & 7) * 8;
+      if (key >= n) continue;  // a row past the round: the new key may be staged there
+      *reinterpret_cast<uint4*>(ks + key * 64 + d0) = kv[i];
+      const uint32_t w4[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt[(d0 + 2 * e) * GQ_VT_LD + key] = (uint16_t)w4[e];
+        vt[(d0 + 2 * e + 1) * GQ_VT_LD + key] = (uint16_t)(w4[e] >> 16);
+      }
+    }
+  };
+  if (nc > 0) load_round(0, min(nc, GQ_VRK));  // cached keys: requested before the q wait
+  {  // q of the group's heads (rows 0 .. QPG-1) and, for the last slice, the new key's k and v
+    const int nq = QPG * 32, total = nq + (last ? 64 : 0);
+    const int HALFW = (NH + 2 * NKV) * 32;
+    (void)HALFW;
+    constexpr int B = 2;
+    auto word = [&](int idx) {
+      if (idx < nq) return p.qkv + (g * QPG + (idx >> 5)) * 32 + (idx & 31);
+      const int i2 = idx - nq;
+      return p.qkv + ((i2 >> 5) ? NH + NKV + g : NH + g) * 32 + (i2 & 31);
+    };
+    for (int base = 0; base < total; base += B * NT) {
+      unsigned long long v[B];
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        const int idx = base + tid + i * NT;
+        v[i] = idx < total ? ld_coh_u64(word(idx)) : 0ull;
+      }
+      poll_tagged<B>(p, v, qtag, [&](int i) { return word(base + tid + i * NT); },
+                     [&](int i) { return base + tid + i * NT < total; });
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        const int idx = base + tid + i * NT;
+        if (idx < total) {
+          uint16_t* dst = idx < nq ? qs + (idx >> 5) * 64 : ((idx - nq) >> 5 ? vn : kn);
+          const int dp = idx & 31;  // NEOX pair: dims dp and dp + 32
+          dst[dp] = (uint16_t)v[i];
+          dst[dp + 32] = (uint16_t)(v[i] >> 16);
+        }
+      }
+    }
+    for (int i = tid; i < (16 - QPG) * 32; i += NT) reinterpret_cast<uint32_t*>(qs + QPG * 64)[i] = 0u;
+  }
+  lds_barrier();
+  stamp(p, slot);
+  float mrun = -INFINITY, lrun = 0.0f;
+  fl_f32x4 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = fl_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint16_t* qrow = qs + r * 64 + c * 8;
+  // value columns past the round's keys up to the chunk edge must be finite (p = 0 there)
+  auto zero_tail = [&](int nr) {
+    for (int i = tid; i < 64 * 16; i += NT) {
+      const int col = nr + (i & 15);
+      if (col < ((nr + 15) & ~15)) vt[(i >> 4) * GQ_VT_LD + col] = 0;
+    }
+  };
+  auto put_new = [&](int t) {  // the new key into row / column t
+    for (int i = tid; i < 64; i += NT) {
+      ks[t * 64 + i] = kn[i];
+      vt[i * GQ_VT_LD + t] = vn[i];
+    }
+  };
+  int kb = 0, ncr = min(GQ_VRK, nc);
+  const bool fits = nc < GQ_VRK;  // the new key fits the (only) round of cached keys
+  bool new_in = last && fits, new_done = !last || fits;
+  if (new_in) put_new(ncr);
+  zero_tail(ncr + (new_in ? 1 : 0));
+  lds_barrier();
+  for (;;) {
+    const int nr = ncr + (new_in ? 1 : 0);
+    if (nr > 0) {
+      const uint4 qa = *reinterpret_cast<const uint4*>(qrow);
+      const uint4 qb = *reinterpret_cast<const uint4*>(qrow + 32);
+      for (int ch = wave; ch * 16 < nr; ch += NWAVE) {
+        const uint16_t* krow = ks + (ch * 16 + r) * 64 + c * 8;
+        fl_f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(fl_bf16x8, *reinterpret_cast<const uint4*>(krow)),
+            __builtin_bit_cast(fl_bf16x8, qa), st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(fl_bf16x8, *reinterpret_cast<const uint4*>(krow + 32)),
+            __builtin_bit_cast(fl_bf16x8, qb), st, 0, 0, 0);
+        // st[i]: score of head row r, round key ch * 16 + 4c + i
+        float sv[4], mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kl = ch * 16 + 4 * c + i;
+          sv[i] = kl < nr ? st[i] * p.attn_scale * 1.4426950408889634f : -INFINITY;
+          mx = fmaxf(mx, sv[i]);
+        }
+        mx = xor32_max(xor16_max(mx));
+        const float mn = fmaxf(mrun, mx);
+        const float mu = (mn == -INFINITY) ? 0.0f : mn;
+        const float corr = __builtin_amdgcn_exp2f(mrun - mu);
+        float pv[4];
+        float ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pv[i] = __builtin_amdgcn_exp2f(sv[i] - mu);
+          ps += pv[i];
+        }
+        ps = xor32_sum(xor16_sum(ps));
+        lrun = lrun * corr + ps;
+        mrun = mn;
+        uint32_t ph[2], pm[2], pl[2];  // p = hi + mid + lo, three bf16 terms
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float a0 = pv[2 * e], a1 = pv[2 * e + 1];
+          ph[e] = pack_bf16x2(a0, a1);
+          const float r0 = a0 - bflo(ph[e]), r1 = a1 - bfhi(ph[e]);
+          pm[e] = pack_bf16x2(r0, r1);
+          pl[e] = pack_bf16x2(r0 - bflo(pm[e]), r1 - bfhi(pm[e]));
+        }
+        typedef short fl_s16x4 __attribute__((ext_vector_type(4)));
+        const fl_s16x4 bh = __builtin_bit_cast(fl_s16x4, make_uint2(ph[0], ph[1]));
+        const fl_s16x4 bm = __builtin_bit_cast(fl_s16x4, make_uint2(pm[0], pm[1]));
+        const fl_s16x4 bl = __builtin_bit_cast(fl_s16x4, make_uint2(pl[0], pl[1]));
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          fl_f32x4 acc = o[dt];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] *= corr;
+          const fl_s16x4 va = __builtin_bit_cast(
+              fl_s16x4, *reinterpret_cast<const uint2*>(vt + (dt * 16 + r) * GQ_VT_LD + ch * 16 + 4 * c));
+          acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, bh, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, bm, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, bl, acc, 0, 0, 0);
+          o[dt] = acc;
+        }
+      }
+    }
+    if (kb + GQ_VRK < nc) {  // the next round of cached keys
+      lds_barrier();         // every wave is done with this one
+      kb += GQ_VRK;
+      ncr = min(GQ_VRK, nc - kb);
+      load_round(kb, ncr);
+      new_in = last && kb + GQ_VRK >= nc && ncr < GQ_VRK;  // the last round takes the new key if it fits
+      if (new_in) {
+        put_new(ncr);
+        new_done = true;
+      }
+      zero_tail(ncr + (new_in ? 1 : 0));
+      lds_barrier();
+    } else if (!new_done) {  // the new key in a round of its own (row 0)
+      lds_barrier();
+      ncr = 0;
+      put_new(0);
+      new_in = new_done = true;
+      zero_tail(1);
+      lds_barrier();
+    } else {
+      break;
+    }
+  }
+  stamp(p, slot);
+  // the waves' (max, sum, o) per head row: o[dt][i] at lane (r, c) is head row r, dim 16 dt + 4c + i
+  if (r < GQ_ROWS) {
+    float* w = wp + (wave * GQ_ROWS + r) * 66;
+    if (c == 0) {
+      w[0] = mrun;
+      w[1] = lrun;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[2 + dt * 16 + 4 * c + i] = o[dt][i];
+  }
+  lds_barrier();
+  auto unit_word = [&](int j, int wd) {  // the unit's word wd of head row j, waves in order
+    float mm = -INFINITY;
+    for (int w = 0; w < NWAVE; ++w) mm = fmaxf(mm, wp[(w * GQ_ROWS + j) * 66]);
+    if (wd == 0) return mm;
+    float val = 0.0f;
+    for (int w = 0; w < NWAVE; ++w) {
+      const float* x = wp + (w * GQ_ROWS + j) * 66;
+      const float e = (x[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(x[0] - mm);
+      val += x[wd] * e;
+    }
+    return val;
+  };
+  if (nsl == 1) {
+    for (int it = tid; it < QPG * 64; it += NT) {
+      const int j = it >> 6, d = it & 63;
+      st_coh_u32(p.attn + (g * QPG + j) * 64 + d, f2bf(unit_word(j, 2 + d) / unit_word(j, 1)) | (otag << 16));
+    }
+    lds_barrier();  // wp is done with: the O phase's dequantised chunks go to the same LDS
+  } else {
+    const unsigned long long tg = (unsigned long long)ptag << 32;
+    for (int it = tid; it < QPG * 66; it += NT) {
+      const int j = it / 66, wd = it - j * 66;
+      st_coh_u64(p.part + ((size_t)(g * QPG + j) * MAX_SLICES + sl) * 66 + wd,
+                 (unsigned long long)__float_as_uint(unit_word(j, wd)) | tg);
+    }
+    lds_barrier();  // as above
+    gqa_merge(p, g, sl, nsl, wp, otag, ptag);
+  }
+  stamp(p, slot);
+}
+
 // h[r0+2j], h[r0+2j+1] += bf16(bf16(acc) * rm) (bf16), run by the lead lane of row pair j. The
 // workgroup owns these rows for the whole step (O and down share the row split), so their
 // current values live in registers (ha, hb) of that lane and only the tagged result is stored.
@@ -1254,7 +1583,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
 
     // ---------------- P2: GQA flash-decode attention ----------------
     SliceMerge mg;
-    attention_phase(p, l, t_qkv, t_attn, e0 + 1u, ws, slot, mg);
+    bool gqa = false;
+    if constexpr (C::ROWS) gqa = use_gqa(p);  // (the large budget's registers have no room for it)
+    if constexpr (C::ROWS) {
+      if (gqa) attention_gqa(p, l, t_qkv, t_attn, e0 + 1u, ws, reinterpret_cast<unsigned char*>(dql), slot);
+    }
+    if (!gqa) attention_phase(p, l, t_qkv, t_attn, e0 + 1u, ws, slot, mg);
     stamp(p, slot);
     auto finish_merge = [&] {  // a deferred slice merge (wave 0, raised priority)
       if (mg.pend && tid < 64) {
@@ -2816,7 +3150,7 @@ struct fl_state {
   uint32_t* vflag;              // verify ready flags
   uint32_t* shist;              // fused sampling exchange: per-workgroup histograms
   unsigned long long* sword;    // ... bin totals, maxima, partial sums
-  int att_spw;
+  int att_spw, gq_min, gq_kps;
   int vkps, vtok_work;
   int coop;       // launch with hipLaunchCooperativeKernel (else a plain launch, the default)
   const void* kdec;  // the k_decode instantiation whose chunk budget fits the model
@@ -2955,6 +3289,8 @@ DecodeParams base_params(const fl_weights* w, fl_state* st, int pos) {
   p.shist = st->shist;
   p.sword = st->sword;
   p.att_spw = st->att_spw;
+  p.gq_min = st->gq_min;
+  p.gq_kps = st->gq_kps;
   p.vkps = st->vkps;
   p.vtok_work = st->vtok_work;
   p.amax = st->amax;
@@ -3083,6 +3419,8 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
     st->since_clear = 0;
   }
   st->att_spw = 8;
+  st->gq_min = 4096;
+  st->gq_kps = 128;
   st->vkps = 128;
   st->vtok_work = 2048;
   st->spin_ticks = SPIN_TICKS;
@@ -3096,6 +3434,11 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   if (const char* e = getenv("FLINT_AMD_ATT_STEPS")) {  // tuning knob: steps per wave per slice
     const int v = atoi(e);
     if (v >= 1 && v <= 64) st->att_spw = v;
+  }
+  if (const char* e = getenv("FLINT_AMD_GQA_MIN")) st->gq_min = std::max(0, atoi(e));  // tuning knob
+  if (const char* e = getenv("FLINT_AMD_GQA_KEYS")) {  // tuning knob: keys per GQA slice
+    const int v = atoi(e);
+    if (v >= 16 && v <= 65536) st->gq_kps = v;
   }
   if (const char* e = getenv("FLINT_AMD_VERIFY_SLICE_KEYS")) {  // tuning knob: keys per verify slice
     const int v = atoi(e);

@@ -138,6 +138,28 @@ def test_decode_multi_slice_attention(dev, monkeypatch, steps_per_wave):
         assert am_e == am_o or near_tie(lo, bar)
 
 
+@pytest.mark.parametrize("name,keys", [("tiny", 16), ("tiny", 300), ("small", 64), ("small", 4096)])
+def test_decode_gqa_attention(dev, monkeypatch, name, keys):
+    """The long-context attention on the matrix cores (one unit per KV group and key slice, the
+    group's query heads as MFMA rows), forced from the first key: one slice (the unit writes its
+    heads), many slices (merged by head over the slices), a new key that fits the last round or
+    takes a round of its own (256 cached keys), an empty cache."""
+    monkeypatch.setenv("FLINT_AMD_GQA_MIN", "0")
+    monkeypatch.setenv("FLINT_AMD_GQA_KEYS", str(keys))
+    args, sd, eng, orc = make_pair(name, seed=6)
+    bar = logit_bar(name)
+    eng.setup_caches(1, 1024)
+    orc.setup_caches(eng.max_seq_length)
+    for pos in (0, 9, 256, 517, 1000):
+        fill_kv_random(eng, orc, pos, seed=pos + 3)
+        tok = (7 * pos + 3) % args.vocab_size
+        am_e, am_o, (ok, d, within, same), lg, lo, fe, fo = _step_compare(eng, orc, tok, pos, name)
+        log(f"{name} gqa keys={keys}: pos={pos} max|dlogit|={d:.3e} ({within:.1%} within 2e-2) "
+            f"argmax eng={am_e} oracle={am_o}")
+        assert ok
+        assert am_e == am_o or near_tie(lo, bar)
+
+
 @pytest.mark.parametrize("name,budget", [("small", "large"), ("wide", None)])
 def test_decode_large_chunk_budget(dev, monkeypatch, name, budget):
     """The decode kernel is built for two per-thread chunk budgets; models that fit the small one

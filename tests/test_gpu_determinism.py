@@ -40,7 +40,7 @@ def _same(runs):
     return [i for i, r in enumerate(runs[1:], 1) if not torch.equal(r, ref)]
 
 
-@pytest.mark.parametrize("pos", [600, 1500, 4000])  # 2, 3 and 6 key slices per head
+@pytest.mark.parametrize("pos", [600, 1500, 4000, 4150])  # 2, 3, 6 slices per head; by KV group
 def test_decode_repeats_bitwise(model, pos):
     args, eng = model
     tok = torch.tensor([1234], dtype=torch.int32, device="cuda")
