@@ -1010,10 +1010,13 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
 // words and the unit of slice s merges the heads j = s (mod nsl) over the slices (gqa_merge: in
 // a fixed order, so the result is deterministic). Units are numbered u = s * NKV + g, so a
 // group's slices run on workgroups of one XCD. Taken from p.gq_min cached keys on (4096: measured
-// against the per-head units, -18 / -15 / -35 us per step at ctx 4096 / 6144 / 8192, +40 to +55 at
-// 2048-3072), with slices of at least p.gq_kps = 128 keys (at most 32 per group).
-constexpr int GQ_VRK = 256;                      // keys per LDS round
+// against the per-head units, -7 / 0 / -3 / -31 / -26 / -19 us per step at ctx 4096 / 5120 / 6144 /
+// 7168 / 8192 / 8320, +40 to +55 at 2048-3072), with slices of at least p.gq_kps = 128 keys (at
+// most 32 per group). Rounds of 288 keys keep one round per slice up to ctx 9216: with 256 a
+// context just past 8192 took a second, nearly empty round (+52 us at 8320; 288 costs ~4 us below).
+constexpr int GQ_VRK = 288;                      // keys per LDS round (32 slices x 288 keys: one round up to ctx 9216)
 constexpr int GQ_VT_LD = GQ_VRK + 8;             // V^T row pitch (bf16)
+constexpr int GQ_CPT = (GQ_VRK * 8 + NT - 1) / NT;  // 16-byte K (and V) chunks per thread per round
 constexpr int GQ_ROWS = 8;                       // query heads per KV group this path takes
 constexpr int GQ_MAXSL = 32;                     // slices per group (4 per wave in the merge)
 constexpr int GQ_KS = 0, GQ_VT = GQ_KS + GQ_VRK * 128, GQ_WP = GQ_VT + 64 * GQ_VT_LD * 2;
@@ -1114,15 +1117,15 @@ __device__ void attention_gqa(const DecodeParams& p, int l, uint32_t qtag, uint3
   auto load_round = [&](int kb, int n) {
     const auto kr = buf_rsrc(p.kc + cbase + (size_t)(k0 + kb) * 64, (uint32_t)n * 128u);
     const auto vr = buf_rsrc(p.vc + cbase + (size_t)(k0 + kb) * 64, (uint32_t)n * 128u);
-    uint4 kv[4], vv[4];
+    uint4 kv[GQ_CPT], vv[GQ_CPT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {  // GQ_VRK * 8 = 2048 16-byte chunks each of K and V: 4 per thread
+    for (int i = 0; i < GQ_CPT; ++i) {  // loads past the round's n keys read as 0, touching no memory
       const int ci = tid + NT * i;
       kv[i] = buf_ld128(kr, (uint32_t)ci * 16u);
       vv[i] = buf_ld128(vr, (uint32_t)ci * 16u);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < GQ_CPT; ++i) {
       const int ci = tid + NT * i, key = ci >> 3, d0 = (ci & 7) * 8;
       if (key >= n) continue;  // a row past the round: the new key may be staged there
       *reinterpret_cast<uint4*>(ks + key * 64 + d0) = kv[i];
