@@ -2200,6 +2200,24 @@ __device__ __forceinline__ void tile_mma1(const TileW1& tw, int ng, const uint16
   }
 }
 
+// The activation fragment tile_mma1 reads, from the bf16 [*, stride] rows src (device-coherent
+// loads) into the same place of xs: lane (r, c) of wave w copies row m0 + r (r < mh, w < ng),
+// columns k0 + 128 w + 32 c .. + 31, to xs row r, column 128 w + 32 c. Each lane later reads
+// back only its own fragment, so the copy needs no barrier.
+__device__ __forceinline__ void stage_frag(const uint16_t* src, int stride, int m0, int mh, int k0, int ng,
+                                           uint16_t* xs, int ld) {
+  const int lane = tid_here() & 63, wave = tid_here() >> 6;
+  const int r = lane & 15, c = lane >> 4;
+  if (r >= mh || wave >= ng) return;  // rows past mh read xs row VH (zero)
+  const auto rs = buf_rsrc(src + (size_t)m0 * stride, (uint32_t)mh * (uint32_t)stride * 2u);
+  uint4 v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = buf_ld128_coh(rs, (uint32_t)(r * stride + k0 + wave * 128 + c * 32 + e * 8) * 2u);
+  uint4* const dst = reinterpret_cast<uint4*>(xs + r * ld + wave * 128 + c * 32);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dst[e] = v[e];
+}
+
 // four tiles' partials at once: tile i's go to part + i * NWAVE * 256; ends with a barrier
 __device__ __forceinline__ void tile_publish4(float* part, const fl_f32x4 (&acc)[4]) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
@@ -2940,18 +2958,15 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
       for (int h0 = 0; h0 < M; h0 += VH) {
         const int mh = min(VH, M - h0);
         const bool last = h0 + VH >= M;
-        // two tiles' weights requested before the input wait, two behind the rows: loads
-        // complete in order, and the rows queued behind all four tiles arrived later (measured)
+        // the four tiles' weights requested before the input wait (they arrive during it; the
+        // rows queue behind them)
         TileW tw[4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)  // tiles past nt: an empty range, no memory access
+        for (int i = 0; i < 4; ++i)  // tiles past nt: an empty range, no memory access
           tile_load(gu_q, gu_sz, (wg + i * G) * 16, i < nt ? 16 : 0, D, 0, D >> 7, tw[i]);
         if (h0 == 0) wait_flags(p, vf + VF_H1, D / 16, t_h1);
         else lds_barrier();
         stage_norm_rows(p.vh, h0, mh, D, xs, ld, nws, p.eps, part, [] {});
-#pragma unroll
-        for (int i = 2; i < 4; ++i)
-          tile_load(gu_q, gu_sz, (wg + i * G) * 16, i < nt ? 16 : 0, D, 0, D >> 7, tw[i]);
         if (h0 == 0) stamp(p, slot);
         for (int b4 = 0; b4 < nt; b4 += 4) {
           fl_f32x4 acc[4] = {};
@@ -3004,15 +3019,15 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
         const int mh = min(VH, M - h0);
         TileW1 tw[TMAX] = {};
         if (nmine > 0) {
-          if (h0 == 0) wait_flags(p, vf + VF_ACT + 16 * kg0, 16 * kgn, t_act);  // gate/up tiles of this part
-          else lds_barrier();
-          stage_bf16(p.vact, F, h0, mh, kg0 * 128, kgn * 128, xs, ld);
-          // the tiles' weights once the inputs are in (requested before the wait, the staged
-          // rows queued behind them: measured slower)
+          // the tiles' weights before the input wait, then each lane's own activation fragment
+          // (a wave's MFMA reads only its K group) into the LDS place tile_mma1 reads it from:
+          // every lane reads back only what it wrote, so no barrier
 #pragma unroll
           for (int i = 0; i < TMAX; ++i)
             if (i < nmine) tile_load1(d_q, d_sz, (wg / KP + i * GK) * 16, F, kg0, kgn, tw[i]);
-          lds_barrier();
+          if (h0 == 0) wait_flags(p, vf + VF_ACT + 16 * kg0, 16 * kgn, t_act);  // gate/up tiles of this part
+          else lds_barrier();  // every wave is done with the previous pass's fragments
+          stage_frag(p.vact, F, h0, mh, kg0 * 128, kgn, xs, ld);
           if (h0 == 0) stamp(p, p5slot);
         }
         for (int j0 = 0; j0 < nmine; j0 += 4) {
