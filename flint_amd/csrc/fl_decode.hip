@@ -91,7 +91,7 @@ struct DecodeParams {
   int gq_min;                  // attention on the matrix cores by KV group from this many cached keys
   int gq_kps;                  // ... with at least this many keys per slice
   int vkps;                    // verify attention: cached keys per slice (a multiple of 16)
-  int vtok_work;               // verify attention by tokens while tokens per unit x keys <= this
+  int vtok_work;               // verify attention by tokens while (tokens per unit, 1 for <= 2) x keys <= this
   float eps, emb_mult, attn_scale, resid_mult, logits_scaling;
   uint32_t epoch;              // epoch of this launch's first phase (5 per layer)
   unsigned long long* prof;    // optional per-workgroup phase timestamps (100 MHz clock)
@@ -2779,15 +2779,18 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
 }
 
 // Which verify attention runs: by tokens (no merge across workgroups; each unit runs its tokens
-// one after another over every key of its head) while tokens per unit x keys is at most
-// p.vtok_work, else by key slices (matrix cores, merged over the slices). Measured on the 3B
-// shape (40 heads, 256 workgroups) the two meet near 2 tokens per unit at 1024 keys. Returns the
+// over every key of its head, two per pass) while w x keys is at most p.vtok_work (5120), with
+// w = 1 for units of one or two tokens (a pair costs about one token) and w = tokens per unit
+// above; else by key slices (matrix cores, merged over the slices). Measured on the 3B shape
+// (40 heads, 256 workgroups, ctx 512-4096) the two meet at ctx ~5000 for M <= 12 (1 or 2 tokens
+// per unit), ~1800 for M = 16 (3), ~1450 for M = 24 (4) and ~750 for M = 32 (6). Returns the
 // number of ready flags its units set.
 __device__ __forceinline__ int verify_attn_flags(const DecodeParams& p, bool& by_tokens) {
   const int G = grid_here();
   int tpu, ngrp, nsl, kps;
   verify_units(p.NH, p.M, G, tpu, ngrp);
-  by_tokens = tpu * max(p.pos, 1) <= p.vtok_work && p.NH * ngrp <= VF_ACT - VF_ATTN;
+  const int w = tpu <= 2 ? 1 : tpu;
+  by_tokens = w * max(p.pos, 1) <= p.vtok_work && p.NH * ngrp <= VF_ACT - VF_ATTN;
   if (by_tokens) return p.NH * ngrp;
   verify_slices(p, p.pos, p.NH, G, nsl, kps);
   return p.NH * nsl;
@@ -3501,7 +3504,7 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   st->gq_min = 4096;
   st->gq_kps = 128;
   st->vkps = 128;
-  st->vtok_work = 2048;
+  st->vtok_work = 5120;
   st->spin_ticks = SPIN_TICKS;
   // Plain launches by default: one workgroup per CU is all that fits (LDS), the grid is one per
   // CU, and on a device not shared with concurrent work every workgroup is resident at once. A

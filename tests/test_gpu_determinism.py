@@ -68,8 +68,9 @@ def _tree(m, seed):
     return torch.tensor(depth, dtype=torch.int32), mask
 
 
+# attention by tokens for the first three, by key slices for the last two
 @pytest.mark.parametrize("m,tree,pos", [(8, False, 1024), (5, False, 600), (24, True, 1024),
-                                        (32, False, 3000)])
+                                        (24, True, 2048), (32, False, 3000)])
 def test_verify_repeats_bitwise(model, m, tree, pos):
     args, eng = model
     g = torch.Generator(device="cuda").manual_seed(m)
