@@ -33,7 +33,8 @@ def attn_mode(request, monkeypatch):
 @pytest.mark.parametrize("name,pos,m", [("tiny", 0, 5), ("tiny", 77, 8), ("small", 130, 5),
                                         ("small", 200, 16), ("tiny", 300, 1), ("tiny", 3, 32),
                                         ("small", 60, 17), ("small", 250, 20), ("small", 90, 24),
-                                        ("flint-3b-l1", 130, 28), ("flint-3b-l1", 300, 32)])
+                                        ("flint-3b-l1", 130, 28), ("flint-3b-l1", 300, 32),
+                                        ("wide", 100, 8), ("wide", 40, 20)])  # D = 3072: 6 chunks a lane
 def test_verify_chain_matches_oracle(dev, attn_mode, name, pos, m):
     args, sd, eng, orc = make_pair(name, seed=11)
     eng.setup_caches(1, 512)
