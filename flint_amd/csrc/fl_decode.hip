@@ -461,11 +461,15 @@ __device__ void stage_tagged(const DecodeParams& p, const uint32_t* src, int n, 
 //    activation values once per phase. Partial sums meet in LDS.
 //  - by rows: 2^lg lanes per row (rs_lg), lane j of row r takes chunks j + i * 2^lg of row r,
 //    so a thread's partial sums add up in a register and a row's sum is a DPP reduction.
+//  - by row pairs: 2^lg lanes per pair of rows 2p, 2p+1 (rp_lg); lane j's i-th chunk is chunk
+//    j + (i / 2) * 2^lg of row 2p + i % 2, so chunks 2k and 2k+1 of a thread cover the same 32
+//    activations: each read of x from LDS serves both rows (gate and up of one output).
 struct ChunkMap {
   bool by_rows;
   int S;    // by stride
-  int lg;   // by rows
+  int lg;   // by rows / row pairs
   int cpr, rows;
+  bool pairs;
 };
 __device__ __forceinline__ int cs_stride(int K) {
   const int cpr = K >> 5;
@@ -478,6 +482,16 @@ __device__ __forceinline__ int rs_lg(int rows, int cpr) {
   while (lg > 0 && ((rows << lg) > NT || (1 << (lg - 1)) >= cpr)) --lg;
   return lg;
 }
+// lanes per row pair: a power of two <= 64, pairs * lanes <= NT, and no more lanes than chunks
+__device__ __host__ __forceinline__ int rp_lg(int rows, int cpr) {
+  const int pairs = (rows + 1) >> 1;
+  int lg = 6;
+  while (lg > 0 && ((pairs << lg) > NT || (1 << (lg - 1)) >= cpr)) --lg;
+  return lg;
+}
+__device__ __forceinline__ ChunkMap map_pairs(int K, int rows) {
+  return ChunkMap{true, NT, rp_lg(rows, K >> 5), K >> 5, rows, true};
+}
 __device__ __forceinline__ ChunkMap map_stride(int K, int rows, int S) {
   return ChunkMap{false, S, 0, K >> 5, rows};
 }
@@ -487,7 +501,8 @@ __device__ __forceinline__ ChunkMap map_rows(int K, int rows) {
 // chunk index of thread tid's i-th chunk; past every buffer's end where it has none (reads 0)
 __device__ __forceinline__ uint32_t chunk_f(const ChunkMap& m, int tid, int i) {
   if (m.by_rows) {
-    const int row = tid >> m.lg, c = (tid & ((1 << m.lg) - 1)) + (i << m.lg);
+    const int row = m.pairs ? 2 * (tid >> m.lg) + (i & 1) : tid >> m.lg;
+    const int c = (tid & ((1 << m.lg) - 1)) + ((m.pairs ? i >> 1 : i) << m.lg);
     return (row < m.rows && c < m.cpr) ? (uint32_t)(row * m.cpr + c) : 0x0FFFFFFFu;
   }
   return tid < m.S ? (uint32_t)(tid + i * m.S) : 0x0FFFFFFFu;
@@ -633,7 +648,7 @@ __device__ __forceinline__ int row_lanes_lg(int rows) {
 // GEMV modes: chunks by stride with partial sums in LDS (GM_STRIDE), the same with each thread
 // in one column of chunks (GM_COLUMN: its 32 x values read once, into registers), or by rows
 // (GM_ROWS: partial sums in registers, rows summed by DPP; no LDS partials, no barrier).
-enum { GM_STRIDE = 0, GM_COLUMN = 1, GM_ROWS = 2 };
+enum { GM_STRIDE = 0, GM_COLUMN = 1, GM_ROWS = 2, GM_PAIRS = 3 };
 
 // y[r] = sum_k x[k] * dq[r0+r, k] for the chunks loaded by gemv_load with mapping m (mode MODE);
 // x staged in xs; chunks i < PD come dequantised ahead: pre_dot(i, x4) is their dot with x.
@@ -654,6 +669,35 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
     for (int j = J0 + i * (NPRE - J0) / MC; j < J0 + (i + 1) * (NPRE - J0) / MC; ++j)
       next_load(nx, j, wn, sn);
   };
+  if constexpr (MODE == GM_PAIRS) {  // as GM_ROWS, two rows per lane group over the same chunks
+    static_assert(MC % 2 == 0, "chunks come in row pairs");
+    const int lg = m.lg, L = 1 << lg;
+    const int pr = tid >> lg, lj = tid & (L - 1);
+    const bool on = 2 * pr < rows;
+    __builtin_amdgcn_s_setprio(1);
+    float acc_a = 0.0f, acc_b = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MC / 2; ++k) {
+      const int c = lj + (k << lg);
+      const uint4* x4 = reinterpret_cast<const uint4*>(xs) + xslot(4 * min(c, cpr - 1));
+      const uint4 xr[4] = {x4[0], x4[1], x4[2], x4[3]};  // read once for both rows
+      const int i = 2 * k;
+      const bool ok = on && c < cpr;
+      const float ya = (i < PD) ? pre_dot(i, xr) : chunk_dot(wr[i], sr[i], xr, 0.0f);
+      acc_a += ok ? ya : 0.0f;
+      next(i);
+      __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time
+      const float yb = (i + 1 < PD) ? pre_dot(i + 1, xr) : chunk_dot(wr[i + 1], sr[i + 1], xr, 0.0f);
+      acc_b += ok ? yb : 0.0f;
+      next(i + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    acc_a = group_sum(acc_a, L);
+    acc_b = group_sum(acc_b, L);
+    if (on && lj == 0) epi(pr, acc_a, acc_b);
+    __builtin_amdgcn_s_setprio(0);
+    return;
+  }
   if constexpr (MODE == GM_ROWS) {
     const int lg = m.lg, L = 1 << lg;
     const int row = tid >> lg, lj = tid & (L - 1);
@@ -1511,9 +1555,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
   // chunk mappings: O and down keep each thread in one column of chunks; QKV and gate/up go by
   // rows in the instantiations that have them (C::ROWS), else by column / by stride
   const int sD = cs_stride(D), sF = cs_stride(F);
-  constexpr int M_QKV = C::ROWS ? GM_ROWS : GM_COLUMN, M_GU = C::ROWS ? GM_ROWS : GM_STRIDE;
+  constexpr int M_QKV = C::ROWS ? GM_ROWS : GM_COLUMN, M_GU = C::ROWS ? GM_PAIRS : GM_STRIDE;
   auto map_qkv = [&](int n) { return C::ROWS ? map_rows(D, n) : map_stride(D, n, sD); };
-  auto map_gu = [&](int n) { return C::ROWS ? map_rows(D, n) : map_stride(D, n, NT); };
+  auto map_gu = [&](int n) { return C::ROWS ? map_pairs(D, n) : map_stride(D, n, NT); };
   int r0, rows;
   row_range(NQKV, wg, G, r0, rows);
   gemv_load(p.w.wqkv_q, p.w.wqkv_sz, r0, rows, D, map_qkv(rows), w_qkv, s_qkv);
@@ -3202,7 +3246,8 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 // A GEMV phase's rows per workgroup fit its chunk budget: cap chunks per thread, dealt with
 // mode GM_STRIDE (stride NT), GM_COLUMN (stride cs_stride(k): NT / (k / 32) rows of chunks per
-// round) or GM_ROWS (2^rs_lg lanes per row: ceil((k / 32) / lanes) chunks each).
+// round), GM_ROWS (2^rs_lg lanes per row: ceil((k / 32) / lanes) chunks each) or GM_PAIRS
+// (2^rp_lg lanes per row pair: twice that).
 int phase_fits(int n, int k, int G, int cap, int mode) {
   int R = (n + G - 1) / G;
   R += (R & 1);
@@ -3212,6 +3257,10 @@ int phase_fits(int n, int k, int G, int cap, int mode) {
     int lg = 5;  // rs_lg
     while (lg > 0 && ((R << lg) > NT || (1 << (lg - 1)) >= cpr)) --lg;
     return R <= NT && (cpr + (1 << lg) - 1) >> lg <= cap;
+  }
+  if (mode == GM_PAIRS) {
+    const int lg = rp_lg(R, cpr);
+    return R <= 2 * NT && 2 * ((cpr + (1 << lg) - 1) >> lg) <= cap;
   }
   return mode == GM_COLUMN ? R <= (NT / cpr) * cap : (long)R * cpr <= (long)cap * NT;
 }
@@ -3470,7 +3519,7 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
     using C = decltype(c);
     return phase_fits(NQKV, D, G, C::QKV, C::ROWS ? GM_ROWS : GM_COLUMN) &&
            phase_fits(D, D, G, C::O, GM_COLUMN) &&
-           phase_fits(2 * F, D, G, C::GU, C::ROWS ? GM_ROWS : GM_STRIDE) &&
+           phase_fits(2 * F, D, G, C::GU, C::ROWS ? GM_PAIRS : GM_STRIDE) &&
            phase_fits(D, F, G, C::D, GM_COLUMN);
   };
   // FLINT_AMD_DECODE_BUDGET=large selects the large-budget instantiation for any model (tests)
