@@ -165,7 +165,7 @@ __device__ __forceinline__ T spin_until(const DecodeParams& p, T v, Ok ok, Ld ld
   while (!ok(v)) {
     __builtin_amdgcn_s_sleep(2);
     v = ld();
-    if ((++it & 63u) == 0) {
+    if (__builtin_expect((++it & 63u) == 0, 0)) {  // rare: out of the hot code
       if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
       if (__builtin_amdgcn_s_memrealtime() - t0 > p.spin_ticks) {
         __hip_atomic_store(p.err, (int32_t)FL_E_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -205,7 +205,7 @@ __device__ __forceinline__ void poll_tagged(const DecodeParams& p, unsigned long
 #pragma unroll
     for (int i = 0; i < B; ++i)
       if (valid(i) && !ok(v[i])) v[i] = ld_coh_u64(addr(i));
-    if ((it & 63u) == 63u) {
+    if (__builtin_expect((it & 63u) == 63u, 0)) {
       if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return;
       if (__builtin_amdgcn_s_memrealtime() - t0 > p.spin_ticks) {
         __hip_atomic_store(p.err, (int32_t)FL_E_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1633,7 +1633,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
     bool gqa = false;
     if constexpr (C::ROWS) gqa = use_gqa(p);  // (the large budget's registers have no room for it)
     if constexpr (C::ROWS) {
-      if (gqa) attention_gqa(p, l, t_qkv, t_attn, e0 + 1u, ws, reinterpret_cast<unsigned char*>(dql), slot);
+      // placed out of the layer loop's hot code (instruction cache misses of the common path)
+      if (__builtin_expect(gqa, 0)) [[unlikely]]
+        attention_gqa(p, l, t_qkv, t_attn, e0 + 1u, ws, reinterpret_cast<unsigned char*>(dql), slot);
     }
     if (!gqa) attention_phase(p, l, t_qkv, t_attn, e0 + 1u, ws, slot, mg);
     stamp(p, slot);
@@ -1961,7 +1963,7 @@ __device__ __forceinline__ void wait_flags(const DecodeParams& p, const uint32_t
         if (it == 0) t0 = __builtin_amdgcn_s_memrealtime();
         __builtin_amdgcn_s_sleep(2);
         if (!ok) v = buf_ld128_coh(rs, (uint32_t)lane * 16u);
-        if ((it & 63u) == 63u) {
+        if (__builtin_expect((it & 63u) == 63u, 0)) {
           if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
           if (__builtin_amdgcn_s_memrealtime() - t0 > p.spin_ticks) {
             __hip_atomic_store(p.err, (int32_t)FL_E_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
