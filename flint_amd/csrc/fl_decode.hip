@@ -2161,14 +2161,16 @@ __device__ __forceinline__ void stage_norm_rows(const uint16_t* src, int m0, int
 }
 
 // The weights of one 16-row tile of an [N, K] int4 matrix over the K groups g0 .. g0+ng-1
-// (ng <= 32): this wave's groups g0 + wave + 8i, one 16-byte quarter-group per lane. Loading
+// (ng <= NWAVE * TW_G): this wave's groups g0 + wave + 8i, one 16-byte quarter-group per lane. Loading
 // does not depend on the token rows, so QKV and gate/up request tiles before they wait for their
 // inputs, and every phase requests the next tile before it computes the current one. Loads
 // complete in order: rows staged after a tile's request arrive only after that tile, so O and the
 // down projection (whose wait is short) request theirs once the rows are in.
+constexpr int TW_G = 3;  // K groups per wave of a tile: D <= 3072 is at most 24 groups, 3 per wave
+static_assert(TW_G * NWAVE * 128 >= 64 * 8 * LM_MAXC, "a tile's K groups fit TW_G per wave at the largest D");
 struct TileW {
-  uint4 w[4];
-  uint32_t s[4];
+  uint4 w[TW_G];
+  uint32_t s[TW_G];
 };
 __device__ __forceinline__ void tile_load(const uint32_t* __restrict__ q, const uint32_t* __restrict__ sz,
                                           int n0, int rows, int K, int g0, int ng, TileW& tw) {
@@ -2178,7 +2180,7 @@ __device__ __forceinline__ void tile_load(const uint32_t* __restrict__ q, const 
   const auto wr = buf_rsrc(q + (size_t)n0 * (K >> 3), (uint32_t)rows * (uint32_t)(K >> 1));
   const auto sr = buf_rsrc(sz + (size_t)n0 * groups, (uint32_t)rows * (uint32_t)groups * 4u);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < TW_G; ++i) {
     const int u = wave + NWAVE * i;
     const uint32_t gg = (uint32_t)(g0 + u);
     const bool in = u < ng;
@@ -2193,7 +2195,7 @@ __device__ __forceinline__ void tile_mma(const TileW& tw, int ng, const uint16_t
   const int r = lane & 15, c = lane >> 4;
   const uint16_t* xrow = xs + (r < mh ? r : VH) * ld + c * 32;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < TW_G; ++i) {
     const int u = wave + NWAVE * i;
     if (u < ng) {  // wave-uniform
       uint4 xa[4];
@@ -2284,9 +2286,10 @@ __device__ __forceinline__ float tile_sum(const float* part, int t) {
 
 // tokens per attention unit and units per head (attention by tokens): the fewest tokens per unit
 // (at most VH) that give every workgroup at most one unit, where such a count exists
-__device__ __forceinline__ void verify_units(int NH, int M, int G, int& tpu, int& ngrp) {
-  tpu = min(VH, (NH * M + G - 1) / G);
-  while (tpu < min(VH, M) && NH * ((M + tpu - 1) / tpu) > G) ++tpu;
+__host__ __device__ inline void verify_units(int NH, int M, int G, int& tpu, int& ngrp) {
+  const int t0 = (NH * M + G - 1) / G, mx = M < VH ? M : VH;
+  tpu = t0 < VH ? t0 : VH;
+  while (tpu < mx && NH * ((M + tpu - 1) / tpu) > G) ++tpu;
   ngrp = (M + tpu - 1) / tpu;
 }
 
@@ -2831,17 +2834,31 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
 // (40 heads, 256 workgroups, ctx 512-4096) the two meet at ctx ~5000 for M <= 12 (1 or 2 tokens
 // per unit), ~1800 for M = 16 (3), ~1450 for M = 24 (4) and ~750 for M = 32 (6). Returns the
 // number of ready flags its units set.
-__device__ __forceinline__ int verify_attn_flags(const DecodeParams& p, bool& by_tokens) {
-  const int G = grid_here();
-  int tpu, ngrp, nsl, kps;
-  verify_units(p.NH, p.M, G, tpu, ngrp);
+// The host picks the k_verify instantiation by this rule (each holds one of the two attentions:
+// the slice attention alone is 35 KB of code, and without it the by-tokens layer loop fits the
+// instruction cache far better).
+__host__ __device__ inline bool verify_by_tokens(int NH, int M, int pos, int G, int vtok_work) {
+  int tpu, ngrp;
+  verify_units(NH, M, G, tpu, ngrp);
   const int w = tpu <= 2 ? 1 : tpu;
-  by_tokens = w * max(p.pos, 1) <= p.vtok_work && p.NH * ngrp <= VF_ACT - VF_ATTN;
-  if (by_tokens) return p.NH * ngrp;
-  verify_slices(p, p.pos, p.NH, G, nsl, kps);
-  return p.NH * nsl;
+  return w * (pos > 1 ? pos : 1) <= vtok_work && NH * ngrp <= VF_ACT - VF_ATTN;
+}
+// ready flags the attention units of mode AM (1: by tokens, 2: by key slices) set
+template <int AM>
+__device__ __forceinline__ int verify_attn_flags(const DecodeParams& p) {
+  const int G = grid_here();
+  if constexpr (AM == 1) {
+    int tpu, ngrp;
+    verify_units(p.NH, p.M, G, tpu, ngrp);
+    return p.NH * ngrp;
+  } else {
+    int nsl, kps;
+    verify_slices(p, p.pos, p.NH, G, nsl, kps);
+    return p.NH * nsl;
+  }
 }
 
+template <int AM>  // attention by tokens (1) or by key slices (2), as verify_by_tokens picks
 __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
   (void)pv;  // read through params_here()
   const DecodeParams& p = params_here();
@@ -2954,9 +2971,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     }
     stamp(p, slot);
     // ---------------- P2: attention ----------------
-    bool by_tokens;
-    (void)verify_attn_flags(p, by_tokens);
-    if (by_tokens) attention_verify_tokens(p, l, t_qkv, t_attn, vsm, slot);
+    if constexpr (AM == 1) attention_verify_tokens(p, l, t_qkv, t_attn, vsm, slot);
     else attention_verify(p, l, t_qkv, t_attn, vsm, slot);
     // the attention unit used the staged-rows region: the zero row again
     for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + VH * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -2968,8 +2983,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
         const int mh = min(VH, M - h0);
         TileW tw;
         if (h0 == 0) {
-          bool by_tokens;
-          wait_flags(p, vf + VF_ATTN, verify_attn_flags(p, by_tokens), t_attn);
+          wait_flags(p, vf + VF_ATTN, verify_attn_flags<AM>(p), t_attn);
         } else {
           lds_barrier();
         }
@@ -3587,13 +3601,13 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   // (one attention unit per workgroup: at least one per query head; one ready flag per head)
   if (D <= 4096 && 2 * F / 16 <= VF_WORDS - VF_ACT && d->n_head <= cu && d->n_head <= VF_ACT - VF_ATTN) {
     const size_t vl = verify_lds_bytes(D);
-    int vocc = 0;
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_verify),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)vl) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&vocc, reinterpret_cast<const void*>(k_verify),
-                                                     NT, vl) == hipSuccess &&
-        vocc >= 1)
-      st->verify_ok = 1;
+    st->verify_ok = 1;
+    for (const void* kv : {reinterpret_cast<const void*>(k_verify<1>), reinterpret_cast<const void*>(k_verify<2>)}) {
+      int vocc = 0;
+      if (!(hipFuncSetAttribute(kv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)vl) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&vocc, kv, NT, vl) == hipSuccess && vocc >= 1))
+        st->verify_ok = 0;
+    }
     (void)hipGetLastError();
   }
   int rc = FL_OK;
@@ -3751,11 +3765,12 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
   p.prof_slots = st->prof_slots;
   void* args[] = {&p};
   const unsigned lds = (unsigned)verify_lds_bytes(st->d.dim);
+  const void* kv = verify_by_tokens(st->d.n_head, m, pos, st->vgrid, st->vtok_work)
+                       ? reinterpret_cast<const void*>(k_verify<1>)
+                       : reinterpret_cast<const void*>(k_verify<2>);
   const hipError_t e =
-      st->coop ? hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_verify),
-                                            dim3(st->vgrid), dim3(NT), args, lds, as_stream(stream))
-               : hipLaunchKernel(reinterpret_cast<const void*>(k_verify), dim3(st->vgrid),
-                                 dim3(NT), args, lds, as_stream(stream));
+      st->coop ? hipLaunchCooperativeKernel(kv, dim3(st->vgrid), dim3(NT), args, lds, as_stream(stream))
+               : hipLaunchKernel(kv, dim3(st->vgrid), dim3(NT), args, lds, as_stream(stream));
   if (e != hipSuccess) return FL_E_LAUNCH;
   advance_epoch(st);
   return FL_OK;
