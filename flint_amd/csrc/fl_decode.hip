@@ -1073,8 +1073,10 @@ __device__ __forceinline__ void gqa_slices(int pos, int NKV, int G, int kps, int
   spk = (pos + nsl - 1) / nsl;
   nsl = max(1, (pos + spk - 1) / spk);
 }
-__device__ __forceinline__ bool use_gqa(const DecodeParams& p) {
-  return p.pos >= p.gq_min && p.NH / p.NKV <= GQ_ROWS && p.NKV <= grid_here();
+// whether a decode launch takes the attention by KV group (the host picks the k_decode
+// instantiation that holds it by the same rule)
+__host__ __device__ inline bool gqa_applies(int pos, int gq_min, int NH, int NKV, int G) {
+  return pos >= gq_min && NH / NKV <= GQ_ROWS && NKV <= G;
 }
 
 // The unit of slice sl of KV group g merges the group's heads j = sl, sl + nsl, ... over the nsl
@@ -1498,7 +1500,9 @@ __device__ unsigned long long sample_epilogue(const DecodeParams& p, int r0, int
   return best;
 }
 
-template <class C>
+// GQ: the attention by KV group in place of the per-head units (long contexts, gqa_applies; an
+// instantiation of its own, so that neither attention's code sits in the other's layer loop)
+template <class C, bool GQ = false>
 __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
   (void)pv;  // read through params_here()
   const DecodeParams& p = params_here();
@@ -1629,15 +1633,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
     stamp(p, slot);
 
     // ---------------- P2: GQA flash-decode attention ----------------
-    SliceMerge mg;
-    bool gqa = false;
-    if constexpr (C::ROWS) gqa = use_gqa(p);  // (the large budget's registers have no room for it)
-    if constexpr (C::ROWS) {
-      // placed out of the layer loop's hot code (instruction cache misses of the common path)
-      if (__builtin_expect(gqa, 0)) [[unlikely]]
-        attention_gqa(p, l, t_qkv, t_attn, e0 + 1u, ws, reinterpret_cast<unsigned char*>(dql), slot);
+    SliceMerge mg;  // (stays empty with GQ: no merge deferred to the O phase)
+    if constexpr (GQ) {
+      static_assert(C::ROWS, "the large budget's registers have no room for the attention by KV group");
+      attention_gqa(p, l, t_qkv, t_attn, e0 + 1u, ws, reinterpret_cast<unsigned char*>(dql), slot);
+    } else {
+      attention_phase(p, l, t_qkv, t_attn, e0 + 1u, ws, slot, mg);
     }
-    if (!gqa) attention_phase(p, l, t_qkv, t_attn, e0 + 1u, ws, slot, mg);
     stamp(p, slot);
     auto finish_merge = [&] {  // a deferred slice merge (wave 0, raised priority)
       if (mg.pend && tid < 64) {
@@ -3300,7 +3302,8 @@ struct fl_state {
   int att_spw, gq_min, gq_kps;
   int vkps, vtok_work;
   int coop;       // launch with hipLaunchCooperativeKernel (else a plain launch, the default)
-  const void* kdec;  // the k_decode instantiation whose chunk budget fits the model
+  const void* kdec;     // the k_decode instantiation whose chunk budget fits the model
+  const void* kdec_gq;  // ... with the attention by KV group (small budget only; else null)
   int verify_ok;  // k_verify's dynamic LDS fits and a grid of it is co-resident
   unsigned long long* amax;
   uint32_t* done;
@@ -3490,10 +3493,12 @@ int decode_launch(const fl_weights* w, fl_state* st, const int32_t* token_in, ui
   p.prof = st->prof;
   p.prof_slots = st->prof_slots;
   void* args[] = {&p};
+  const void* kd = st->kdec_gq && gqa_applies(pos, st->gq_min, st->d.n_head, st->d.n_kv_head, st->grid)
+                       ? st->kdec_gq
+                       : st->kdec;
   const hipError_t e =
-      st->coop ? hipLaunchCooperativeKernel(st->kdec, dim3(st->grid), dim3(NT), args, 0,
-                                            as_stream(stream))
-               : hipLaunchKernel(st->kdec, dim3(st->grid), dim3(NT), args, 0, as_stream(stream));
+      st->coop ? hipLaunchCooperativeKernel(kd, dim3(st->grid), dim3(NT), args, 0, as_stream(stream))
+               : hipLaunchKernel(kd, dim3(st->grid), dim3(NT), args, 0, as_stream(stream));
   if (e != hipSuccess) return FL_E_LAUNCH;
   advance_epoch(st);
   return FL_OK;
@@ -3547,12 +3552,21 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kdec, NT, 0) != hipSuccess)
     return FL_E_HIP;
   if (occ < 1 || cu < 1) return FL_E_LAUNCH;
+  const void* kdec_gq = nullptr;
+  if (small) {
+    int occ_gq = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ_gq, reinterpret_cast<const void*>(k_decode<ChunksSmall, true>),
+                                                     NT, 0) != hipSuccess)
+      return FL_E_HIP;
+    if (occ_gq >= 1) kdec_gq = reinterpret_cast<const void*>(k_decode<ChunksSmall, true>);
+  }
   fl_state* st = (fl_state*)calloc(1, sizeof(fl_state));
   if (!st) return FL_E_HIP;
   st->d = *d;
   st->max_seq = max_seq;
   st->grid = G;
   st->kdec = kdec;
+  st->kdec_gq = kdec_gq;
   st->vgrid = cu;
   st->kc = k_cache;
   st->vc = v_cache;
