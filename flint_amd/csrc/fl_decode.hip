@@ -784,14 +784,17 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
 // workgroup, whose 8 waves take interleaved steps so that each group of 8 steps covers 64
 // consecutive keys. `spw` is the target number of steps per wave: slices = ceil(steps /
 // (8 * spw)), at most G / NH, at least 1 (the new key at pos always has a slice).
-__device__ __forceinline__ void attn_slices(int pos, int NH, int G, int spw, int& nsl, int& sps) {
+__host__ __device__ inline void attn_slices(int pos, int NH, int G, int spw, int& nsl, int& sps) {
   const int ns = (pos + 7) >> 3;
   const int per = NWAVE * spw;
-  nsl = max(1, (ns + per - 1) / per);
-  const int cap = max(1, min(MAX_SLICES, G / NH));
+  nsl = (ns + per - 1) / per;
+  if (nsl < 1) nsl = 1;
+  int cap = G / NH < MAX_SLICES ? G / NH : MAX_SLICES;
+  if (cap < 1) cap = 1;
   if (nsl > cap) nsl = cap;
   sps = (ns + nsl - 1) / nsl;
-  nsl = sps > 0 ? max(1, (ns + sps - 1) / sps) : 1;
+  nsl = sps > 0 ? (ns + sps - 1) / sps : 1;
+  if (nsl < 1) nsl = 1;
 }
 
 // GQA flash-decode attention of one layer (engine/model.py:171-179: q.k^T * scale, softmax and
@@ -858,6 +861,9 @@ __device__ __forceinline__ void slice_merge(const DecodeParams& p, const SliceMe
   st_coh_u32(p.attn + mg.hq * 64 + d, f2bf(O / Ls) | (otag << 16));
 }
 
+// DEFER: the kernel instantiation that leaves slice 0's merge to the O phase from
+// DEFER_MERGE_SLICES slices on (the other one merges here whatever the slice count)
+template <bool DEFER>
 __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uint32_t otag,
                                 uint32_t ptag, float* ws, int& slot, SliceMerge& mg) {
   // steps per wave per round, in groups of RG: a group whose first step lies past the slice is
@@ -1033,10 +1039,10 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
       mg.O = O;
       mg.hq = hq;
       mg.nsl = nsl;
-      if (nsl < DEFER_MERGE_SLICES) slice_merge(p, mg, otag, ptag);
+      if (!DEFER || nsl < DEFER_MERGE_SLICES) slice_merge(p, mg, otag, ptag);
     }
   }
-  mg.pend = sl == 0 && nsl >= DEFER_MERGE_SLICES;
+  mg.pend = DEFER && sl == 0 && nsl >= DEFER_MERGE_SLICES;
   __builtin_amdgcn_s_setprio(0);
   stamp(p, slot);
 }
@@ -1500,9 +1506,12 @@ __device__ unsigned long long sample_epilogue(const DecodeParams& p, int r0, int
   return best;
 }
 
-// GQ: the attention by KV group in place of the per-head units (long contexts, gqa_applies; an
-// instantiation of its own, so that neither attention's code sits in the other's layer loop)
-template <class C, bool GQ = false>
+// AT, the attention of this instantiation: per-head units merging their slices in the attention
+// phase (0) or, from DEFER_MERGE_SLICES slices on, in the O phase (1); by KV group (2, long
+// contexts, gqa_applies). One instantiation each, picked by the host per launch, so that no
+// attention's code sits in another's layer loop (the layer loop of the first is 58 KB, inside the
+// 64 KB instruction cache; with the deferred merge in it, 67 KB).
+template <class C, int AT>
 __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
   (void)pv;  // read through params_here()
   const DecodeParams& p = params_here();
@@ -1633,12 +1642,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
     stamp(p, slot);
 
     // ---------------- P2: GQA flash-decode attention ----------------
-    SliceMerge mg;  // (stays empty with GQ: no merge deferred to the O phase)
-    if constexpr (GQ) {
+    SliceMerge mg;  // (stays empty unless AT == 1: no merge deferred to the O phase)
+    if constexpr (AT == 2) {
       static_assert(C::ROWS, "the large budget's registers have no room for the attention by KV group");
       attention_gqa(p, l, t_qkv, t_attn, e0 + 1u, ws, reinterpret_cast<unsigned char*>(dql), slot);
     } else {
-      attention_phase(p, l, t_qkv, t_attn, e0 + 1u, ws, slot, mg);
+      attention_phase<AT == 1>(p, l, t_qkv, t_attn, e0 + 1u, ws, slot, mg);
     }
     stamp(p, slot);
     auto finish_merge = [&] {  // a deferred slice merge (wave 0, raised priority)
@@ -3302,8 +3311,10 @@ struct fl_state {
   int att_spw, gq_min, gq_kps;
   int vkps, vtok_work;
   int coop;       // launch with hipLaunchCooperativeKernel (else a plain launch, the default)
-  const void* kdec;     // the k_decode instantiation whose chunk budget fits the model
-  const void* kdec_gq;  // ... with the attention by KV group (small budget only; else null)
+  // the k_decode instantiations of the chunk budget that fits the model, by attention: per-head
+  // units (0), with the slice merge deferred to the O phase (1), by KV group (2; small budget only,
+  // else null)
+  const void* kdec[3];
   int verify_ok;  // k_verify's dynamic LDS fits and a grid of it is co-resident
   unsigned long long* amax;
   uint32_t* done;
@@ -3493,9 +3504,14 @@ int decode_launch(const fl_weights* w, fl_state* st, const int32_t* token_in, ui
   p.prof = st->prof;
   p.prof_slots = st->prof_slots;
   void* args[] = {&p};
-  const void* kd = st->kdec_gq && gqa_applies(pos, st->gq_min, st->d.n_head, st->d.n_kv_head, st->grid)
-                       ? st->kdec_gq
-                       : st->kdec;
+  const void* kd = st->kdec[0];
+  if (st->kdec[2] && gqa_applies(pos, st->gq_min, st->d.n_head, st->d.n_kv_head, st->grid)) {
+    kd = st->kdec[2];
+  } else {
+    int nsl, sps;
+    attn_slices(pos, st->d.n_head, st->grid, st->att_spw, nsl, sps);
+    if (nsl >= DEFER_MERGE_SLICES) kd = st->kdec[1];
+  }
   const hipError_t e =
       st->coop ? hipLaunchCooperativeKernel(kd, dim3(st->grid), dim3(NT), args, 0, as_stream(stream))
                : hipLaunchKernel(kd, dim3(st->grid), dim3(NT), args, 0, as_stream(stream));
@@ -3512,7 +3528,7 @@ int fl_device_info(int32_t* num_cu, int32_t* decode_grid) {
   if (hipGetDevice(&dev) != hipSuccess) return FL_E_HIP;
   if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return FL_E_HIP;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_decode<ChunksLarge>),
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_decode<ChunksLarge, 0>),
                                                    NT, 0) != hipSuccess)
     return FL_E_HIP;
   if (num_cu) *num_cu = cu;
@@ -3547,26 +3563,21 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   const char* budget = getenv("FLINT_AMD_DECODE_BUDGET");
   const bool small = fits(ChunksSmall{}) && !(budget && strcmp(budget, "large") == 0);
   if (!small && !fits(ChunksLarge{})) return FL_E_ARG;
-  const void* kdec = small ? reinterpret_cast<const void*>(k_decode<ChunksSmall>)
-                           : reinterpret_cast<const void*>(k_decode<ChunksLarge>);
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kdec, NT, 0) != hipSuccess)
-    return FL_E_HIP;
-  if (occ < 1 || cu < 1) return FL_E_LAUNCH;
-  const void* kdec_gq = nullptr;
-  if (small) {
-    int occ_gq = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ_gq, reinterpret_cast<const void*>(k_decode<ChunksSmall, true>),
-                                                     NT, 0) != hipSuccess)
-      return FL_E_HIP;
-    if (occ_gq >= 1) kdec_gq = reinterpret_cast<const void*>(k_decode<ChunksSmall, true>);
+  const void* kdec[3] = {
+      small ? reinterpret_cast<const void*>(k_decode<ChunksSmall, 0>) : reinterpret_cast<const void*>(k_decode<ChunksLarge, 0>),
+      small ? reinterpret_cast<const void*>(k_decode<ChunksSmall, 1>) : reinterpret_cast<const void*>(k_decode<ChunksLarge, 1>),
+      small ? reinterpret_cast<const void*>(k_decode<ChunksSmall, 2>) : nullptr};
+  for (const void* k : kdec) {
+    if (!k) continue;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, NT, 0) != hipSuccess) return FL_E_HIP;
+    if (occ < 1 || cu < 1) return FL_E_LAUNCH;
   }
   fl_state* st = (fl_state*)calloc(1, sizeof(fl_state));
   if (!st) return FL_E_HIP;
   st->d = *d;
   st->max_seq = max_seq;
   st->grid = G;
-  st->kdec = kdec;
-  st->kdec_gq = kdec_gq;
+  for (int i = 0; i < 3; ++i) st->kdec[i] = kdec[i];
   st->vgrid = cu;
   st->kc = k_cache;
   st->vc = v_cache;
