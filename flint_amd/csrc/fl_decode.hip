@@ -1059,7 +1059,8 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
 // its heads' outputs; otherwise every unit publishes each head's (max, sum, o) as tagged fp32
 // words and the unit of slice s merges the heads j = s (mod nsl) over the slices (gqa_merge: in
 // a fixed order, so the result is deterministic). Units are numbered u = s * NKV + g, so a
-// group's slices run on workgroups of one XCD. Taken from p.gq_min cached keys on (4096: measured
+// group's slices run on workgroups of one XCD. The k_decode<C, 2> instantiation, which the host
+// picks from p.gq_min cached keys on (gqa_applies; 4096: measured
 // against the per-head units, -7 / 0 / -3 / -31 / -26 / -19 us per step at ctx 4096 / 5120 / 6144 /
 // 7168 / 8192 / 8320, +40 to +55 at 2048-3072), with slices of at least p.gq_kps = 128 keys (at
 // most 32 per group). Rounds of 288 keys keep one round per slice up to ctx 9216: with 256 a
