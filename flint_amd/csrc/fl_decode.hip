@@ -2111,12 +2111,9 @@ __device__ __forceinline__ void norm_rows(uint16_t* xs, int ld, int M, int D, co
 // normalised values to LDS. The same arithmetic in the same order as stage_bf16 + norm_rows, with
 // one LDS write per chunk instead of a staging write, two row reads and a write (at M = 8 the
 // separate norm took 2.1 us of a workgroup's time per phase, measured with in-kernel
-// timestamps). `issued` runs once the first pass's row loads are requested, before their data is
-// used: loads requested there (weight tiles) complete after the rows. Ends with a barrier.
-template <typename Issued>
+// timestamps). Ends with a barrier.
 __device__ __forceinline__ void stage_norm_rows(const uint16_t* src, int m0, int mh, int D, uint16_t* xs,
-                                                int ld, const uint16_t* nw, float eps, float* red,
-                                                Issued&& issued) {
+                                                int ld, const uint16_t* nw, float eps, float* red) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
   int wpr = 1;  // waves per row, as norm_rows
   while (wpr * 2 * mh <= NWAVE) wpr *= 2;
@@ -2133,7 +2130,6 @@ __device__ __forceinline__ void stage_norm_rows(const uint16_t* src, int m0, int
       const int c = sub * 64 + lane + j * step;
       v[j] = buf_ld128_coh(rs, (on && c < nch) ? (uint32_t)(m * D + c * 8) * 2u : 0xFFFFFFF0u);
     }
-    if (r0 == 0) issued();
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < LM_MAXC; ++j) {
@@ -2942,7 +2938,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
         } else {
           if (h0 == 0) wait_flags(p, vf + VF_H2, D / 16, t_prev);
           else lds_barrier();
-          stage_norm_rows(p.vh, h0, mh, D, xs, ld, nws, p.eps, part, [] {});
+          stage_norm_rows(p.vh, h0, mh, D, xs, ld, nws, p.eps, part);
         }
         if (h0 == 0) stamp(p, slot);
         for (int t = wg; t < NQKV / 16; t += G) {
@@ -3041,7 +3037,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
           tile_load(gu_q, gu_sz, (wg + i * G) * 16, i < nt ? 16 : 0, D, 0, D >> 7, tw[i]);
         if (h0 == 0) wait_flags(p, vf + VF_H1, D / 16, t_h1);
         else lds_barrier();
-        stage_norm_rows(p.vh, h0, mh, D, xs, ld, nws, p.eps, part, [] {});
+        stage_norm_rows(p.vh, h0, mh, D, xs, ld, nws, p.eps, part);
         if (h0 == 0) stamp(p, slot);
         for (int b4 = 0; b4 < nt; b4 += 4) {
           fl_f32x4 acc[4] = {};
@@ -3209,7 +3205,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
       } else {
         lds_barrier();
       }
-      stage_norm_rows(p.vh, h0, mh, D, xs, ld, nws, p.eps, part, [] {});
+      stage_norm_rows(p.vh, h0, mh, D, xs, ld, nws, p.eps, part);
       if (h0 == 0) stamp(p, slot);
       if (p.feat && wg == 0)
         for (int i = tid; i < mh * D; i += NT) p.feat[(size_t)h0 * D + i] = xs[(i / D) * ld + (i % D)];
