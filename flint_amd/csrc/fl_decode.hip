@@ -51,7 +51,7 @@ struct ChunksLarge {  // dim <= 3072, inter <= 8192 (any shape the state accepts
   static constexpr bool ROWS = false;
 };
 struct ChunksSmall {  // e.g. flint-3b on 256 CUs: 3 / 2 / 10 / 5 chunks per thread
-  static constexpr int QKV = 3, O = 2, GU = 10, D = 5, G3 = 3, NPRE_GU = 7, PR_GU = 1, PR_D = 2;
+  static constexpr int QKV = 3, O = 2, GU = 10, D = 5, G3 = 4, NPRE_GU = 8, PR_GU = 1, PR_D = 2;
   static constexpr bool ROWS = true;  // QKV and gate/up by rows
 };
 // chunks per thread dequantised while the phase's input is exchanged: QKV in registers (16 per
