@@ -1060,9 +1060,8 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
 // words and the unit of slice s merges the heads j = s (mod nsl) over the slices (gqa_merge: in
 // a fixed order, so the result is deterministic). Units are numbered u = s * NKV + g, so a
 // group's slices run on workgroups of one XCD. The k_decode<C, 2> instantiation, which the host
-// picks from p.gq_min cached keys on (gqa_applies; 4096: measured
-// against the per-head units, -7 / 0 / -3 / -31 / -26 / -19 us per step at ctx 4096 / 5120 / 6144 /
-// 7168 / 8192 / 8320, +40 to +55 at 2048-3072), with slices of at least p.gq_kps = 128 keys (at
+// picks from p.gq_min cached keys on (gqa_applies; off by default: the per-head kernels measure as
+// fast or faster up to 16 K keys on flint-3b), with slices of at least p.gq_kps = 128 keys (at
 // most 32 per group). Rounds of 288 keys keep one round per slice up to ctx 9216: with 256 a
 // context just past 8192 took a second, nearly empty round (+52 us at 8320; 288 costs ~4 us below).
 constexpr int GQ_VRK = 288;                      // keys per LDS round (32 slices x 288 keys: one round up to ctx 9216)
@@ -3588,7 +3587,7 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
     st->since_clear = 0;
   }
   st->att_spw = 8;
-  st->gq_min = 4096;
+  st->gq_min = 1 << 30;  // the attention by KV group only on request (FLINT_AMD_GQA_MIN)
   st->gq_kps = 128;
   st->vkps = 128;
   st->vtok_work = 5120;

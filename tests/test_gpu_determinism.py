@@ -27,7 +27,12 @@ def model(dev):
     from flint_amd.model import Transformer
     args = ModelArgs.from_name("flint-3b")
     eng = Transformer.from_weights(args, synth_weights(args, 0, device="cuda"), "cuda")
+    # the attention by KV group (off by default) from 4096 cached keys, so that the decode cases
+    # cover all three attentions
+    mp = pytest.MonkeyPatch()
+    mp.setenv("FLINT_AMD_GQA_MIN", "4096")
     eng.setup_caches(1, 4200)
+    mp.undo()
     g = torch.Generator(device="cuda").manual_seed(11)
     eng.k_cache.normal_(generator=g)
     eng.v_cache.normal_(generator=g)
@@ -40,7 +45,7 @@ def _same(runs):
     return [i for i, r in enumerate(runs[1:], 1) if not torch.equal(r, ref)]
 
 
-@pytest.mark.parametrize("pos", [600, 1500, 4000, 4150])  # 2, 3, 6 slices per head; by KV group
+@pytest.mark.parametrize("pos", [600, 1500, 4000, 4150])  # 2, 3, 6 slices per head (merge deferred from 4); by KV group
 def test_decode_repeats_bitwise(model, pos):
     args, eng = model
     tok = torch.tensor([1234], dtype=torch.int32, device="cuda")
