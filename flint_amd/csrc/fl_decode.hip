@@ -2989,13 +2989,13 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
       for (int h0 = 0; h0 < M; h0 += VH) {
         const int mh = min(VH, M - h0);
         TileW tw;
+        tile_load(o_q, o_sz, wg * 16, 16, D, 0, D >> 7, tw);  // before the wait, as every phase's tiles
         if (h0 == 0) {
           wait_flags(p, vf + VF_ATTN, verify_attn_flags<AM>(p), t_attn);
         } else {
           lds_barrier();
         }
         stage_bf16(p.vattn, D, h0, mh, 0, D, xs, ld);
-        tile_load(o_q, o_sz, wg * 16, 16, D, 0, D >> 7, tw);  // after the rows, as in P5
         lds_barrier();
         if (h0 == 0) stamp(p, slot);
         fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
