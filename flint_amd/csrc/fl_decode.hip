@@ -2171,8 +2171,8 @@ __device__ __forceinline__ void stage_norm_rows(const uint16_t* src, int m0, int
 // (ng <= NWAVE * TW_G): this wave's groups g0 + wave + 8i, one 16-byte quarter-group per lane. Loading
 // does not depend on the token rows, so QKV and gate/up request tiles before they wait for their
 // inputs, and every phase requests the next tile before it computes the current one. Loads
-// complete in order: rows staged after a tile's request arrive only after that tile, so O and the
-// down projection (whose wait is short) request theirs once the rows are in.
+// complete in order: rows staged after a tile's request arrive only after that tile (measured
+// faster all the same in every phase: the tiles arrive during the wait).
 constexpr int TW_G = 3;  // K groups per wave of a tile: D <= 3072 is at most 24 groups, 3 per wave
 static_assert(TW_G * NWAVE * 128 >= 64 * 8 * LM_MAXC, "a tile's K groups fit TW_G per wave at the largest D");
 struct TileW {
