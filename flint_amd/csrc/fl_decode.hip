@@ -1903,8 +1903,9 @@ __host__ __device__ inline size_t verify_xs_bytes(int D) {
   return xs > (size_t)VA_BYTES ? xs : (size_t)VA_BYTES;
 }
 __host__ __device__ inline size_t verify_nw_bytes(int D) { return ((size_t)D * 4 + 15) & ~(size_t)15; }
+constexpr int VPART_TILES = 5;  // tiles whose wave partials the LDS holds at once (down projection rounds)
 inline size_t verify_lds_bytes(int D) {
-  return verify_xs_bytes(D) + verify_nw_bytes(D) + 4 * NWAVE * 256 * 4 + FL_MAX_VERIFY * 16 * 2;
+  return verify_xs_bytes(D) + verify_nw_bytes(D) + VPART_TILES * NWAVE * 256 * 4 + FL_MAX_VERIFY * 16 * 2;
 }
 
 // A norm weight vector (bf16 [D], D % 8 == 0) into LDS as two copies of its bf16 pairs, one with
@@ -2274,11 +2275,12 @@ __device__ __forceinline__ void stage_frag(const uint16_t* src, int stride, int 
 }
 
 // four tiles' partials at once: tile i's go to part + i * NWAVE * 256; ends with a barrier
-__device__ __forceinline__ void tile_publish4(float* part, const fl_f32x4 (&acc)[4]) {
+template <int N>
+__device__ __forceinline__ void tile_publish4(float* part, const fl_f32x4 (&acc)[N]) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
   const int r = lane & 15, c = lane >> 4;
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < N; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) part[(t * NWAVE + wave) * 256 + (c * 4 + i) * 16 + r] = acc[t][i];
   lds_barrier();
@@ -2877,7 +2879,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
   uint16_t* xs = reinterpret_cast<uint16_t*>(vsm);  // also the attention unit's region
   uint16_t* nws = reinterpret_cast<uint16_t*>(vsm + verify_xs_bytes(D));  // RMSNorm weights [D]
   float* part = reinterpret_cast<float*>(vsm + verify_xs_bytes(D) + verify_nw_bytes(D));
-  uint16_t* hres = reinterpret_cast<uint16_t*>(part + 4 * NWAVE * 256);  // [FL_MAX_VERIFY][16]
+  uint16_t* hres = reinterpret_cast<uint16_t*>(part + VPART_TILES * NWAVE * 256);  // [FL_MAX_VERIFY][16]
   for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + VH * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
   int slot = 0;  // optional timestamps, same slots as k_decode's
   stamp(p, slot);
@@ -3084,7 +3086,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
       const int k = wg % KP, kg0 = k * GPP, kgn = min(GPP, ng - kg0);
       const int nmine = (wg < GK * KP) ? max(0, (ntile - wg / KP + GK - 1) / GK) : 0;
       unsigned long long* const dpart = p.part;  // [tile][part][FL_MAX_VERIFY][16]
-      constexpr int TMAX = 8;  // tiles per workgroup whose weights are requested together
+      constexpr int R = VPART_TILES, TMAX = 2 * R;  // tiles per round; tiles requested together
       for (int h0 = 0; h0 < M; h0 += VH) {
         const int mh = min(VH, M - h0);
         TileW1 tw[TMAX] = {};
@@ -3100,21 +3102,21 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
           stage_frag(p.vact, F, h0, mh, kg0 * 128, kgn, xs, ld);
           if (h0 == 0) stamp(p, p5slot);
         }
-        for (int j0 = 0; j0 < nmine; j0 += 4) {
+        for (int j0 = 0; j0 < nmine; j0 += R) {
           if (j0 >= TMAX) {  // more tiles than prefetched (few workgroups): one round at a time
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < R; ++i)
               if (j0 + i < nmine) tile_load1(d_q, d_sz, (wg / KP + (j0 + i) * GK) * 16, F, kg0, kgn, tw[i]);
           }
-          fl_f32x4 acc[4] = {};
+          fl_f32x4 acc[R] = {};
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < R; ++i)
             if (j0 + i < nmine) {
-              const TileW1& w = j0 >= TMAX ? tw[i] : (j0 == 0 ? tw[i] : tw[4 + i]);
+              const TileW1& w = j0 >= TMAX ? tw[i] : (j0 == 0 ? tw[i] : tw[R + i]);
               tile_mma1(w, kgn, xs, ld, mh, acc[i]);
             }
           tile_publish4(part, acc);
-          for (int it = tid; it < 4 * 256; it += NT) {
+          for (int it = tid; it < R * 256; it += NT) {
             const int i = it >> 8, ml = (it >> 4) & 15, n = it & 15;
             if (j0 + i < nmine && ml < mh) {
               const int t = wg / KP + (j0 + i) * GK;
