@@ -3134,12 +3134,33 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
         if (tid < 16 * M) {
           const int m = tid >> 4, n = tid & 15;
           auto ok = [t_h2](unsigned long long v) { return (uint32_t)(v >> 32) == t_h2; };
+          const unsigned long long* const a0 = dpart + ((size_t)wg * KP * FL_MAX_VERIFY + m) * 16 + n;
+          constexpr size_t KS = (size_t)FL_MAX_VERIFY * 16;  // one part's stride
           float sum = 0.0f;
-          for (int kk = 0; kk < KP; ++kk) {
-            const unsigned long long* a = dpart + (((size_t)wg * KP + kk) * FL_MAX_VERIFY + m) * 16 + n;
-            unsigned long long v = ld_coh_u64(a);
-            if (!ok(v)) v = spin_until(p, v, ok, [a]() { return ld_coh_u64(a); });
-            sum += __uint_as_float((uint32_t)v);
+          bool in = false;
+          if (KP <= 8 && M <= VH) {
+            // one token pass: all parts requested at once; if one is not in yet, the parts are
+            // read again below one at a time, each waited for (with several passes the parts
+            // arrive spread out and the batch seldom finds them all: measured slower there)
+            unsigned long long v8[8];
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) v8[kk] = kk < KP ? ld_coh_u64(a0 + kk * KS) : 0ull;
+            in = true;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) in = in && (kk >= KP || ok(v8[kk]));
+            if (__builtin_expect(in, 1)) {
+#pragma unroll
+              for (int kk = 0; kk < 8; ++kk)
+                if (kk < KP) sum += __uint_as_float((uint32_t)v8[kk]);
+            }
+          }
+          if (!in) {
+            for (int kk = 0; kk < KP; ++kk) {
+              const unsigned long long* a = a0 + kk * KS;
+              unsigned long long v = ld_coh_u64(a);
+              if (!ok(v)) v = spin_until(p, v, ok, [a]() { return ld_coh_u64(a); });
+              sum += __uint_as_float((uint32_t)v);
+            }
           }
           const float o = rbf(rbf(sum) * p.resid_mult);  // engine/model.py:163
           const uint32_t h2 = f2bf(bf2f(hres[m * 16 + n]) + o);
