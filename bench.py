@@ -118,18 +118,73 @@ def verify_latency(model, args, dev, ctx=1024, reps=20):
     out = torch.empty(1, dtype=torch.int32, device=dev)
     dec_us = timed(lambda: model.decode_step(tok[:1], ctx, token_out=out))
     res = {}
-    for m in (5, 8):
+    gt = torch.Generator().manual_seed(7)
+    parent = [-1] + [int(torch.randint(0, i, (1,), generator=gt)) for i in range(1, 8)]
+    tdepth, tmask = tree_mask(parent)
+    shapes = [("5", 5, None, None), ("8", 8, None, None),
+              ("tree8", 8, tdepth.to(dev), tmask.to(dev))]
+    for name, m, depth, amask in shapes:
         logits = torch.empty(m, args.vocab_size, dtype=torch.float32, device=dev)
         feat = torch.empty(m, args.dim, dtype=torch.bfloat16, device=dev)
         touts = torch.empty(m, dtype=torch.int32, device=dev)
-        depth = torch.arange(m, dtype=torch.int32, device=dev)
-        amask = torch.tril(torch.ones(m, m, dtype=torch.uint8, device=dev))
-        res[str(m)] = round(timed(lambda: model.verify(tok[:m], ctx, depth=depth, amask=amask,
-                                                       logits=logits, feat=feat,
-                                                       tokens_out=touts)), 1)
+        if depth is None:
+            depth = torch.arange(m, dtype=torch.int32, device=dev)
+            amask = torch.tril(torch.ones(m, m, dtype=torch.uint8, device=dev))
+        res[name] = round(timed(lambda: model.verify(tok[:m], ctx, depth=depth, amask=amask,
+                                                     logits=logits, feat=feat,
+                                                     tokens_out=touts)), 1)
     model.check()
     return {"ctx": ctx, "decode_us": round(dec_us, 1), "verify_us": res,
+            "tree8_parents": parent,
             "cost_vs_decode": {k: round(v / dec_us, 3) for k, v in res.items()}}
+
+
+def tree_mask(parent):
+    """depth and ancestor-or-self mask of a draft tree given by parent indices (parent[0] = -1),
+    as reference spec_tree.py:101-104 builds them."""
+    m = len(parent)
+    depth = torch.zeros(m, dtype=torch.int32)
+    amask = torch.zeros(m, m, dtype=torch.uint8)
+    for i in range(m):
+        j = i
+        while j >= 0:
+            amask[i, j] = 1
+            j = parent[j]
+        depth[i] = int(amask[i].sum()) - 1
+    return depth, amask
+
+
+def handoff_probe(dev, words=2560, rounds=2000):
+    """Latency of one inter-workgroup hand-off of a `words`-word tagged vector (10 KB at D = 2560
+    32-bit words, an activation vector of the decode kernel), from fl_probe_handoff: one
+    workgroup per CU, `rounds` chained all-to-all hand-offs; median over the workgroups of their
+    time per round. Modes: across all workgroups (every XCD) over the decode kernel's uncached
+    exchange memory; within each XCD's 32 workgroups over the same memory; within each XCD over
+    ordinary device memory (L2-local coherent loads). Also reports whether every workgroup ran on
+    XCD blockIdx % 8 (the mapping the XCD-local modes assume)."""
+    from flint_amd import _lib
+    import ctypes
+    res = {"words": words, "rounds": rounds}
+    grid = ctypes.c_int32()
+    for mode, name in ((0, "all_uncached_us"), (1, "xcd_uncached_us"), (2, "xcd_l2_us")):
+        out = torch.zeros(2 * 1024, dtype=torch.int64, device=dev)
+        for _ in range(2):      # the first call allocates and warms up
+            _lib.call("fl_probe_handoff", mode, words, rounds, _lib.ptr(out), ctypes.byref(grid),
+                      _lib.stream_ptr())
+            torch.cuda.synchronize()
+        o = out[:2 * grid.value].view(-1, 2).cpu()
+        ticks = o[:, 0].double()
+        info = o[:, 1]
+        timeouts = int(((info >> 32) & 1).sum())
+        # 100 MHz ticks: 0.01 us each
+        res[name] = round(float(ticks.median()) * 0.01 / rounds, 3) if timeouts == 0 else None
+        res[name.replace("_us", "_max_us")] = round(float(ticks.max()) * 0.01 / rounds, 3)
+        if timeouts:
+            res[name.replace("_us", "_timeouts")] = timeouts
+        if mode == 0:
+            xcc = (info & 0xF).tolist()
+            res["xcd_is_blockidx_mod_8"] = all(x == i % 8 for i, x in enumerate(xcc))
+    return res
 
 
 class KnownDraft:
@@ -353,6 +408,11 @@ def main():
                     help="skip the speculative-loop timing (chain / tree with a known draft)")
     ap.add_argument("--no-sampling", action="store_true",
                     help="skip the sampler timings (standalone and fused into the decode launch)")
+    ap.add_argument("--no-handoff", action="store_true",
+                    help="skip the hand-off micro-benchmark (fl_probe_handoff)")
+    ap.add_argument("--maps", default=None,
+                    help="write the process's memory map (/proc/self/maps) to this file at the end, "
+                         "to attribute the frames of a crash during interpreter exit")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="after timing, run one device-to-device copy of this many MiB (the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -456,6 +516,11 @@ def main():
         sampling.update(fused_sampling(model, args, dev, a.ctx))
         log(f"sampling over {args.vocab_size} logits: {sampling}")
 
+    handoff = None
+    if not a.no_handoff:
+        handoff = handoff_probe(dev)
+        log(f"hand-off of a {handoff['words']}-word tagged vector: {handoff}")
+
     if a.copy_probe_mb > 0:
         n = a.copy_probe_mb * (1 << 20)
         src = torch.ones(n, dtype=torch.uint8, device=dev)
@@ -500,11 +565,16 @@ def main():
         "long_context": long,
         "gemv_sweep": gemv,
         "sampling": sampling,
+        "handoff": handoff,
     }
     print(json.dumps(out), flush=True)
     # release the decode state (and its device memory) before interpreter shutdown
     torch.cuda.synchronize()
     model.close()
+    if a.maps:
+        os.makedirs(os.path.dirname(os.path.abspath(a.maps)), exist_ok=True)
+        with open("/proc/self/maps") as src, open(a.maps, "w") as dst:
+            dst.write(src.read())
 
 
 if __name__ == "__main__":

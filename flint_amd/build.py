@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libflint_amd.so")
 OBJDIR = os.path.join(HERE, "_build")
-SOURCES = ["fl_quant.hip", "fl_decode.hip", "fl_sample.hip"]
+SOURCES = ["fl_quant.hip", "fl_decode.hip", "fl_sample.hip", "fl_probe.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -45,7 +45,43 @@ def build(verbose=False):
     os.replace(tmp, OUT)
     if verbose:
         print(f"built {OUT}")
+    ext = build_torch_ext()
+    if verbose:
+        print(f"built {ext}")
     return OUT
+
+
+TORCH_EXT = "_torch_ops"
+
+
+def torch_ext_path():
+    import sysconfig
+    return os.path.join(HERE, TORCH_EXT + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_torch_ext():
+    """The torch-extension binding (csrc/fl_torch.cpp: pybind11 ops over torch tensors) as
+    flint_amd/_torch_ops*.so, linked against libflint_amd.so beside it. A host-only C++ file:
+    it calls the C ABI and needs torch's headers, not HIP's."""
+    import sysconfig
+    import torch
+    from torch.utils import cpp_extension
+    out = torch_ext_path()
+    incs = cpp_extension.include_paths() + [sysconfig.get_paths()["include"]]
+    libs = cpp_extension.library_paths()
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
+           os.path.join(CSRC, "fl_torch.cpp"), "-o", out + ".tmp",
+           f"-DTORCH_EXTENSION_NAME={TORCH_EXT}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-Wno-deprecated-declarations",
+           *[f"-I{i}" for i in incs], *[f"-L{l}" for l in libs], f"-L{HERE}",
+           "-lflint_amd", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+           "-Wl,-rpath,$ORIGIN", *[f"-Wl,-rpath,{l}" for l in libs]]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"torch extension build failed:\n{r.stderr[-4000:]}")
+    os.replace(out + ".tmp", out)
+    return out
 
 
 if __name__ == "__main__":

@@ -81,6 +81,15 @@ def load_hf_safetensors(path, args: ModelArgs, device="cpu"):
     return state_dict_from_hf(hf, args)
 
 
+def hf_to_interleaved_perm(n_heads, head_dim):
+    """Row permutation from HF (NEOX half-split) order to gpt-fast's interleaved order: row
+    (h, t, i) of a head (t in {0, 1}, i < head_dim / 2) goes to (h, i, t), as gpt-fast's
+    convert_hf_checkpoint.py:75-81 permute does; w_interleaved = w_hf[perm]."""
+    i = torch.arange(head_dim // 2)
+    within = torch.stack([i, i + head_dim // 2], dim=1).reshape(-1)
+    return (torch.arange(n_heads).unsqueeze(1) * head_dim + within.unsqueeze(0)).reshape(-1)
+
+
 def interleaved_to_hf(w, n_head, head_dim):
     """Undo gpt-fast's permute (convert_hf_checkpoint.py:75-81), which takes HF rows (h, t, i) to
     (h, i, t) for t in {0, 1}, i < head_dim / 2."""

@@ -1931,14 +1931,15 @@ constexpr int VF_H1 = 0, VF_H2 = 256, VF_ATTN = 512, VF_ACT = VF_ATTN + 256;
 constexpr int VF_WORDS = VF_ACT + 2048;
 
 // Key slices of verify attention per query head: nsl units, one per p.vkps cached keys (default 128)
-// but at most VNS
-// and G / NH (so all units of a launch fit the grid, one each), unit s covering the cached keys
-// [s kps, min(pos, (s+1) kps)) (kps a multiple of 16); the last unit also takes the new keys.
-// With pos <= p.vkps there is one unit per head and no merge.
+// but at most VNS, G / NH (so all units of a launch fit the grid, one each) and
+// (VF_ACT - VF_ATTN) / NH (each unit's ready flag VF_ATTN + head * nsl + s stays inside the
+// attention flag region on any grid; the host accepts NH <= VF_ACT - VF_ATTN), unit s covering the
+// cached keys [s kps, min(pos, (s+1) kps)) (kps a multiple of 16); the last unit also takes the
+// new keys. With pos <= p.vkps there is one unit per head and no merge.
 constexpr int VNS = 16;
 __device__ __forceinline__ void verify_slices(const DecodeParams& p, int pos, int NH, int G, int& nsl, int& kps) {
   const int ch = (pos + 15) >> 4;
-  const int cap = max(1, min(VNS, G / NH));
+  const int cap = max(1, min(min(VNS, G / NH), (VF_ACT - VF_ATTN) / NH));
   nsl = max(1, min(cap, (pos + p.vkps - 1) / p.vkps));  // a slice per vkps keys, while units last
   kps = ((ch + nsl - 1) / nsl) * 16;
   nsl = kps ? max(1, (pos + kps - 1) / kps) : 1;
@@ -3393,8 +3394,10 @@ int dev_alloc(fl_state* st, T** p, size_t count) {
 }
 
 // The tagged exchange buffers (activations handed between workgroups inside a launch) live in
-// uncached device memory: every access goes to the memory side directly instead of through the
-// per-XCD L2s, which makes an all-to-all hand-off about 20% faster. Uncached memory is never freed
+// uncached device memory (hipDeviceMallocUncached). On gfx950 its lines are still held in the
+// L2s, coherently (the exchange reads count as L2 hits, not as uncached requests or HBM reads);
+// what it buys is that the device-coherent (sc1) stores and loads of the hand-offs need no L2
+// write-back or invalidate, and it measured about 2% faster end to end than ordinary memory. Uncached memory is never freed
 // once a kernel has read it (memory allocated after such a free has been seen to hold wrong
 // values), so a destroyed state returns its blocks to this per-process pool, and later states on
 // the same device reuse them, cleared (a stale tag must never match a new phase).

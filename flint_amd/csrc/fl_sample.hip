@@ -1,7 +1,8 @@
 // Temperature / top-k sampling of logit rows on the GPU (reference engine/generate.py:36-55).
 //
-// Each row is split over SP_C chunks, one workgroup each, in one cooperative launch; grid-wide
-// syncs separate the steps that need the whole row. The reference's steps with its bf16 rounding
+// Each row is split over up to SP_C chunks, one workgroup each, in one plain launch; per-row
+// barriers (an arrival counter in the row's scratch, bounded waits) separate the steps that need
+// the whole row. The reference's steps with its bf16 rounding
 // points: x = bf16(l / max(T, 1e-5)); the top-k pivot is the k-th largest x, found by a two-pass
 // radix select over the 16-bit ordered keys of the bf16 values (each chunk's 256-bin histogram
 // of the high byte, summed over the row in a fixed order, then the low byte within the selected
@@ -10,9 +11,9 @@
 // given; the sample is the first index of the largest bf16(p / q), which is
 // multinomial_sample_one_no_sync's argmax(probs / exponential noise): 64-bit atomicMax of
 // (ratio, ~index) per row, read out by the row's last chunk to finish.
-#include <hip/hip_cooperative_groups.h>
 #include <algorithm>
 #include <mutex>
+#include <stdlib.h>
 #include "fl_common.h"
 
 namespace {
@@ -30,9 +31,13 @@ struct SampleWs {
   float mx[SP_C], ps[SP_C];                    // per chunk: max x, partial sum of exp(x - max)
   unsigned long long best;                     // (ratio bits, ~index), atomicMax
   unsigned int arrived;                        // chunks done (the last one reads best out)
+  unsigned int bar;                            // barrier arrivals of this launch (reset by the last chunk)
+  unsigned int fail;                           // a chunk's barrier wait timed out (reset by the last chunk)
 };
 
-// scratch words written before a grid sync and read after it by other workgroups (possibly on
+constexpr unsigned long long SAMPLE_WAIT_TICKS = 200000000ull;  // 2 s of the 100 MHz realtime clock
+
+// scratch words written before a row barrier and read after it by other workgroups (possibly on
 // other XCDs): device-coherent accesses
 __device__ __forceinline__ void st_ws(unsigned* a, unsigned v) {
   __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -40,6 +45,29 @@ __device__ __forceinline__ void st_ws(unsigned* a, unsigned v) {
 __device__ __forceinline__ void st_ws(float* a, unsigned v) { st_ws(reinterpret_cast<unsigned*>(a), v); }
 __device__ __forceinline__ unsigned ld_ws(unsigned* a) {
   return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Barrier of the C chunk workgroups of one row: every thread's scratch stores are acknowledged
+// (s_waitcnt 0) before the workgroup's arrival is counted, and the workgroup leaves once the
+// row's count reaches `target` (C per barrier so far). The launch is a plain one: its grid (at
+// most 16 rows x 64 chunks of 256 threads) is checked on the host to fit the device at once, so
+// every chunk is resident on an idle device; should one not be (other work holding its CU), the
+// wait gives up after 2 s and the row's token is reported as -1 instead of hanging.
+__device__ __forceinline__ void row_sync(SampleWs* ws, unsigned target, bool* timed_out) {
+  wait_mem();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(&ws->bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (ld_ws(&ws->bar) < target) {
+      __builtin_amdgcn_s_sleep(2);
+      if (__builtin_amdgcn_s_memrealtime() - t0 > SAMPLE_WAIT_TICKS) {
+        *timed_out = true;
+        break;
+      }
+    }
+  }
+  __syncthreads();
 }
 
 __device__ __forceinline__ float wg_max(float v, float* red) {
@@ -85,19 +113,19 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float* __restrict__ logi
                                                   const float* __restrict__ noise,
                                                   int32_t* __restrict__ tokens_out,
                                                   float* __restrict__ probs_out, SampleWs* __restrict__ wsa) {
-  namespace cg = cooperative_groups;
-  cg::grid_group grid = cg::this_grid();
   __shared__ int hist[256];
   __shared__ int sel[2];
   __shared__ float red[SP_NWAVE];
   __shared__ unsigned long long ured[SP_NWAVE];
-  __shared__ bool last;
+  __shared__ bool last, timed_out;
   const int tid = threadIdx.x, row = blockIdx.x / C, c = blockIdx.x % C;
   const int CH = (V + C - 1) / C, j0 = c * CH, j1 = min(V, j0 + CH);
   SampleWs* ws = wsa + row;
-  // the row's argmax word and arrival count start at zero: cleared here, before the first grid
-  // sync, which orders it before every chunk's use after the last one (so a scratch block that
-  // another call left in any state is valid input)
+  unsigned nsync = 0;  // row barriers passed
+  if (tid == 0) timed_out = false;
+  // the row's argmax word and arrival count start at zero: cleared here, before the first row
+  // barrier, which orders it before every chunk's use after the last one. The barrier counter
+  // itself is zero at launch: the last chunk of the previous call on this scratch reset it.
   if (c == 0 && tid == 0) {
     __hip_atomic_store(&ws->best, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&ws->arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -131,7 +159,7 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float* __restrict__ logi
       }
       __syncthreads();
       st_ws(reinterpret_cast<unsigned*>(&ws->hist[c][pass][tid]), (unsigned)hist[tid]);
-      grid.sync();
+      row_sync(ws, (unsigned)C * ++nsync, &timed_out);
       // the row's counts: thread t sums bins 4(t % 64) .. +3 over chunks t / 64, t / 64 + 4, ...
       // (16-byte coherent loads, all issued before any is used), then the 4 partial sums meet in LDS
       const auto hr = buf_rsrc(&ws->hist[0][0][0], (uint32_t)sizeof(ws->hist));
@@ -164,7 +192,7 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float* __restrict__ logi
       __syncthreads();
     }
   } else {
-    grid.sync();
+    row_sync(ws, (unsigned)C * ++nsync, &timed_out);
   }
   // the row's max (kept entries include it), then the partial sum of exp(x - max) over kept x
   // chunk cc's value is loaded by thread cc (one round trip), then reduced over the workgroup
@@ -179,7 +207,7 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float* __restrict__ logi
   }
   s = wg_sum(s, red);
   if (tid == 0) st_ws(reinterpret_cast<unsigned*>(&ws->ps[c]), __float_as_uint(s));
-  grid.sync();
+  row_sync(ws, (unsigned)C * ++nsync, &timed_out);
   s = tid < C ? __uint_as_float(ld_ws(reinterpret_cast<unsigned*>(&ws->ps[tid]))) : 0.0f;
   s = wg_sum(s, red);  // a fixed reduction tree: the same sum in every chunk
   // p = bf16(exp(x - max) / sum); argmax(bf16(p / q)), the first index among equal ratios
@@ -209,14 +237,19 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float* __restrict__ logi
   best = wg_umax(best, ured);
   if (tid == 0) {
     if (best) __hip_atomic_fetch_max(&ws->best, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (timed_out) __hip_atomic_store(&ws->fail, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const unsigned prev = __hip_atomic_fetch_add(&ws->arrived, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     last = prev == (unsigned)(C - 1);
   }
   __syncthreads();
-  if (last && tid == 0) {  // every chunk's atomicMax precedes its arrival: read out, reset for the next call
+  // every chunk's atomicMax and failure mark precede its arrival, and every chunk has left its
+  // last barrier: the last one reads the row out and resets the scratch for the next call
+  if (last && tid == 0) {
     const unsigned long long b =
         __hip_atomic_exchange(&ws->best, 0ull, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-    tokens_out[row] = (int32_t)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull));
+    const bool failed = __hip_atomic_exchange(&ws->fail, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    tokens_out[row] = failed ? -1 : (int32_t)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull));
+    __hip_atomic_store(&ws->bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&ws->arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -225,8 +258,7 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float* __restrict__ logi
 
 namespace {
 
-// Rows per cooperative launch, and rows of each scratch block: 16 rows of up to SP_C chunks fill
-// the chip's 256 CUs once.
+// Rows per launch, and rows of each scratch block: 16 rows of up to SP_C chunks.
 constexpr int SAMPLE_ROWS = 16;
 
 // Scratch of fl_sample_noalloc: a fixed block per device for SAMPLE_ROWS rows (2.1 MB), part of
@@ -237,6 +269,27 @@ static __device__ __align__(256) SampleWs scratch[SAMPLE_ROWS];
 std::mutex g_scratch_mu;
 SampleWs* g_scratch_ptr[64] = {};
 
+// Workgroups of k_sample the device holds at once (occupancy x CUs), per device, looked up on the
+// first call: a launch's grid must fit, since its row barriers wait for every chunk of a row.
+std::mutex g_fit_mu;
+int g_fit[64] = {};
+int sample_capacity(int dev) {
+  std::lock_guard<std::mutex> lk(g_fit_mu);
+  if (!g_fit[dev]) {
+    int cu = 0, occ = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_sample), SP_NT, 0) !=
+            hipSuccess)
+      return 0;
+    g_fit[dev] = cu * occ;
+  }
+  return g_fit[dev];
+}
+bool sample_coop() {
+  const char* e = getenv("FLINT_AMD_COOPERATIVE");
+  return e && atoi(e) != 0;
+}
+
 int sample_launch(const float* logits, int32_t rows, int32_t vocab, float temperature, int32_t top_k,
                   uint64_t seed, uint64_t offset, const float* noise, int32_t* tokens_out,
                   float* probs_out, SampleWs* wsp, void* stream) {
@@ -246,6 +299,10 @@ int sample_launch(const float* logits, int32_t rows, int32_t vocab, float temper
   int v = vocab, ci = C, tk = top_k;
   uint32_t slo = (uint32_t)seed, shi = (uint32_t)(seed >> 32), olo = (uint32_t)offset, ohi = (uint32_t)(offset >> 32);
   float td = tdiv;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FL_E_HIP;
+  const int cap = sample_capacity(dev);
+  const bool coop = sample_coop();
   for (int r0 = 0; r0 < rows; r0 += SAMPLE_ROWS) {  // SAMPLE_ROWS rows per launch (the scratch's rows)
     const int n = std::min(SAMPLE_ROWS, rows - r0);
     const float* lg = logits + (size_t)r0 * vocab;
@@ -254,8 +311,12 @@ int sample_launch(const float* logits, int32_t rows, int32_t vocab, float temper
     float* po = probs_out ? probs_out + (size_t)r0 * vocab : nullptr;
     int rb = r0;
     void* args[] = {(void*)&lg, &v, &ci, &rb, &td, &tk, &slo, &shi, &olo, &ohi, (void*)&nz, &to, &po, &wsp};
-    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_sample), dim3(n * C),
-                                                    dim3(SP_NT), args, 0, reinterpret_cast<hipStream_t>(stream));
+    if (n * C > cap) return FL_E_LAUNCH;  // the row barriers need every chunk resident at once
+    // a plain launch (FLINT_AMD_COOPERATIVE=1: a cooperative one, which also guarantees residency)
+    const hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+    const hipError_t e =
+        coop ? hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_sample), dim3(n * C), dim3(SP_NT), args, 0, hs)
+             : hipLaunchKernel(reinterpret_cast<const void*>(k_sample), dim3(n * C), dim3(SP_NT), args, 0, hs);
     if (e != hipSuccess) return FL_E_LAUNCH;
   }
   return FL_OK;

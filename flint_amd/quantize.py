@@ -61,7 +61,7 @@ def gemv_int4(q, sz, x, y=None):
 
 
 def gemm_int4(q, sz, x, y=None):
-    """Y[M,N] = bf16(X[M,K] . dq[N,K]^T), M <= 16, weights read once for all M rows."""
+    """Y[M,N] = bf16(X[M,K] . dq[N,K]^T), M <= 32, weights read once for all M rows."""
     _check_dev(q, torch.int32, "q")
     _check_dev(sz, torch.int32, "sz")
     _check_dev(x, torch.bfloat16, "x")
@@ -113,8 +113,8 @@ def scales_and_zeros_gptfast(sz):
 class WeightOnlyInt4Linear(torch.nn.Module):
     """Drop-in for reference engine/quantize.py:483-525 (groupsize 128), on the HIP GEMVs.
 
-    forward(x [..., K] bf16) -> [..., N] bf16; M = prod(leading dims) <= 16 rows per call
-    (one weight read for all rows), as in decode and speculative verify.
+    forward(x [..., K] bf16) -> [..., N] bf16; M = prod(leading dims) <= 32 rows per call
+    (one weight read for all rows), as in decode and speculative verify; more rows raise.
     """
 
     def __init__(self, in_features, out_features, bias=False, device=None, groupsize=GROUP):

@@ -132,7 +132,10 @@ int fl_state_force_timeout(fl_state* st, int32_t on);
 /* Last error recorded by a kernel (FL_OK or FL_E_TIMEOUT); synchronises the stream. */
 int fl_state_check(fl_state* st, void* stream);
 
-/* One full decode step in ONE persistent cooperative launch: embedding of *token_in at
+/* One full decode step in ONE persistent launch (one workgroup per CU, every workgroup resident
+ * at once on an idle device; a plain launch by default, hipLaunchCooperativeKernel when the
+ * environment sets FLINT_AMD_COOPERATIVE=1 at fl_state_create; every inter-workgroup wait is
+ * bounded either way, see fl_state_set_wait_limit): embedding of *token_in at
  * position pos, all layers, final norm, LM head, greedy argmax (first index on ties over the
  * bf16-rounded logits) written to *token_out. logits (fp32 [V], bf16-exact values) and
  * feat (bf16 [D], post-final-norm hidden) are optional (NULL to skip).
@@ -188,9 +191,12 @@ int fl_kv_move(fl_state* st, const int32_t* src, const int32_t* dst, int32_t n, 
  * largest is dropped (ties with it stay); p = bf16(softmax(x)); the token is the first index of
  * the largest bf16(p / q). q is noise[rows, vocab] when given, else bf16(-log u) with u from
  * Philox4x32-10, key = seed, counter = (index, row, offset low, offset high). probs_out
- * [rows, vocab] (optional) receives p. top_k = 0 means no top-k. Up to 16 rows per
- * cooperative launch (more rows: several launches); the library keeps one scratch block per device
- * (allocated on the first call), so calls on one device must be stream-ordered.
+ * [rows, vocab] (optional) receives p. top_k = 0 means no top-k. Up to 16 rows per launch
+ * (more rows: several launches), each row split over up to 64 workgroups that meet at per-row
+ * barriers (a plain launch whose grid is checked to fit the device at once: FL_E_LAUNCH if not;
+ * cooperative with FLINT_AMD_COOPERATIVE=1); a row whose barrier wait timed out (2 s: a chunk
+ * was not resident) gets token -1. The library keeps one scratch block per device (allocated on
+ * the first call), so calls on one device must be stream-ordered.
  * Replaces reference engine/generate.py:36-55 (multinomial_sample_one_no_sync, logits_to_probs,
  * sample). */
 int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperature, int32_t top_k,
@@ -208,6 +214,21 @@ int fl_sample(const float* logits, int32_t rows, int32_t vocab, float temperatur
 int fl_sample_noalloc(const float* logits, int32_t rows, int32_t vocab, float temperature,
                       int32_t top_k, uint64_t seed, uint64_t offset, const float* noise,
                       int32_t* tokens_out, float* probs_out, void* stream);
+
+/* ---- diagnostics ------------------------------------------------------------------------ */
+
+/* Hand-off micro-benchmark, no counterpart in the reference (which times its grid barrier in
+ * isolation, result.md:38-40): one launch of one 512-thread workgroup per CU hands a tagged
+ * vector of `words` 32-bit words (4..8192) from every producer workgroup to every consumer
+ * workgroup `rounds` times in a chain, the way the decode / verify kernels hand activations
+ * between phases. mode 0: all workgroups, over the uncached exchange memory the kernels use;
+ * mode 1: the workgroups of each XCD separately (blockIdx % 8), same memory; mode 2: the
+ * workgroups of each XCD over ordinary device memory (coherent loads served by that XCD's L2).
+ * out (device, uint64 [2 * grid]): per workgroup the 100 MHz-clock ticks of all rounds, then its
+ * XCC_ID register | (1 << 32) if a wait timed out (0.5 s bound). *grid receives the number of
+ * workgroups (the CU count). Stream-ordered; allocates its exchange buffers on the first call. */
+int fl_probe_handoff(int32_t mode, int32_t words, int32_t rounds, uint64_t* out, int32_t* grid,
+                     void* stream);
 
 #ifdef __cplusplus
 }

@@ -146,6 +146,10 @@ class OracleModel:
         self.k_cache = self.v_cache = None
         self.linear, self.softmax, self.silu = IMPLS["torch"]
         self.last_residual = None
+        # trace: when a list, forward() appends per layer a dict of that layer's input and
+        # intermediate values (q, k, v after RoPE, attention output, SwiGLU output, output)
+        self.trace = None
+        self._rec = None
 
     def set_order(self, name):
         """Implementation of the reference semantics (IMPLS): "torch" (the default), "g128",
@@ -186,7 +190,24 @@ class OracleModel:
             ys.append(attention(q[m], self.k_cache[l, :, :T], self.v_cache[l, :, :T], valid, a.attn_scale,
                                 self.softmax))
         y = torch.stack(ys)
+        if self._rec is not None:
+            self._rec.update(q=q.reshape(M, -1), k=k.reshape(M, -1), v=v.reshape(M, -1), attn=y)
         return self.linear(y, w["wo"])
+
+    def layer(self, l, x, pos, depth=None, amask=None):
+        """Decoder block l on the M tokens x (bf16 [M, D]) at cache slots pos..pos+M-1 (reference
+        engine/model.py:160-164): h = x + attn(norm(x)) * rm; out = h + ffn(norm(h)) * rm."""
+        a, w, lin = self.args, self.w[l], self.linear
+        self._rec = {"x": x} if self.trace is not None else None
+        h1 = x + self.layer_attention(l, x, pos, depth, amask) * a.residual_multiplier
+        hn = rms_norm(h1, w["ffn_norm"], a.norm_eps)
+        act = self.silu(lin(hn, w["w1"])) * lin(hn, w["w3"])
+        out = h1 + lin(act, w["w2"]) * a.residual_multiplier
+        if self._rec is not None:
+            self._rec.update(act=act, out=out)
+            self.trace.append(self._rec)
+            self._rec = None
+        return out
 
     def forward(self, idx, pos, depth=None, amask=None, h=None):
         """idx int [M] at cache slots pos..pos+M-1 -> (logits bf16 [M, V], post-norm hidden bf16 [M, D]).
@@ -197,11 +218,7 @@ class OracleModel:
         lin = self.linear
         x = h.to(torch.bfloat16) if h is not None else self.embed[idx.long()] * a.embedding_multiplier
         for l in range(self.L):
-            w = self.w[l]
-            h1 = x + self.layer_attention(l, x, pos, depth, amask) * a.residual_multiplier
-            hn = rms_norm(h1, w["ffn_norm"], a.norm_eps)
-            ff = lin(self.silu(lin(hn, w["w1"])) * lin(hn, w["w3"]), w["w2"])
-            x = h1 + ff * a.residual_multiplier
+            x = self.layer(l, x, pos, depth, amask)
         self.last_residual = x
         xn = rms_norm(x, self.norm, a.norm_eps)
         logits = lin(xn, self.embed) / a.logits_scaling

@@ -1,4 +1,5 @@
 """Shared helpers of the parity tests: build engine + oracle from the same seeded weights."""
+import os
 import sys
 
 import torch
@@ -9,6 +10,29 @@ from flint_amd.synth import ModelArgs, synth_weights
 def log(*a):
     print(*a, flush=True)
     sys.stdout.flush()
+
+
+def record(line):
+    """log() a parity figure and, when FLINT_AMD_PARITY_OUT names a file, append it there (the
+    per-step / per-layer parity summaries kept beside the profiles)."""
+    log(line)
+    path = os.environ.get("FLINT_AMD_PARITY_OUT")
+    if path:
+        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+        with open(path, "a") as f:
+            f.write(line + "\n")
+
+
+def ulp_stats(e, r):
+    """Distance of bf16 values e from r (same shape, any float dtype) in bf16 ulps:
+    {same: fraction bit-identical, in1: fraction within one ulp of the larger magnitude of the pair,
+     top: max |e - r| in ulps of the largest magnitude in the vector}."""
+    e, r = e.float().reshape(-1), r.float().reshape(-1)
+    d = (e - r).abs()
+    own = bf16_ulp(torch.maximum(e.abs(), r.abs()))
+    top = bf16_ulp(torch.maximum(e.abs().max(), r.abs().max()))
+    return {"same": float((d == 0).float().mean()), "in1": float((d <= own).float().mean()),
+            "top": float((d / top).max())}
 
 
 def make_pair(name, seed=0, n_layer=None, device="cuda", weight_device="cpu", **over):

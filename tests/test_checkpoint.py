@@ -10,6 +10,7 @@ from flint_amd.checkpoint import (interleaved_to_hf, load_gptfast_checkpoint, lo
                                   state_dict_from_gptfast, state_dict_from_hf)
 from flint_amd.synth import ModelArgs, synth_weights
 from oracle.model import hf_to_interleaved_perm
+import flint_amd.checkpoint as ck
 
 
 def _args():
@@ -75,6 +76,10 @@ def test_interleaved_to_hf_inverts_the_permute():
         w = torch.randn(nh * hd, dim)
         assert torch.equal(interleaved_to_hf(_gptfast_permute(w, nh, hd, dim), nh, hd), w)
         assert torch.equal(interleaved_to_hf(w[hf_to_interleaved_perm(nh, hd)], nh, hd), w)
+        # the product's forward permutation equals the reference permute (and the oracle's)
+        perm = ck.hf_to_interleaved_perm(nh, hd)
+        assert torch.equal(w[perm], _gptfast_permute(w, nh, hd, dim))
+        assert torch.equal(perm, hf_to_interleaved_perm(nh, hd))
 
 
 def _gptfast_names(sd, args):

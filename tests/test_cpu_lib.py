@@ -88,3 +88,21 @@ def test_bench_rejects_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode != 0 and "one GPU" in r.stderr
+
+
+def test_torch_extension_loads():
+    """The torch-extension binding (flint_amd/_torch_ops*.so, built by flint_amd.build) imports on
+    the CPU and exposes the reference's op forms over torch tensors; argument checks run before
+    any device call."""
+    from flint_amd import build
+    if not os.path.exists(build.torch_ext_path()):
+        pytest.skip("torch extension not built (run python -m flint_amd.build)")
+    import flint_amd._torch_ops as ops
+    assert ops.version() >= 1
+    for name in ("decode_hidden", "decode_step", "verify", "check"):
+        assert hasattr(ops.Engine, name)
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    q = torch.zeros(8, 32, dtype=torch.int32)
+    sz = torch.zeros(8, 2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="device tensor"):
+        ops.int4_linear(x, q, sz, 0)

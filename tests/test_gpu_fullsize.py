@@ -15,14 +15,15 @@ test_gpu_verify.py and below) and the resulting K/V rows are copied into the ora
 compared step then starts from the same cache on both sides, and from there each side writes its
 own rows (teacher forcing on the engine's tokens).
 """
+import math
 import time
 
 import pytest
 import torch
 
 from flint_amd.synth import ModelArgs, synth_weights
-from tests.helpers import (log, logit_bar, logit_stats, near_tie, oracle_pair, row_bars,
-                           top2_margin)
+from tests.helpers import (log, logit_bar, logit_stats, near_tie, oracle_pair, record, row_bars,
+                           top2_margin, ulp_stats)
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(600)]
 
@@ -163,12 +164,25 @@ def test_config0_pos0_known_answer(one_layer):
 
 # ------------------------------------------------------------------ config 2: 40 layers, ctx 512
 
+def _flip_slack(a, b):
+    """Slack of a comparison of two flip counts over the same steps: about two standard deviations
+    of the difference of two binomial counts with the same rate (var ~ a + b), plus one."""
+    return int(math.ceil(2.0 * math.sqrt(a + b))) + 1
+
+
 def test_config2_full_model_greedy_64(full):
     """BASELINE config 2 / the north star's parity clause: the 40-layer int4 model, 512-token
     prompt, 64 greedy steps. Every step's logits within the 40-layer bars, the greedy token equal
     to the oracle's argmax on the engine's own prefix (teacher forcing) except at near-ties, and
     the kernel's mean distance over the steps no more than twice the oracle's own second-order
-    distance on the same steps."""
+    distance on the same steps.
+
+    Argmax flips are counted against the oracle's own: on every step the oracle also runs in its
+    three other valid implementations (per-group summation order; exp2-based softmax / SiLU; both),
+    and each implementation's flips against the default are counted on the same steps. The kernel
+    may flip no more often than the worst of them plus _flip_slack. (At 40 layers the oracle's own
+    implementations disagree on the greedy token at some of these steps, so "identical argmax over
+    64 free-running steps" holds for no implementation; the count is what can be compared.)"""
     args, eng, orc = full
     n = 511
     prompt = _prefill_both(eng, orc, n, seed=512)
@@ -182,19 +196,165 @@ def test_config2_full_model_greedy_64(full):
     eng.check()
     toks, lg = seq.cpu(), logits.cpu()
     ties, k_mean, o_mean, within = 0, [], [], []
+    others = ("g128", "exp2")
+    flips = {"g128+exp2": 0, **{o: 0 for o in others}}
     for i in range(steps):
         t = torch.tensor([int(toks[i])])
-        alt, ref = oracle_pair(orc, lambda: orc.forward(t, n + i)[0][0].float())
+        run = lambda: orc.forward(t, n + i)[0][0].float()    # noqa: E731
+        extra = {}
+        for o in others:       # run before the default: each forward rewrites its cache rows
+            orc.set_order(o)
+            try:
+                extra[o] = run()
+            finally:
+                orc.set_order("torch")
+        alt, ref = oracle_pair(orc, run)
         st, fl, tie = _check_step(f"config2 step {i} pos {n + i}", FULL, lg[i], ref, alt)
         assert int(torch.argmax(lg[i])) == int(toks[i + 1])     # fused argmax = argmax of the logits
+        am = int(torch.argmax(ref))
+        fo = {"g128+exp2": int(torch.argmax(alt)) != am, **{o: int(torch.argmax(extra[o])) != am for o in others}}
+        for k, v in fo.items():
+            flips[k] += v
+        record(f"config2 step {i:2d} pos {n + i}: margin {top2_margin(ref):.4f} kernel max|d| {st['max']:.4f} "
+               f"mean {st['mean']:.2e} {'FLIP' if tie else 'same'} | oracle "
+               + " ".join(f"{k} {'FLIP' if v else 'same'}" for k, v in fo.items()))
         ties += tie
         k_mean.append(st["mean"])
         o_mean.append(fl["mean"])
         within.append(st["within"])
     km, om_ = sum(k_mean) / steps, sum(o_mean) / steps
-    log(f"config2: {steps} steps, {ties} argmax differences (all near-ties), mean|d| kernel {km:.3e} "
-        f"vs oracle 2nd order {om_:.3e}, within 2e-2 {sum(within) / steps:.2%} on average")
+    worst = max(flips.values())
+    slack = _flip_slack(ties, worst)
+    record(f"config2: {steps} teacher-forced steps: kernel argmax flips {ties} (all near-ties); the oracle's "
+           f"own implementations against its default: {flips}; bar {worst} + {slack}; mean|d| kernel "
+           f"{km:.3e} vs oracle 2nd order {om_:.3e}, within 2e-2 {sum(within) / steps:.2%} on average")
     assert km <= 2 * om_
+    assert ties <= worst + slack, (ties, flips, slack)
+
+
+# ------------------------------------------------------------------ every layer, teacher-forced
+
+def _layer_engine(eng, l, holder):
+    """Layer l of eng's packed model as a one-layer engine (views of the same device tensors, no
+    copy); holder keeps one Transformer whose state and KV cache are reused for every layer."""
+    from flint_amd.model import PackedModel, Transformer
+    pk = eng.packed
+    t = {n: getattr(pk, n)[l:l + 1] for n in ("wqkv_q", "wqkv_sz", "wo_q", "wo_sz", "wgu_q", "wgu_sz",
+                                              "wd_q", "wd_sz", "attn_norm", "ffn_norm")}
+    t["final_norm"], t["embed"] = pk.final_norm, pk.embed
+    args1 = ModelArgs.from_name(L1)
+    p1 = PackedModel.from_tensors(args1, t, eng.device)
+    if "e" not in holder:
+        holder["e"] = Transformer(args1, p1)
+        holder["e"].setup_caches(1, eng.max_seq_length)
+    e1 = holder["e"]
+    e1.packed, e1._cw = p1, p1.c_weights()
+    return e1
+
+
+def _slip_layer(orc, l, x, pos):
+    """Layer l of the oracle with ONE planted rounding-point mistake (test-only): the SwiGLU
+    product formed in fp32 and rounded once instead of bf16(bf16(silu(g)) * u)
+    (engine/model.py:227-228). Returns the layer's SwiGLU output and output."""
+    import torch.nn.functional as F
+    from oracle.model import rms_norm
+    a, w, lin = orc.args, orc.w[l], orc.linear
+    h1 = x + orc.layer_attention(l, x, pos) * a.residual_multiplier
+    hn = rms_norm(h1, w["ffn_norm"], a.norm_eps)
+    act = (F.silu(lin(hn, w["w1"]).float()) * lin(hn, w["w3"]).float()).to(torch.bfloat16)
+    return act, h1 + lin(act, w["w2"]) * a.residual_multiplier
+
+
+# bars of one layer's values against the oracle's (every q/k/v, attention, SwiGLU and output
+# value of the layer): the fraction not bit-identical at most three times the oracle's second
+# implementation's on the same input plus 0.2% (v_dot2_f32_bf16's rare misrounding and the
+# hardware exp2 / rcp), at least 99.5% within one ulp of their own magnitude, and every value
+# within two ulps of the vector's largest
+MISMATCH_X, MISMATCH_ABS, IN1_MIN, TOP_MAX = 3.0, 2e-3, 0.995, 2.0
+
+
+def _per_layer(full, n, seed, label):
+    """Teacher-forced check of every layer at cache position n: the oracle runs the whole model
+    (recording each layer's input and values); each layer of the engine then runs alone from the
+    oracle's input to that layer, over the same cache rows, through fl_decode_hidden, and its q, k,
+    v (after RoPE), attention output, SwiGLU output and written-back residual are compared with the
+    oracle's layer. The reference checks its attention and MLP blocks in isolation the same way
+    (bench/megakernel_attn_test.py:64-67, bench/megakernel_test.py:52-55)."""
+    args, eng, orc = full
+    prompt = _prefill_both(eng, orc, n, seed=seed)
+    tok = torch.tensor([int(prompt[n])])
+    orc.trace = []
+    try:
+        orc.forward(tok, n)
+        ref_tr = orc.trace
+    finally:
+        orc.trace = None
+    NH, NKV, D = args.n_head, args.n_local_heads, args.dim
+    holder, worst = {}, {}
+    slip_caught = 0
+    try:
+        for l in range(args.n_layer):
+            e1 = _layer_engine(eng, l, holder)
+            e1.k_cache[0, :, :n] = eng.k_cache[l, :, :n]
+            e1.v_cache[0, :, :n] = eng.v_cache[l, :, :n]
+            x = ref_tr[l]["x"]
+            h = x.reshape(-1).to(eng.device).clone()
+            e1.decode_hidden(h, n)
+            e1.check()
+            act = e1.activations()
+            qkv = act["qkv"].cpu()
+            ker = {"q": qkv[:NH * 64], "k": qkv[NH * 64:(NH + NKV) * 64], "v": qkv[(NH + NKV) * 64:],
+                   "attn": act["attn"].cpu(), "act": act["act"].cpu(), "out": h.cpu()}
+            assert torch.equal(ker["k"].view(NKV, 64), e1.k_cache[0, :, n].cpu())
+            assert torch.equal(ker["v"].view(NKV, 64), e1.v_cache[0, :, n].cpu())
+            # the oracle's second implementation of the same layer on the same input and cache
+            orc.set_order("g128+exp2")
+            orc.trace = []
+            try:
+                orc.layer(l, x, n)
+                alt = orc.trace[0]
+            finally:
+                orc.trace = None
+                orc.set_order("torch")
+            slip_act, slip_out = _slip_layer(orc, l, x, n)
+            ref = ref_tr[l]
+            line = f"{label} layer {l:2d}:"
+            for name in ("q", "k", "v", "attn", "act", "out"):
+                sk, sa = ulp_stats(ker[name], ref[name]), ulp_stats(alt[name], ref[name])
+                line += (f" {name} {1 - sk['same']:.2%}/{1 - sa['same']:.2%} in1 {sk['in1']:.2%}"
+                         f" top {sk['top']:.1f}")
+                bar = MISMATCH_X * (1 - sa["same"]) + MISMATCH_ABS
+                w = worst.setdefault(name, [0.0, 0.0, 1.0, 0.0])
+                w[0] = max(w[0], 1 - sk["same"])
+                w[1] = max(w[1], 1 - sa["same"])
+                w[2] = min(w[2], sk["in1"])
+                w[3] = max(w[3], sk["top"])
+                assert 1 - sk["same"] <= bar, (label, l, name, sk, sa)
+                assert sk["in1"] >= IN1_MIN and sk["top"] <= TOP_MAX, (label, l, name, sk)
+                if name == "act":
+                    ss = ulp_stats(slip_act, ref["act"])
+                    slip_caught += (1 - ss["same"]) > bar
+                    line += f" [planted slip {1 - ss['same']:.2%}]"
+            record(line)
+    finally:
+        if "e" in holder:
+            holder["e"].close()
+    record(f"{label}: worst over {args.n_layer} layers (kernel not bit-identical / oracle 2nd impl not "
+           f"bit-identical / kernel within 1 ulp / kernel max ulps of the largest): " +
+           ", ".join(f"{k} {v[0]:.2%}/{v[1]:.2%}/{v[2]:.2%}/{v[3]:.1f}" for k, v in worst.items()) +
+           f"; a planted SwiGLU rounding slip fails the act bar in {slip_caught} of {args.n_layer} layers")
+    assert slip_caught == args.n_layer
+
+
+def test_every_layer_teacher_forced_ctx512(full):
+    """All 40 layers, one at a time, at position 511 after a 511-token prompt (config 2's context)."""
+    _per_layer(full, 511, 5120, "per-layer ctx511")
+
+
+def test_every_layer_teacher_forced_ctx8192(full):
+    """All 40 layers, one at a time, at position 8188 after an 8188-token prompt (config 3's
+    context: attention over 8189 keys, the per-head slices merged in the O phase)."""
+    _per_layer(full, 8188, 81920, "per-layer ctx8188")
 
 
 # ------------------------------------------------------------------ config 3: 40 layers, ctx 8192

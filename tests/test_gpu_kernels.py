@@ -92,7 +92,9 @@ def test_gemv_matches_oracle_linear(dev):
 
 
 GEMM_CASES = [(3584, 2560, 5), (2560, 8192, 8), (16384, 2560, 16), (24, 384, 3), (8, 128, 1),
-              (2560, 2560, 2)]
+              (2560, 2560, 2),
+              # the second 16-row activation block (tokens 16..31), with N not a multiple of 16
+              (3584, 2560, 17), (2568, 8192, 24), (1000, 2560, 32), (24, 384, 32)]
 
 
 @pytest.mark.parametrize("n,k,m", GEMM_CASES)
@@ -118,10 +120,11 @@ def test_gemm_vs_fp64(dev, n, k, m):
     assert mism < 2e-3
 
 
-def test_gemm_rows_match_gemv(dev):
+@pytest.mark.parametrize("m", [8, 32])
+def test_gemm_rows_match_gemv(dev, m):
     """Row m of the M-row GEMM equals the M=1 GEMV of x[m] up to fp32 summation order."""
     from flint_amd.quantize import quantize_int4, gemm_int4, gemv_int4
-    n, k, m = 3584, 2560, 8
+    n, k = 3584, 2560
     w = _weights(n, k, 9)
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(10)).to(torch.bfloat16)
     q, sz = quantize_int4(w.to(dev))
@@ -131,3 +134,51 @@ def test_gemm_rows_match_gemv(dev):
         d = (y[i].float() - yv.float()).abs()
         assert float(d.max()) <= float(yv.float().abs().max()) * 2.0 ** -7
         assert float((d > 0).float().mean()) < 2e-3
+
+
+@pytest.mark.parametrize("lead", [(1,), (8,), (2, 16), (32,)])
+def test_weight_only_int4_linear(dev, lead):
+    """WeightOnlyInt4Linear (the drop-in for reference engine/quantize.py:483-525) at M = 1
+    (the GEMV) and M up to 32 (the GEMM, leading dimensions flattened) against the oracle's
+    linear on the dequantised weights; its buffers hold the quantised values exactly."""
+    from flint_amd.quantize import WeightOnlyInt4Linear, unpack_q, unpack_sz
+    from oracle import quant
+    n, k = 2560, 2560
+    w = _weights(n, k, 12)
+    mod = WeightOnlyInt4Linear.from_float(w.to(dev))
+    qo, so, zo = quant.group_quantize(w)
+    assert torch.equal(unpack_q(mod.weight).cpu(), qo)
+    s, z = unpack_sz(mod.scales_and_zeros)
+    assert torch.equal(s.cpu().view(torch.int16), so.view(torch.int16))
+    assert torch.equal(z.cpu().view(torch.int16), zo.view(torch.int16))
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(*lead, k, generator=g).to(torch.bfloat16)
+    y = mod(x.to(dev)).cpu()
+    assert y.shape == (*lead, n) and y.dtype == torch.bfloat16
+    ref = torch.nn.functional.linear(x.reshape(-1, k), quant.dq_linear_weight(w)).view(*lead, n)
+    diff = (y.float() - ref.float()).abs().max().item()
+    mism = (y != ref).float().mean().item()
+    log(f"WeightOnlyInt4Linear lead={lead}: max|diff|={diff:.3e} mismatch={mism:.2e}")
+    assert mism < 2e-3 and diff <= 2.0 ** -7 * float(ref.float().abs().max())
+    with pytest.raises(Exception):
+        mod(torch.zeros(33, k, dtype=torch.bfloat16, device=dev))
+
+
+def test_scales_and_zeros_gptfast_layout(dev):
+    """scales_and_zeros_gptfast gives gpt-fast's [K/128, N, 2] bf16 tensor
+    (reference engine/quantize.py:79-93 pack_scales_and_zeros) of the same values the oracle
+    packs."""
+    from flint_amd.quantize import quantize_int4, scales_and_zeros_gptfast
+    from oracle import quant
+    n, k = 384, 1024
+    w = _weights(n, k, 14, "edge")
+    q, sz = quantize_int4(w.to(dev))
+    got = scales_and_zeros_gptfast(sz).cpu()
+    _, so, zo = quant.group_quantize(w)
+    ref = quant.pack_scales_and_zeros(so, zo)
+    assert got.shape == (k // 128, n, 2) and got.dtype == torch.bfloat16
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    # the reference's definition: entry [g, n] = (scale, zero) of row n, group g
+    for g, r in ((0, 0), (3, 17), (7, n - 1)):
+        assert got[g, r, 0].view(torch.int16) == so[r, g].view(torch.int16)
+        assert got[g, r, 1].view(torch.int16) == zo[r, g].view(torch.int16)

@@ -183,3 +183,72 @@ def test_forward_chain_equals_sequential_steps():
         l2, h2 = o2.forward(toks[i:i + 1], i)
         assert float((l1[i].float() - l2[0].float()).abs().max()) <= 2e-2
     assert torch.equal(o1.k_cache, o2.k_cache) or float((o1.k_cache.float() - o2.k_cache.float()).abs().max()) <= 0.05
+
+
+def _tree(parent):
+    """depth and ancestor-or-self mask of a tree given by parent indices (parent[0] = -1), as
+    reference spec_tree.py:101-104 builds them."""
+    m = len(parent)
+    depth = torch.zeros(m, dtype=torch.int32)
+    amask = torch.zeros(m, m, dtype=torch.uint8)
+    for i in range(m):
+        j = i
+        while j >= 0:
+            amask[i, j] = 1
+            j = parent[j]
+        depth[i] = int(amask[i].sum()) - 1
+    return depth, amask
+
+
+def _path(parent, i):
+    p = []
+    while i >= 0:
+        p.append(i)
+        i = parent[i]
+    return p[::-1]
+
+
+def test_forward_tree_rows_equal_chain_of_their_path():
+    """The oracle's tree forward (depth / amask, reference verify_mega.cu:106-244 semantics and
+    spec_tree.py:46-51): row i of an M-node tree verify equals the last row of a plain chain
+    forward of the root -> i path at consecutive slots, for every node (RoPE at pos + depth, the
+    same keys in the same order). A dropped ancestor in the mask or a depth off by one breaks it."""
+    from flint_amd.synth import ModelArgs, synth_weights
+    a = ModelArgs.from_name("tiny")
+    sd = synth_weights(a, 3)
+    pos = 9
+    parent = [-1, 0, 0, 1, 1, 2, 3, 5, 3, 7]
+    depth, amask = _tree(parent)
+    g = torch.Generator().manual_seed(5)
+    toks = torch.randint(0, a.vocab_size, (len(parent),), generator=g)
+    kv = torch.randn(2, a.n_layer, a.n_local_heads, pos, 64, generator=g).to(torch.bfloat16)
+
+    def model():
+        o = om.OracleModel(a, sd)
+        o.setup_caches(64)
+        o.k_cache[:, :, :pos], o.v_cache[:, :, :pos] = kv[0], kv[1]
+        return o
+    o = model()
+    tree, _ = o.forward(toks, pos, depth=depth, amask=amask)
+    worst = 0.0
+    for i in range(len(parent)):
+        p = _path(parent, i)
+        oc = model()
+        chain, _ = oc.forward(toks[p], pos)
+        d = float((tree[i].float() - chain[-1].float()).abs().max())
+        worst = max(worst, d)
+        assert d <= 2e-2, (i, p, d)
+    # planted mistakes: node 6 (path 0-1-3-6) without its grandparent in the mask; node 9 with
+    # every depth one too large
+    bad = amask.clone()
+    bad[6, 1] = 0
+    o = model()
+    wrong, _ = o.forward(toks, pos, depth=depth, amask=bad)
+    oc = model()
+    chain, _ = oc.forward(toks[_path(parent, 6)], pos)
+    assert float((wrong[6].float() - chain[-1].float()).abs().max()) > 10 * max(worst, 1e-3)
+    o = model()
+    wrong, _ = o.forward(toks, pos, depth=depth + 1, amask=amask)
+    oc = model()
+    chain, _ = oc.forward(toks[_path(parent, 9)], pos)
+    assert float((wrong[9].float() - chain[-1].float()).abs().max()) > 10 * max(worst, 1e-3)

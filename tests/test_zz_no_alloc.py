@@ -45,3 +45,35 @@ def test_sample_noalloc_rejects_oversized_input(dev):
     tok = torch.zeros(1, dtype=torch.int32, device="cuda")
     rc = _call("fl_sample_noalloc", lg, 1, 65537, 1.0, 0, 0, 0, tok, None)
     assert rc == -1  # FL_E_ARG: vocab above the scratch's 65536
+
+
+def test_sample_noalloc_in_a_captured_graph(dev):
+    """The entry point is for callers that cannot allocate, code under HIP graph capture among
+    them: captured once into a graph (after a first direct call, which looks the scratch address
+    up), every replay over new logits written between replays gives the tokens and probabilities
+    of a direct call on the same logits."""
+    rows, vocab, top_k = 4, 49152, 200
+    g = torch.Generator(device="cuda").manual_seed(5)
+    lg = torch.empty(rows, vocab, dtype=torch.float32, device="cuda")
+    tok = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+    pr = torch.empty(rows, vocab, dtype=torch.float32, device="cuda")
+    lg.copy_((torch.randn(rows, vocab, device="cuda", generator=g) * 2).to(torch.bfloat16).float())
+    _lib.check("fl_sample_noalloc", _call("fl_sample_noalloc", lg, rows, vocab, 0.9, top_k, 77, 3, tok, pr))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _call("fl_sample_noalloc", lg, rows, vocab, 0.9, top_k, 77, 3, tok, pr)
+    _lib.check("fl_sample_noalloc (captured)", rc)
+    for i in range(4):
+        lg.copy_((torch.randn(rows, vocab, device="cuda", generator=g) * 2).to(torch.bfloat16).float())
+        tok.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        tg, pg = tok.cpu(), pr.cpu()
+        td = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+        pd = torch.empty(rows, vocab, dtype=torch.float32, device="cuda")
+        _lib.check("fl_sample_noalloc", _call("fl_sample_noalloc", lg, rows, vocab, 0.9, top_k, 77, 3, td, pd))
+        torch.cuda.synchronize()
+        print(f"replay {i}: tokens {tg.tolist()}", flush=True)
+        assert torch.equal(tg, td.cpu()) and torch.equal(pg, pd.cpu())
+        assert bool(((tg >= 0) & (tg < vocab)).all())
