@@ -310,7 +310,40 @@ def gemv_sweep(args, dev, sets=40, rounds=3):
         out[name] = {"n": n, "k": k, "us": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
                      "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     rot = sets * sum(W[nm][0][0].numel() * 4 + W[nm][1][0].numel() * 4 for nm, _, _ in shapes)
-    return {"sets_per_shape": sets, "rotation_bytes": rot, "shapes": out}
+    # the same weights in the tiled layout, through the matrix-core GEMV (fl_gemv_int4_tiled)
+    T = {}
+    for name, n, k in shapes:
+        q = W[name][0]
+        qt = torch.empty(sets, n // 16, k // 128, 64, 4, dtype=torch.int32, device=dev)
+        for i in range(sets):
+            _lib.call("fl_tile_int4", _lib.ptr(q[i]), _lib.ptr(qt[i]), n, k, sp)
+        T[name] = qt
+
+    def call_t(name, i):
+        q, sz, x, y, n, k = W[name]
+        _lib.call("fl_gemv_int4_tiled", _lib.ptr(T[name][i]), _lib.ptr(sz[i]), _lib.ptr(x), _lib.ptr(y), n, k, sp)
+    for i in range(sets):
+        for name, _, _ in shapes:
+            call_t(name, i)
+    torch.cuda.synchronize()
+    ev = {name: [] for name, _, _ in shapes}
+    for _ in range(rounds):
+        for i in range(sets):
+            for name, _, _ in shapes:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                call_t(name, i)
+                e1.record(stream)
+                ev[name].append((e0, e1))
+    torch.cuda.synchronize()
+    tiled = {}
+    for name, n, k in shapes:
+        us = sum(a.elapsed_time(b) for a, b in ev[name]) * 1000.0 / len(ev[name])
+        nbytes = n * k // 2 + n * (k // 128) * 4 + 2 * k + 2 * n
+        tiled[name] = {"us": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                       "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del T
+    return {"sets_per_shape": sets, "rotation_bytes": rot, "shapes": out, "tiled_mfma": tiled}
 
 
 def long_context(model, args, dev, ctx=8192, steps=128):
@@ -408,6 +441,8 @@ def main():
                     help="skip the speculative-loop timing (chain / tree with a known draft)")
     ap.add_argument("--no-sampling", action="store_true",
                     help="skip the sampler timings (standalone and fused into the decode launch)")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="run only the config-1 GEMV sweep and print its JSON (for profiling)")
     ap.add_argument("--no-handoff", action="store_true",
                     help="skip the hand-off micro-benchmark (fl_probe_handoff)")
     ap.add_argument("--maps", default=None,
@@ -427,6 +462,11 @@ def main():
 
     dev = torch.device("cuda:0")
     args = ModelArgs.from_name(a.config)
+    if a.gemv_only:
+        gemv = gemv_sweep(args, dev)
+        log(f"config 1 (fl_gemv_int4, {gemv['rotation_bytes'] / 1e9:.2f} GB rotation): {gemv}")
+        print(json.dumps({"gemv_sweep": gemv}), flush=True)
+        return
     log(f"synthesising {a.config} weights on the GPU")
     sd = synth_weights(args, seed=0, device=dev)
     model = Transformer.from_weights(args, sd, dev)

@@ -29,7 +29,7 @@ EXPORTS = [
     "fl_state_profile", "fl_state_buffers", "fl_state_set_wait_limit",
     "fl_state_force_timeout",
     "fl_decode_step", "fl_decode_sample", "fl_decode_hidden", "fl_verify", "fl_kv_move", "fl_sample",
-    "fl_sample_noalloc", "fl_probe_handoff",
+    "fl_sample_noalloc", "fl_probe_handoff", "fl_tile_int4", "fl_dequant_int4_tiled", "fl_gemv_int4_tiled",
 ]
 
 
@@ -96,6 +96,9 @@ def load(path=LIB_PATH):
         "fl_sample": ([vp, i32, i32, f32, i32, ctypes.c_uint64, ctypes.c_uint64, vp, vp, vp, vp], i32),
         "fl_sample_noalloc": ([vp, i32, i32, f32, i32, ctypes.c_uint64, ctypes.c_uint64, vp, vp, vp, vp], i32),
         "fl_probe_handoff": ([i32, i32, i32, vp, vp, vp], i32),
+        "fl_tile_int4": ([vp, vp, i32, i32, vp], i32),
+        "fl_dequant_int4_tiled": ([vp, vp, vp, i32, i32, vp], i32),
+        "fl_gemv_int4_tiled": ([vp, vp, vp, vp, i32, i32, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libflint_amd.so")
 OBJDIR = os.path.join(HERE, "_build")
-SOURCES = ["fl_quant.hip", "fl_decode.hip", "fl_sample.hip", "fl_probe.hip"]
+SOURCES = ["fl_quant.hip", "fl_decode.hip", "fl_sample.hip", "fl_probe.hip", "fl_tiled.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -23,9 +23,14 @@ FLAGS = [
 ]
 
 
+# per-source extra flags: the MFMA-dequant kernels keep their matrix-core results in VGPRs (the
+# accumulation registers would cost a copy per result read by the vector ALUs)
+EXTRA = {"fl_tiled.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src):
     obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

@@ -54,8 +54,9 @@ __global__ __launch_bounds__(PR_NT, 1) void k_probe_handoff(uint32_t* __restrict
   for (int r = 0; r < rounds && !timed_out; ++r) {
     uint32_t* v = vec + (size_t)(r & 1) * words;
     const uint32_t tag = (uint32_t)(r % 65535) + 1u;
+    // stored without waiting for them (the kernels' producers do not wait either: the tag in
+    // every word is what the consumers check)
     for (int i = w0 + tid; i < w1; i += PR_NT) st_coh_u32(v + i, (tag << 16) | (uint32_t)(i & 0xFFFF));
-    wait_mem();
     // poll: every thread requests its words, then re-requests the ones not yet tagged
     uint32_t got[PR_MAXP];
 #pragma unroll

@@ -4,6 +4,7 @@
 // :102-128, :131-135): every step is a bf16 tensor op in the reference, so every step here
 // computes in fp32 and rounds to bf16 (RNE) at the same points.
 #include "fl_common.h"
+#include <algorithm>
 
 namespace {
 
@@ -133,6 +134,93 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(const uint32_t* __restric
   if (row < rows && li == 0) y[r0 + row] = (uint16_t)f2bf(acc);
 }
 
+// M=1 GEMV streamed by persistent waves (the shapes whose K is 2560 or 8192, i.e. every int4
+// layer of the 3B model). One workgroup of GV_NW waves per CU; a wave takes tiles of 64 >> LG
+// rows, 2^LG lanes per row and C 16-byte chunks per lane (one row's K / 32 chunks exactly), and
+// walks tiles t, t + W, t + 2W, ... (W waves in the grid) with two register buffers: the next
+// tile's weights are requested before the current tile is dequantised, so the HBM stream and
+// the VALU work overlap instead of every workgroup loading, then computing. The activation
+// vector is staged in LDS once per workgroup (its requests go out first, ahead of the weights,
+// so the first tile does not wait behind them). A row's partial sums meet in a DPP reduction
+// over its lanes (fixed order); its first lane writes y. All loads are range-checked buffer
+// loads (tiles past N read zeros and store nothing), so no load sits under a branch.
+constexpr int GV_NW = 8;
+constexpr int GV_NT = GV_NW * 64;
+
+template <int LG, int C>
+__device__ __forceinline__ void gv_load(__amdgpu_buffer_rsrc_t wr, __amdgpu_buffer_rsrc_t sr, int t, int n,
+                                        int cpr, int gpr, uint4 (&w)[C], uint32_t (&s)[C]) {
+  const int lane = threadIdx.x & 63;
+  const int row = t * (64 >> LG) + (lane >> LG), j = lane & ((1 << LG) - 1);
+  const bool ok = row < n;
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const int c = j + (i << LG);
+    w[i] = buf_ld128(wr, ok ? (uint32_t)(row * cpr + c) * 16u : 0xFFFFFFF0u);
+    s[i] = buf_ld32(sr, ok ? (uint32_t)(row * gpr + (c >> 2)) * 4u : 0xFFFFFFF0u);
+  }
+}
+
+template <int LG, int C>
+__device__ __forceinline__ void gv_tile(const uint4* xs, int t, int n, const uint4 (&w)[C],
+                                        const uint32_t (&s)[C], uint16_t* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int row = t * (64 >> LG) + (lane >> LG), j = lane & ((1 << LG) - 1);
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const int c = j + (i << LG);
+    acc = chunk_dot(w[i], s[i], xs + 5 * c, acc);  // chunk c's 4 x slots start at 5c (bank spread)
+  }
+  acc = group_sum(acc, 1 << LG);
+  if (j == 0 && row < n) y[row] = (uint16_t)f2bf(acc);
+}
+
+template <int LG, int C>
+__global__ __launch_bounds__(GV_NT, 1) void k_gemv_stream(const uint32_t* __restrict__ q,
+                                                          const uint32_t* __restrict__ sz,
+                                                          const uint16_t* __restrict__ x,
+                                                          uint16_t* __restrict__ y, int n, int k) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint4* xs = reinterpret_cast<uint4*>(smem);  // x: logical slot v at v + v / 4
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int cpr = k >> 5, gpr = k >> 7;
+  const int ntiles = (n + (64 >> LG) - 1) / (64 >> LG);
+  const int W = gridDim.x * GV_NW;
+  const auto xr = buf_rsrc(x, (uint32_t)k * 2u);
+  const auto wr = buf_rsrc(q, (uint32_t)n * (uint32_t)(k >> 1));
+  const auto sr = buf_rsrc(sz, (uint32_t)n * (uint32_t)gpr * 4u);
+  constexpr int XPT = 8192 / 8 / GV_NT;  // 16-byte x slots per thread (k <= 8192)
+  uint4 xv[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) xv[i] = buf_ld128(xr, (uint32_t)(tid + i * GV_NT) * 16u);
+  uint4 wa[C], wb[C];
+  uint32_t sa[C], sb[C];
+  int t = blockIdx.x * GV_NW + wave;
+  // a wave takes tiles in pairs (t, t + W): both tiles' requests go out together, then both are
+  // computed (no register buffer is carried across the loop, so nothing has to be copied)
+  gv_load<LG, C>(wr, sr, t, n, cpr, gpr, wa, sa);
+  gv_load<LG, C>(wr, sr, t + W, n, cpr, gpr, wb, sb);
+  __builtin_amdgcn_sched_barrier(0);
+  // every thread stores its slots (the LDS holds XPT * GV_NT of them; slots past K hold zeros),
+  // so no store, and no load feeding one, sits under a branch that would wait for every load
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int v = tid + i * GV_NT;
+    xs[v + (v >> 2)] = xv[i];
+  }
+  lds_barrier();
+  while (t < ntiles) {
+    gv_tile<LG, C>(xs, t, n, wa, sa, y);
+    if (t + W < ntiles) gv_tile<LG, C>(xs, t + W, n, wb, sb, y);
+    t += 2 * W;
+    if (t >= ntiles) break;
+    gv_load<LG, C>(wr, sr, t, n, cpr, gpr, wa, sa);
+    gv_load<LG, C>(wr, sr, t + W, n, cpr, gpr, wb, sb);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Y[M, N] = bf16(X[M, K] . dq[N, K]^T), 1 <= M <= 16, on the matrix cores: one workgroup of 4
 // waves per 16-row tile of W; the waves take the K/128 groups round-robin, each lane dequantises
 // one 16-byte chunk per group (row n0 + l%16, chunk l/16) and feeds it to four MFMA steps, so
@@ -224,6 +312,26 @@ int fl_gemv_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint1
                  int32_t k, void* stream) {
   if (!q || !sz || !x || !y || n <= 0 || k <= 0 || (k % FL_GROUP) != 0 || k > 16384)
     return FL_E_ARG;
+  // K = 2560 / 8192: the streamed kernel, one workgroup per CU (fewer when N has fewer tiles)
+  if ((k == 2560 || k == 8192) && (int64_t)n * (k / 2) <= 0x7FFFFFFFll) {
+    const void* kern = k == 2560 ? reinterpret_cast<const void*>(k_gemv_stream<4, 5>)
+                                 : reinterpret_cast<const void*>(k_gemv_stream<6, 4>);
+    const int rpt = k == 2560 ? 4 : 1;
+    static int cus = 0;
+    if (!cus) {
+      int dev = 0;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        return FL_E_HIP;
+    }
+    const int tiles = (n + rpt - 1) / rpt;
+    const int blocks = std::min(cus, (tiles + GV_NW - 1) / GV_NW);
+    const size_t shm = (size_t)(8192 / 8 + 8192 / 32) * 16;  // every thread's x slots (k <= 8192)
+    const int nn = n, kk = k;
+    void* args[] = {(void*)&q, (void*)&sz, (void*)&x, (void*)&y, (void*)&nn, (void*)&kk};
+    return hipLaunchKernel(kern, dim3(blocks), dim3(GV_NT), args, shm, as_stream(stream)) == hipSuccess
+               ? FL_OK : FL_E_LAUNCH;
+  }
   const int cpr = k / 32;
   // rows per workgroup: as many as keep every thread at <= kGemvMaxChunks chunks, at most 16
   int rows = (kGemvThreads * kGemvMaxChunks) / cpr;

@@ -1,0 +1,234 @@
+// int4 GEMV whose exact dequantisation runs on the matrix cores, over a tiled weight layout.
+//
+// The dequantisation contract is the same as everywhere in this library, gpt-fast's
+// bf16(bf16((q - 8) * s) + z) (reference engine/quantize.py:138-155), and y = bf16(sum x * dq) with
+// fp32 accumulation (quantize.py:517-525). On the vector ALUs that takes about 4.4 operations per
+// weight (fl_common.h dq32 + the dot), which bounds an HBM-streaming GEMV at about half of the
+// bandwidth. Here the two exact fp32 steps and the dot run as MFMAs instead:
+//   D1 = A1 . diag(s) + C1:  A1 = (128 + q) as bf16 (one AND-OR per two weights puts the nibble in
+//        the mantissa of 128.0), C1 = -136 s, so D1 = (q - 8) s exactly (one nonzero product);
+//        v_cvt_pk_bf16_f32 rounds it to bf16 (RNE), the reference's first rounding;
+//   D2 = I . a + C2:  C2 = z, so D2 = fp32(a + z), the reference's fp32 add; cvt rounds it again;
+//   D3 += x . dq  (16x16x32 MFMA over two 16-position tiles; every output row holds the same sum).
+// Both dequantisation MFMAs have one nonzero product per output plus the accumulator, so their
+// fp32 results are exactly the reference's (D1 is exactly representable; D2 is one fp32 addition,
+// and where that addition rounds, |a| is below 2^-16 |z| and the bf16 rounding gives z either way).
+// The vector ALUs keep the nibble extraction and the four roundings: about 2.4 operations per
+// weight instead of 4.4.
+//
+// Tiled layout (fl_tile_int4 converts this library's row layout into it): for each block of 16 rows
+// and each 128-column group, 1 KB; lane l = 16 b + c of a wave reads the 16 bytes at l * 16:
+// 4 words holding rows 4b..4b+3 at the 8 columns c + 16 t (t = 0..7):
+//   word 0: bits 4t..4t+3 = q[4b][c + 16t], bits 16+4t.. = q[4b+1][c + 16t]   (t = 0..3)
+//   word 1: the same for t = 4..7;  words 2 / 3: rows 4b+2 / 4b+3.
+// That is the A operand of a 16x16x16 MFMA (lane: 4 consecutive k = rows, at i = column c) for each
+// of the 8 tiles, after one AND-OR per register. Scale / zero words stay [N, K/128].
+#include "fl_common.h"
+#include <algorithm>
+
+namespace {
+
+typedef short fl_s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ fl_s16x4 s4(uint32_t lo, uint32_t hi) {
+  return __builtin_bit_cast(fl_s16x4, make_uint2(lo, hi));
+}
+__device__ __forceinline__ fl_bf16x8 b8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_bit_cast(fl_bf16x8, make_uint4(a, b, c, d));
+}
+// (w & mask) | magic in one instruction (the mask in an SGPR, the magic in a VGPR: gfx950's
+// three-operand encoding takes no literal)
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(magic));
+  return r;
+}
+
+// row layout -> tiled layout: one thread per 16-byte tiled chunk
+__global__ __launch_bounds__(256) void k_tile_int4(const uint32_t* __restrict__ q, uint4* __restrict__ qt,
+                                                   int n, int k) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int G = k >> 7;
+  const int64_t chunks = (int64_t)(n >> 4) * G * 64;
+  if (idx >= chunks) return;
+  const int l = (int)(idx & 63), b = l >> 4, c = l & 15;
+  const int64_t blk = idx >> 6;
+  const int g = (int)(blk % G), rb = (int)(blk / G);
+  const int kw = k >> 3;  // words per row
+  auto nib = [&](int r, int col) -> uint32_t {  // q[r][col] of the row layout
+    const uint32_t w = q[(size_t)r * kw + (col >> 3)];
+    return (w >> (4 * nib_pos(col & 7))) & 0xFu;
+  };
+  uint32_t wd[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {      // rows 4b + 2h, 4b + 2h + 1 -> words 2h, 2h + 1
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int col = g * 128 + c + 16 * t;
+      const int r = rb * 16 + 4 * b + 2 * h;
+      const uint32_t v = nib(r, col) | (nib(r + 1, col) << 16);
+      wd[2 * h + (t >> 2)] |= v << (4 * (t & 3));
+    }
+  }
+  qt[idx] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+}
+
+// This lane's per-group constants: B1 = diag(s) (k = 4b + e, column c), C1 = -136 s_c,
+// C2 = z_c, from the (scale, zero) word of row c of the block
+struct GroupK {
+  uint32_t b1lo, b1hi;
+  fl_f32x4 c1, c2;
+};
+__device__ __forceinline__ GroupK group_k(uint32_t szw, int d) {  // d = c - 4b
+  const uint32_t sb = szw & 0xFFFFu;
+  GroupK k;
+  k.b1lo = d == 0 ? sb : (d == 1 ? sb << 16 : 0u);
+  k.b1hi = d == 2 ? sb : (d == 3 ? sb << 16 : 0u);
+  const float c1 = -136.0f * bf2f(sb), z = bf2f(szw >> 16);
+  k.c1 = fl_f32x4{c1, c1, c1, c1};
+  k.c2 = fl_f32x4{z, z, z, z};
+  return k;
+}
+
+// Dequantise one 16x16 tile (registers r0 / r1 from the tiled chunk: (128 + q) pairs of rows
+// 4b, 4b+1 and 4b+2, 4b+3 at column c) into this lane's bf16 pairs of columns 4b .. 4b+3 of row c.
+__device__ __forceinline__ void tile_dq(uint32_t r0, uint32_t r1, const GroupK& k, uint32_t ilo, uint32_t ihi,
+                                        uint32_t& o0, uint32_t& o1) {
+  const fl_f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(s4(r0, r1), s4(k.b1lo, k.b1hi), k.c1, 0, 0, 0);
+  const uint32_t a0 = pack_bf16x2(d1[0], d1[1]), a1 = pack_bf16x2(d1[2], d1[3]);
+  const fl_f32x4 d2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(s4(ilo, ihi), s4(a0, a1), k.c2, 0, 0, 0);
+  o0 = pack_bf16x2(d2[0], d2[1]);
+  o1 = pack_bf16x2(d2[2], d2[3]);
+}
+
+// One 1 KB unit (16 rows x one 128-group) of the tiled matrix, dequantised and dotted with x:
+// acc += x[group] . dq^T. w: this lane's 16 bytes; xs: x in LDS (bf16, plain order).
+__device__ __forceinline__ void unit_dot(uint4 w, uint32_t szw, const uint16_t* xs, int g, uint32_t ilo,
+                                         uint32_t ihi, fl_f32x4& acc) {
+  const int lane = threadIdx.x & 63, b = lane >> 4, c = lane & 15;
+  const GroupK k = group_k(szw, c - 4 * b);
+  const uint32_t magic = 0x43004300u, mask = 0x000F000Fu;
+  uint32_t wa = w.x, wb = w.y, wc = w.z, wd = w.w;
+#pragma unroll
+  for (int tp = 0; tp < 4; ++tp) {  // tiles 2tp, 2tp + 1: one 16x16x32 dot MFMA per pair
+    uint32_t q0[2], q1[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int t = 2 * tp + h;
+      uint32_t& lo = t < 4 ? wa : wb;
+      uint32_t& hi = t < 4 ? wc : wd;
+      const uint32_t r0 = and_or(lo, mask, magic), r1 = and_or(hi, mask, magic);
+      lo >>= 4;
+      hi >>= 4;
+      tile_dq(r0, r1, k, ilo, ihi, q0[h], q1[h]);
+    }
+    // x at columns 4b .. 4b+3 of tiles 2tp and 2tp + 1 (k = 8b + e of the MFMA)
+    const uint2 xa = *reinterpret_cast<const uint2*>(xs + g * 128 + 32 * tp + 4 * b);
+    const uint2 xb = *reinterpret_cast<const uint2*>(xs + g * 128 + 32 * tp + 16 + 4 * b);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b8(xa.x, xa.y, xb.x, xb.y), b8(q0[0], q1[0], q0[1], q1[1]),
+                                                  acc, 0, 0, 0);
+  }
+}
+
+// y = bf16(W x): one workgroup of TW_NW waves per 16-row block (blocks strided over the grid); the
+// waves take the block's 128-groups round-robin, their partial sums meet in LDS in wave order.
+constexpr int TW_NW = 4;
+__global__ __launch_bounds__(TW_NW * 64) void k_gemv_tiled(const uint4* __restrict__ qt, const uint32_t* __restrict__ sz,
+                                                           const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                           int n, int k) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+  float* part = reinterpret_cast<float*>(smem + (size_t)k * 2);  // [TW_NW][16]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = k >> 7, nb = n >> 4;
+  for (int i = tid; i < (k >> 3); i += TW_NW * 64)
+    reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(x)[i];
+  __syncthreads();
+  const int b = lane >> 4, c = lane & 15, d = c - 4 * b;
+  const uint32_t one = 0x3F80u;  // bf16 1.0: the identity's A fragment (k = 4b + e, row c)
+  const uint32_t ilo = d == 0 ? one : (d == 1 ? one << 16 : 0u), ihi = d == 2 ? one : (d == 3 ? one << 16 : 0u);
+  for (int rb = blockIdx.x; rb < nb; rb += gridDim.x) {
+    fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint4* blk = qt + (size_t)rb * G * 64;
+    const uint32_t* srow = sz + (size_t)(rb * 16 + c) * G;
+    for (int g = wave; g < G; g += TW_NW) unit_dot(blk[(size_t)g * 64 + lane], srow[g], xs, g, ilo, ihi, acc);
+    if (lane < 16) part[wave * 16 + lane] = acc[0];
+    __syncthreads();
+    if (tid < 16) {
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < TW_NW; ++w) v += part[w * 16 + tid];
+      y[rb * 16 + tid] = (uint16_t)f2bf(v);
+    }
+    __syncthreads();
+  }
+}
+
+// Dequantisation through the same MFMA steps, bf16 [N, K] in row order (for the bit-exactness
+// check against the reference's dequantisation): one wave per 1 KB unit.
+__global__ __launch_bounds__(256) void k_dequant_tiled(const uint4* __restrict__ qt, const uint32_t* __restrict__ sz,
+                                                       uint16_t* __restrict__ out, int n, int k) {
+  const int lane = threadIdx.x & 63;
+  const int64_t unit = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
+  const int G = k >> 7;
+  if (unit >= (int64_t)(n >> 4) * G) return;
+  const int g = (int)(unit % G), rb = (int)(unit / G);
+  const int b = lane >> 4, c = lane & 15, d = c - 4 * b;
+  const uint32_t one = 0x3F80u;
+  const uint32_t ilo = d == 0 ? one : (d == 1 ? one << 16 : 0u), ihi = d == 2 ? one : (d == 3 ? one << 16 : 0u);
+  const uint4 w = qt[unit * 64 + lane];
+  const GroupK kk = group_k(sz[(size_t)(rb * 16 + c) * G + g], d);
+  const uint32_t magic = 0x43004300u, mask = 0x000F000Fu;
+  uint32_t wa = w.x, wb = w.y, wc = w.z, wd = w.w;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    uint32_t& lo = t < 4 ? wa : wb;
+    uint32_t& hi = t < 4 ? wc : wd;
+    const uint32_t r0 = and_or(lo, mask, magic), r1 = and_or(hi, mask, magic);
+    lo >>= 4;
+    hi >>= 4;
+    uint32_t o0, o1;
+    tile_dq(r0, r1, kk, ilo, ihi, o0, o1);
+    // row c of the block, columns 16t + 4b .. +3 of group g
+    *reinterpret_cast<uint2*>(out + (size_t)(rb * 16 + c) * k + g * 128 + 16 * t + 4 * b) = make_uint2(o0, o1);
+  }
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+int fl_tile_int4(const uint32_t* q, uint32_t* qt, int32_t n, int32_t k, void* stream) {
+  if (!q || !qt || n <= 0 || k <= 0 || (n % 16) != 0 || (k % FL_GROUP) != 0) return FL_E_ARG;
+  const int64_t chunks = (int64_t)(n / 16) * (k / 128) * 64;
+  const int64_t blocks = (chunks + 255) / 256;
+  if (blocks > 0x7FFFFFFF) return FL_E_ARG;
+  hipLaunchKernelGGL(k_tile_int4, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), q,
+                     reinterpret_cast<uint4*>(qt), n, k);
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+}
+
+int fl_dequant_int4_tiled(const uint32_t* qt, const uint32_t* sz, uint16_t* out, int32_t n, int32_t k,
+                          void* stream) {
+  if (!qt || !sz || !out || n <= 0 || k <= 0 || (n % 16) != 0 || (k % FL_GROUP) != 0) return FL_E_ARG;
+  const int64_t units = (int64_t)(n / 16) * (k / 128);
+  const int64_t blocks = (units + 3) / 4;
+  if (blocks > 0x7FFFFFFF) return FL_E_ARG;
+  hipLaunchKernelGGL(k_dequant_tiled, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint4*>(qt), sz, out, n, k);
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+}
+
+int fl_gemv_int4_tiled(const uint32_t* qt, const uint32_t* sz, const uint16_t* x, uint16_t* y, int32_t n,
+                       int32_t k, void* stream) {
+  if (!qt || !sz || !x || !y || n <= 0 || k <= 0 || (n % 16) != 0 || (k % FL_GROUP) != 0 || k > 16384)
+    return FL_E_ARG;
+  const size_t shm = (size_t)k * 2 + TW_NW * 16 * 4;
+  hipLaunchKernelGGL(k_gemv_tiled, dim3(n / 16), dim3(TW_NW * 64), shm, as_stream(stream),
+                     reinterpret_cast<const uint4*>(qt), sz, x, y, n, k);
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+}
+
+}  // extern "C"

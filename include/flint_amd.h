@@ -93,6 +93,25 @@ int fl_gemv_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint1
 int fl_gemm_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint16_t* y,
                  int32_t m, int32_t n, int32_t k, void* stream);
 
+/* ---- tiled layout: the exact dequantisation on the matrix cores ------------------------- */
+
+/* The same int4 values in the tiled layout the matrix-core GEMV reads (N % 16 == 0): per block
+ * of 16 rows and 128-column group, 1 KB; 16 bytes per lane l = 16b + c of a wave: words 0 / 1 hold
+ * rows 4b, 4b+1 at columns c + 16t (t = 0..3 / 4..7: row 4b at bits 4(t%4), row 4b+1 at 16 + 4(t%4)),
+ * words 2 / 3 the same for rows 4b+2, 4b+3. qt: uint32 [N/16, K/128, 64, 4]; sz is unchanged.
+ * No counterpart in the reference (its tinygemm tile layout, quantize.py:359-364, serves the
+ * same purpose for its CUDA kernel). */
+int fl_tile_int4(const uint32_t* q, uint32_t* qt, int32_t n, int32_t k, void* stream);
+/* Bit-exact dequantisation of a tiled matrix to bf16 [N,K] (row order) through the GEMV's own
+ * matrix-core steps. Replaces reference engine/quantize.py:138-162 for the tiled layout. */
+int fl_dequant_int4_tiled(const uint32_t* qt, const uint32_t* sz, uint16_t* out, int32_t n, int32_t k,
+                          void* stream);
+/* y[N] = bf16( sum_k x[k] * dq[n,k] ), M = 1, from the tiled layout: both exact dequantisation
+ * steps and the dot on the matrix cores. Replaces reference engine/quantize.py:517-525
+ * WeightOnlyInt4Linear.forward at M = 1 and kernels/int4_gemv.cu:383-424 int4_gemv_v. */
+int fl_gemv_int4_tiled(const uint32_t* qt, const uint32_t* sz, const uint16_t* x, uint16_t* y, int32_t n,
+                       int32_t k, void* stream);
+
 /* ---- decode state --------------------------------------------------------------------- */
 
 /* Binds a caller-owned bf16 KV cache (k_cache, v_cache: [NL, NKV, max_seq, 64] each, device)

@@ -22,8 +22,8 @@ import pytest
 import torch
 
 from flint_amd.synth import ModelArgs, synth_weights
-from tests.helpers import (log, logit_bar, logit_stats, near_tie, oracle_pair, record, row_bars,
-                           top2_margin, ulp_stats)
+from tests.helpers import (bf16_ulp, log, logit_bar, logit_stats, near_tie, oracle_pair, record,
+                           row_bars, top2_margin, ulp_stats)
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(600)]
 
@@ -252,34 +252,54 @@ def _layer_engine(eng, l, holder):
     return e1
 
 
-def _slip_layer(orc, l, x, pos):
-    """Layer l of the oracle with ONE planted rounding-point mistake (test-only): the SwiGLU
-    product formed in fp32 and rounded once instead of bf16(bf16(silu(g)) * u)
-    (engine/model.py:227-228). Returns the layer's SwiGLU output and output."""
+def _stages(orc, l, x, n, ker, impl, slip=False):
+    """The oracle's values of layer l's stages at cache position n, each stage computed from the
+    kernel's own input to that stage (so a difference is that stage's, not one carried in from an
+    earlier stage: a 1-ulp flip in 1% of the attention output already moves about 30% of the SwiGLU
+    outputs by an ulp through the O projection, the norm and the gate/up sums):
+      attn: attention with the kernel's q over the cache rows [0, n) and the kernel's new k / v row;
+      act:  h1 = x + O(kernel attention), norm, gate / up, SwiGLU;
+      out:  h1 (as above) + down(kernel SwiGLU output).
+    impl is one of the oracle's implementations (oracle.model.IMPLS); slip plants ONE rounding
+    mistake (test-only): the SwiGLU product formed in fp32 and rounded once instead of
+    bf16(bf16(silu(g)) * u) (engine/model.py:227-228)."""
     import torch.nn.functional as F
-    from oracle.model import rms_norm
-    a, w, lin = orc.args, orc.w[l], orc.linear
-    h1 = x + orc.layer_attention(l, x, pos) * a.residual_multiplier
+    from oracle.model import IMPLS, attention, rms_norm
+    lin, softmax, silu = IMPLS[impl]
+    a, w = orc.args, orc.w[l]
+    NH, NKV = a.n_head, a.n_local_heads
+    kc = torch.cat([orc.k_cache[l, :, :n], ker["k"].view(NKV, 1, 64)], dim=1)
+    vc = torch.cat([orc.v_cache[l, :, :n], ker["v"].view(NKV, 1, 64)], dim=1)
+    attn = attention(ker["q"].view(NH, 64), kc, vc, torch.ones(n + 1, dtype=torch.bool), a.attn_scale,
+                     softmax).view(1, -1)
+    h1 = x + lin(ker["attn"].view(1, -1), w["wo"]) * a.residual_multiplier
     hn = rms_norm(h1, w["ffn_norm"], a.norm_eps)
-    act = (F.silu(lin(hn, w["w1"]).float()) * lin(hn, w["w3"]).float()).to(torch.bfloat16)
-    return act, h1 + lin(act, w["w2"]) * a.residual_multiplier
+    g, u = lin(hn, w["w1"]), lin(hn, w["w3"])
+    act = (F.silu(g.float()) * u.float()).to(torch.bfloat16) if slip else silu(g) * u
+    out = h1 + lin(ker["act"].view(1, -1), w["w2"]) * a.residual_multiplier
+    return {"attn": attn, "act": act, "out": out}
 
 
-# bars of one layer's values against the oracle's (every q/k/v, attention, SwiGLU and output
-# value of the layer): the fraction not bit-identical at most three times the oracle's second
-# implementation's on the same input plus 0.2% (v_dot2_f32_bf16's rare misrounding and the
-# hardware exp2 / rcp), at least 99.5% within one ulp of their own magnitude, and every value
-# within two ulps of the vector's largest
-MISMATCH_X, MISMATCH_ABS, IN1_MIN, TOP_MAX = 3.0, 2e-3, 0.995, 2.0
+# Bars of one layer's stage outputs against the oracle's on the same stage inputs: the fraction
+# not bit-identical at most three times the oracle's second implementation's (per-group summation
+# order, exp2-based softmax / SiLU) on the same inputs plus 0.3% or four values, whichever is more
+# (v_dot2_f32_bf16's rare misrounding, the hardware exp2 / rcp; k and v have only 512 values), at
+# least 99.5% within one ulp of their own magnitude, and every value within two ulps of the
+# vector's largest. The whole layer from the same input (every stage's differences carried
+# through) is logged beside the oracle's second implementation, not held to a bar: where the layer's
+# update outweighs its input (layer 0, whose input is the N(0, 0.02) embedding), one flipped
+# attention value moves a third of the outputs by an ulp, in either implementation.
+MISMATCH_X, MISMATCH_ABS, MISMATCH_MIN_VALUES, IN1_MIN, TOP_MAX = 3.0, 3e-3, 4, 0.995, 2.0
 
 
 def _per_layer(full, n, seed, label):
     """Teacher-forced check of every layer at cache position n: the oracle runs the whole model
     (recording each layer's input and values); each layer of the engine then runs alone from the
-    oracle's input to that layer, over the same cache rows, through fl_decode_hidden, and its q, k,
-    v (after RoPE), attention output, SwiGLU output and written-back residual are compared with the
-    oracle's layer. The reference checks its attention and MLP blocks in isolation the same way
-    (bench/megakernel_attn_test.py:64-67, bench/megakernel_test.py:52-55)."""
+    oracle's input to that layer, over the same cache rows, through fl_decode_hidden, and each of
+    its stages (q, k, v after RoPE; attention; O + residual + norm + gate/up + SwiGLU; down +
+    residual) is compared with the oracle's stage on the kernel's own inputs to it. The reference
+    checks its attention and MLP blocks in isolation the same way (bench/megakernel_attn_test.py:
+    64-67, bench/megakernel_test.py:52-55)."""
     args, eng, orc = full
     prompt = _prefill_both(eng, orc, n, seed=seed)
     tok = torch.tensor([int(prompt[n])])
@@ -289,8 +309,8 @@ def _per_layer(full, n, seed, label):
         ref_tr = orc.trace
     finally:
         orc.trace = None
-    NH, NKV, D = args.n_head, args.n_local_heads, args.dim
-    holder, worst = {}, {}
+    NH, NKV = args.n_head, args.n_local_heads
+    holder, worst, fails = {}, {}, []
     slip_caught = 0
     try:
         for l in range(args.n_layer):
@@ -307,34 +327,47 @@ def _per_layer(full, n, seed, label):
                    "attn": act["attn"].cpu(), "act": act["act"].cpu(), "out": h.cpu()}
             assert torch.equal(ker["k"].view(NKV, 64), e1.k_cache[0, :, n].cpu())
             assert torch.equal(ker["v"].view(NKV, 64), e1.v_cache[0, :, n].cpu())
-            # the oracle's second implementation of the same layer on the same input and cache
+            # stage A (q, k, v) from the layer input: the oracle's own run, and its second
+            # implementation on the same input
             orc.set_order("g128+exp2")
             orc.trace = []
             try:
                 orc.layer(l, x, n)
-                alt = orc.trace[0]
+                alt_a = orc.trace[0]
             finally:
                 orc.trace = None
                 orc.set_order("torch")
-            slip_act, slip_out = _slip_layer(orc, l, x, n)
-            ref = ref_tr[l]
+            ref = {k: ref_tr[l][k] for k in ("q", "k", "v")}
+            alt = {k: alt_a[k] for k in ("q", "k", "v")}
+            ref.update(_stages(orc, l, x, n, ker, "torch"))
+            alt.update(_stages(orc, l, x, n, ker, "g128+exp2"))
+            slip = _stages(orc, l, x, n, ker, "torch", slip=True)["act"]
             line = f"{label} layer {l:2d}:"
             for name in ("q", "k", "v", "attn", "act", "out"):
                 sk, sa = ulp_stats(ker[name], ref[name]), ulp_stats(alt[name], ref[name])
-                line += (f" {name} {1 - sk['same']:.2%}/{1 - sa['same']:.2%} in1 {sk['in1']:.2%}"
+                bar = MISMATCH_X * (1 - sa["same"]) + max(MISMATCH_ABS, MISMATCH_MIN_VALUES / ker[name].numel())
+                line += (f" {name} {1 - sk['same']:.2%}/{1 - sa['same']:.2%}(bar {bar:.2%}) in1 {sk['in1']:.2%}"
                          f" top {sk['top']:.1f}")
-                bar = MISMATCH_X * (1 - sa["same"]) + MISMATCH_ABS
                 w = worst.setdefault(name, [0.0, 0.0, 1.0, 0.0])
                 w[0] = max(w[0], 1 - sk["same"])
                 w[1] = max(w[1], 1 - sa["same"])
                 w[2] = min(w[2], sk["in1"])
                 w[3] = max(w[3], sk["top"])
-                assert 1 - sk["same"] <= bar, (label, l, name, sk, sa)
-                assert sk["in1"] >= IN1_MIN and sk["top"] <= TOP_MAX, (label, l, name, sk)
+                if not (1 - sk["same"] <= bar and sk["in1"] >= IN1_MIN and sk["top"] <= TOP_MAX):
+                    fails.append((l, name, sk, sa))
                 if name == "act":
-                    ss = ulp_stats(slip_act, ref["act"])
+                    ss = ulp_stats(slip, ref["act"])
                     slip_caught += (1 - ss["same"]) > bar
                     line += f" [planted slip {1 - ss['same']:.2%}]"
+            # the whole layer from the same input, differences of every stage carried through
+            # (logged: config 0's figures, kernel and the oracle's second implementation)
+            def in2(e, r):
+                d = (e.float() - r.float()).abs().reshape(-1)
+                own = bf16_ulp(torch.maximum(e.float().abs(), r.float().abs()).reshape(-1))
+                return float((d <= 2 * own).float().mean())
+            wk, wa = ulp_stats(ker["out"], ref_tr[l]["out"]), ulp_stats(alt_a["out"], ref_tr[l]["out"])
+            line += (f" | whole layer out: kernel {1 - wk['same']:.2%} differ, {in2(ker['out'], ref_tr[l]['out']):.2%}"
+                     f" within 2 ulps; oracle 2nd impl {1 - wa['same']:.2%}, {in2(alt_a['out'], ref_tr[l]['out']):.2%}")
             record(line)
     finally:
         if "e" in holder:
@@ -343,6 +376,7 @@ def _per_layer(full, n, seed, label):
            f"bit-identical / kernel within 1 ulp / kernel max ulps of the largest): " +
            ", ".join(f"{k} {v[0]:.2%}/{v[1]:.2%}/{v[2]:.2%}/{v[3]:.1f}" for k, v in worst.items()) +
            f"; a planted SwiGLU rounding slip fails the act bar in {slip_caught} of {args.n_layer} layers")
+    assert not fails, fails[:5]
     assert slip_caught == args.n_layer
 
 

@@ -182,3 +182,58 @@ def test_scales_and_zeros_gptfast_layout(dev):
     for g, r in ((0, 0), (3, 17), (7, n - 1)):
         assert got[g, r, 0].view(torch.int16) == so[r, g].view(torch.int16)
         assert got[g, r, 1].view(torch.int16) == zo[r, g].view(torch.int16)
+
+
+TILED_SHAPES = [(3584, 2560), (16384, 2560), (2560, 8192), (16, 128), (48, 384)]
+
+
+def _tiled(q, n, k):
+    from flint_amd import _lib
+    qt = torch.empty(n // 16, k // 128, 64, 4, dtype=torch.int32, device=q.device)
+    _lib.call("fl_tile_int4", _lib.ptr(q), _lib.ptr(qt), n, k, _lib.stream_ptr())
+    return qt
+
+
+@pytest.mark.parametrize("n,k", TILED_SHAPES)
+def test_tiled_dequant_bit_exact(dev, n, k):
+    """The matrix-core dequantisation (fl_tile_int4 + fl_dequant_int4_tiled: D1 = (128+q) diag(s)
+    - 136 s, round, D2 = I a + z, round) gives gpt-fast's bf16(bf16((q-8) s) + z) bit for bit,
+    edge groups included (constant group, outlier, two-valued group)."""
+    from flint_amd import _lib
+    from flint_amd.quantize import quantize_int4
+    from oracle import quant
+    w = _weights(n, k, 21, "edge")
+    log(f"tiled dequant n={n} k={k}")
+    q, sz = quantize_int4(w.to(dev))
+    qt = _tiled(q, n, k)
+    out = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
+    _lib.call("fl_dequant_int4_tiled", _lib.ptr(qt), _lib.ptr(sz), _lib.ptr(out), n, k, _lib.stream_ptr())
+    ref = quant.dq_linear_weight(w)
+    assert torch.equal(out.cpu().view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("n,k", TILED_SHAPES)
+def test_tiled_gemv_vs_fp64(dev, n, k):
+    """The matrix-core GEMV within the fp32-accumulation bound of the exact product, and equal to
+    the row-layout GEMV up to fp32 summation order."""
+    from flint_amd import _lib
+    from flint_amd.quantize import quantize_int4, gemv_int4
+    from oracle import quant
+    w = _weights(n, k, 22)
+    x = torch.randn(k, generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)
+    log(f"tiled gemv n={n} k={k}")
+    q, sz = quantize_int4(w.to(dev))
+    qt = _tiled(q, n, k)
+    y = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    _lib.call("fl_gemv_int4_tiled", _lib.ptr(qt), _lib.ptr(sz), _lib.ptr(x.to(dev)), _lib.ptr(y), n, k,
+              _lib.stream_ptr())
+    y = y.cpu()
+    dq = quant.dq_linear_weight(w).double()
+    ref = dq @ x.double()
+    bound = k * 2.0 ** -24 * (dq.abs() @ x.double().abs()) + ref.abs() * 2.0 ** -8 + 1e-30
+    err = (y.double() - ref).abs()
+    assert bool((err <= bound).all()), float((err / bound).max())
+    mism = (y != ref.float().to(torch.bfloat16)).float().mean().item()
+    yr = gemv_int4(q, sz, x.to(dev)).cpu()
+    log(f"  bf16 mismatch vs fp64-rounded {mism:.2e}, vs row-layout GEMV {(y != yr).float().mean().item():.2e}")
+    assert mism < 2e-3
