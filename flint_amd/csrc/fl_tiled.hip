@@ -36,13 +36,20 @@ __device__ __forceinline__ fl_s16x4 s4(uint32_t lo, uint32_t hi) {
 __device__ __forceinline__ fl_bf16x8 b8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   return __builtin_bit_cast(fl_bf16x8, make_uint4(a, b, c, d));
 }
-// (w & mask) | magic in one instruction (the mask in an SGPR, the magic in a VGPR: gfx950's
-// three-operand encoding takes no literal)
-__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t magic) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(magic));
-  return r;
+// (w & mask) | magic: with both constants in registers (hidden from constant folding: gfx950's
+// three-operand encoding takes no literal) the compiler emits one v_and_or_b32 and still sees the
+// instruction, so it keeps the wait states that matrix-core results around it need (inline asm
+// hides those from it: an and-or written as asm here read registers an MFMA was still writing)
+struct AndOrK {
+  uint32_t mask, magic;
+};
+__device__ __forceinline__ AndOrK and_or_k() {
+  uint32_t mask = 0x000F000Fu, magic = 0x43004300u;
+  asm volatile("" : "+s"(mask));
+  asm volatile("" : "+v"(magic));
+  return {mask, magic};
 }
+__device__ __forceinline__ uint32_t and_or(uint32_t w, const AndOrK& k) { return (w & k.mask) | k.magic; }
 
 // row layout -> tiled layout: one thread per 16-byte tiled chunk
 __global__ __launch_bounds__(256) void k_tile_int4(const uint32_t* __restrict__ q, uint4* __restrict__ qt,
@@ -107,7 +114,7 @@ __device__ __forceinline__ void unit_dot(uint4 w, uint32_t szw, const uint16_t* 
                                          uint32_t ihi, fl_f32x4& acc) {
   const int lane = threadIdx.x & 63, b = lane >> 4, c = lane & 15;
   const GroupK k = group_k(szw, c - 4 * b);
-  const uint32_t magic = 0x43004300u, mask = 0x000F000Fu;
+  const AndOrK ao = and_or_k();
   uint32_t wa = w.x, wb = w.y, wc = w.z, wd = w.w;
 #pragma unroll
   for (int tp = 0; tp < 4; ++tp) {  // tiles 2tp, 2tp + 1: one 16x16x32 dot MFMA per pair
@@ -117,7 +124,7 @@ __device__ __forceinline__ void unit_dot(uint4 w, uint32_t szw, const uint16_t* 
       const int t = 2 * tp + h;
       uint32_t& lo = t < 4 ? wa : wb;
       uint32_t& hi = t < 4 ? wc : wd;
-      const uint32_t r0 = and_or(lo, mask, magic), r1 = and_or(hi, mask, magic);
+      const uint32_t r0 = and_or(lo, ao), r1 = and_or(hi, ao);
       lo >>= 4;
       hi >>= 4;
       tile_dq(r0, r1, k, ilo, ihi, q0[h], q1[h]);
@@ -178,13 +185,13 @@ __global__ __launch_bounds__(256) void k_dequant_tiled(const uint4* __restrict__
   const uint32_t ilo = d == 0 ? one : (d == 1 ? one << 16 : 0u), ihi = d == 2 ? one : (d == 3 ? one << 16 : 0u);
   const uint4 w = qt[unit * 64 + lane];
   const GroupK kk = group_k(sz[(size_t)(rb * 16 + c) * G + g], d);
-  const uint32_t magic = 0x43004300u, mask = 0x000F000Fu;
+  const AndOrK ao = and_or_k();
   uint32_t wa = w.x, wb = w.y, wc = w.z, wd = w.w;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     uint32_t& lo = t < 4 ? wa : wb;
     uint32_t& hi = t < 4 ? wc : wd;
-    const uint32_t r0 = and_or(lo, mask, magic), r1 = and_or(hi, mask, magic);
+    const uint32_t r0 = and_or(lo, ao), r1 = and_or(hi, ao);
     lo >>= 4;
     hi >>= 4;
     uint32_t o0, o1;

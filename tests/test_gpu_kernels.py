@@ -209,7 +209,17 @@ def test_tiled_dequant_bit_exact(dev, n, k):
     out = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
     _lib.call("fl_dequant_int4_tiled", _lib.ptr(qt), _lib.ptr(sz), _lib.ptr(out), n, k, _lib.stream_ptr())
     ref = quant.dq_linear_weight(w)
-    assert torch.equal(out.cpu().view(torch.int16), ref.view(torch.int16))
+    got = out.cpu()
+    bad = (got.view(torch.int16) != ref.view(torch.int16))
+    if bool(bad.any()):
+        idx = bad.nonzero()[:12].tolist()
+        rows = bad.nonzero()[:, 0] % 16
+        cols = bad.nonzero()[:, 1] % 128
+        log(f"  {int(bad.sum())} of {bad.numel()} differ; rows mod 16 {torch.bincount(rows, minlength=16).tolist()}; "
+            f"cols mod 16 {torch.bincount(cols % 16, minlength=16).tolist()}; cols // 16 {torch.bincount(cols // 16, minlength=8).tolist()}")
+        for r, c in idx:
+            log(f"  [{r},{c}] got {float(got[r, c])} want {float(ref[r, c])}")
+    assert not bool(bad.any())
 
 
 @pytest.mark.parametrize("n,k", TILED_SHAPES)
