@@ -343,7 +343,45 @@ def gemv_sweep(args, dev, sets=40, rounds=3):
         tiled[name] = {"us": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
                        "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     del T
-    return {"sets_per_shape": sets, "rotation_bytes": rot, "shapes": out, "tiled_mfma": tiled}
+    return {"sets_per_shape": sets, "rotation_bytes": rot, "shapes": out, "tiled_mfma": tiled,
+            "steady_state": gemv_steady(dev)}
+
+
+def gemv_steady(dev, reps=20):
+    """Streaming rate of both M = 1 GEMVs once a call is long enough that its start-up and tail do
+    not count: one N = 131072 x K = 2560 and one N = 40960 x K = 8192 matrix (about 170 MB each,
+    two copies alternated so every call reads HBM), HIP events around `reps` back-to-back calls."""
+    from flint_amd import _lib
+    sp = _lib.stream_ptr()
+    res = {}
+    for n, k in ((131072, 2560), (40960, 8192)):
+        g = torch.Generator(device=dev).manual_seed(3)
+        q = torch.randint(-2 ** 31, 2 ** 31 - 1, (2, n, k // 8), generator=g, device=dev, dtype=torch.int32)
+        sz = torch.full((2, n, k // 128), 0x3A83, dtype=torch.int32, device=dev)
+        qt = torch.empty(2, n // 16, k // 128, 64, 4, dtype=torch.int32, device=dev)
+        for i in range(2):
+            _lib.call("fl_tile_int4", _lib.ptr(q[i]), _lib.ptr(qt[i]), n, k, sp)
+        x = torch.randn(k, generator=g, device=dev).to(torch.bfloat16)
+        y = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        nbytes = n * k // 2 + n * (k // 128) * 4
+        for name, fn in (("stream", lambda i: _lib.call("fl_gemv_int4", _lib.ptr(q[i]), _lib.ptr(sz[i]), _lib.ptr(x),
+                                                        _lib.ptr(y), n, k, sp)),
+                         ("tiled", lambda i: _lib.call("fl_gemv_int4_tiled", _lib.ptr(qt[i]), _lib.ptr(sz[i]),
+                                                       _lib.ptr(x), _lib.ptr(y), n, k, sp))):
+            for i in range(4):
+                fn(i % 2)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(reps):
+                fn(i % 2)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / reps
+            res[f"{name}_{n}x{k}"] = {"us": round(us, 1), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                      "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del q, sz, qt
+    return res
 
 
 def long_context(model, args, dev, ctx=8192, steps=128):
@@ -423,6 +461,18 @@ def sampling_latency(args, dev, reps=50):
     return res
 
 
+def copy_probe(dev, mb):
+    """One device-to-device copy of `mb` MiB: the known-size kernel that calibrates rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters."""
+    n = mb * (1 << 20)
+    src = torch.ones(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy probe: {n} bytes device-to-device")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -465,6 +515,8 @@ def main():
     if a.gemv_only:
         gemv = gemv_sweep(args, dev)
         log(f"config 1 (fl_gemv_int4, {gemv['rotation_bytes'] / 1e9:.2f} GB rotation): {gemv}")
+        if a.copy_probe_mb > 0:
+            copy_probe(dev, a.copy_probe_mb)
         print(json.dumps({"gemv_sweep": gemv}), flush=True)
         return
     log(f"synthesising {a.config} weights on the GPU")
@@ -562,14 +614,7 @@ def main():
         log(f"hand-off of a {handoff['words']}-word tagged vector: {handoff}")
 
     if a.copy_probe_mb > 0:
-        n = a.copy_probe_mb * (1 << 20)
-        src = torch.ones(n, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"copy probe: {n} bytes device-to-device")
-        del src, dst
+        copy_probe(dev, a.copy_probe_mb)
 
     cpu = None
     if not a.no_cpu_baseline:

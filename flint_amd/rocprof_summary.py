@@ -7,6 +7,9 @@
     python -m flint_amd.rocprof_summary --pmc <dir> [<dir> ...] --kernel k_decode --last N
         from `rocprofv3 --pmc ...` runs: every counter's mean per dispatch over the kernel's last N
         dispatches, and the same counters for the last device copy (copyBuffer) if there is one;
+    python -m flint_amd.rocprof_summary --gemv <trace dir> <SQ pmc dir> <fetch dir> <write dir> --copy-bytes B
+        the config-1 GEMV sweep (bench.py --gemv-only --copy-probe-mb M): per kernel variant and
+        shape the kernel time, algorithmic and HBM bytes, VALU issue and wait shares;
     python -m flint_amd.rocprof_summary --traffic <fetch dir> <write dir> --copy-bytes B ...
         from two `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of a bench command that
         ends with a device-to-device copy of B bytes: HBM bytes per dispatch of the kernel, each
@@ -134,6 +137,85 @@ def traffic(fetch_dir, write_dir, kernel, last, copy_bytes, config, copy_kernel=
     return "\n".join(out)
 
 
+def _gemv_label(name, grid, seen):
+    """(variant, shape) of a config-1 GEMV dispatch from bench.gemv_sweep: the streamed row-layout
+    kernel (template <4, 5>: K 2560; <6, 4>: K 8192) and the tiled matrix-core kernel, told apart
+    by kernel name and grid (the tiled O and down share a grid and alternate, O first)."""
+    if "k_gemv_stream<4, 5>" in name:
+        return "stream", {57344: "qkv", 40960: "o", 131072: "gate_up"}.get(grid)
+    if "k_gemv_stream<6, 4>" in name:
+        return "stream", "down"
+    if "k_gemv_tiled" in name:
+        if grid == 40960:
+            seen["t40960"] = seen.get("t40960", 0) + 1
+            return "tiled", "o" if seen["t40960"] % 2 == 1 else "down"
+        return "tiled", {57344: "qkv", 262144: "gate_up"}.get(grid)
+    return None, None
+
+
+GEMV_SHAPES = {"qkv": (3584, 2560), "o": (2560, 2560), "gate_up": (16384, 2560), "down": (2560, 8192)}
+
+
+def gemv(trace_dir, pmc_dir, fetch_dir, write_dir, copy_bytes, skip_frac=0.25):
+    """Config-1 GEMV table: per kernel variant and shape, the kernel time (trace), the algorithmic
+    and HBM (FETCH + WRITE, copy-calibrated) bytes, and the PMC counters' story (VALU issue share,
+    waiting share). The first skip_frac of each series (the sweep's warm-up pass) is left out."""
+    out = []
+    series = {}
+    with open(_find(trace_dir, "kernel_trace.csv")) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    seen = {}
+    for r in rows:
+        v, shp = _gemv_label(r["Kernel_Name"], int(r["Grid_Size_X"]), seen)
+        if v and shp:
+            series.setdefault((v, shp), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+
+    def counters(d):
+        _, crow = _counter_rows(d)
+        per, meta = {}, {}
+        for r in crow:
+            k = int(r["Dispatch_Id"])
+            meta[k] = (r["Kernel_Name"], int(r["Grid_Size"]))
+            per.setdefault(k, {})[r["Counter_Name"]] = per.setdefault(k, {}).get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        res, sn = {}, {}
+        for k in sorted(per):
+            v, shp = _gemv_label(meta[k][0], meta[k][1], sn)
+            if v and shp:
+                res.setdefault((v, shp), []).append(per[k])
+        copy = [per[k] for k in sorted(per) if "copyBuffer" in meta[k][0]]
+        return res, (copy[-1] if copy else None)
+
+    def mean(lst, key):
+        lst = lst[int(len(lst) * skip_frac):]
+        return sum(x[key] for x in lst) / len(lst)
+    sq, _ = counters(pmc_dir)
+    fe, fcopy = counters(fetch_dir)
+    wr, wcopy = counters(write_dir)
+    fscale = fcopy["FETCH_SIZE"] * 1024.0 / copy_bytes
+    wscale = wcopy["WRITE_SIZE"] * 1024.0 / copy_bytes
+    out.append(f"FETCH_SIZE reads {fscale:.4f}x and WRITE_SIZE {wscale:.4f}x the bytes of a {copy_bytes}-byte "
+               f"device copy (the scale applied below)")
+    out.append(f"{'variant':8s} {'shape':8s} {'kernel_us':>9s} {'alg_MB':>8s} {'hbm_MB':>8s} {'GB/s':>7s} {'frac':>6s} "
+               f"{'VALU%':>6s} {'wait%':>6s} {'VALU/wt':>7s}")
+    for (v, shp) in sorted(series, key=lambda t: (t[0], list(GEMV_SHAPES).index(t[1]))):
+        n, k = GEMV_SHAPES[shp]
+        t = series[(v, shp)]
+        t = t[int(len(t) * skip_frac):]
+        us = sum(t) / len(t)
+        alg = n * k // 2 + n * (k // 128) * 4 + 2 * k + 2 * n
+        hbm = (mean(fe[(v, shp)], "FETCH_SIZE") * 1024.0 / fscale + mean(wr[(v, shp)], "WRITE_SIZE") * 1024.0 / wscale)
+        c = sq[(v, shp)]
+        waves = mean(c, "SQ_WAVES")
+        wave_cyc = mean(c, "SQ_WAVE_CYCLES") / waves
+        valu = mean(c, "SQ_ACTIVE_INST_VALU") / waves / wave_cyc   # VALU busy share of a wave's life
+        wait = mean(c, "SQ_WAIT_INST_ANY") / waves / wave_cyc
+        per_w = mean(c, "SQ_INSTS_VALU") * 64.0 / (n * k)          # VALU lane-ops per weight
+        gbs = alg / (us * 1e-6) / 1e9
+        out.append(f"{v:8s} {shp:8s} {us:9.2f} {alg / 1e6:8.2f} {hbm / 1e6:8.2f} {gbs:7.0f} {gbs / 8000.0:6.3f} "
+                   f"{100 * valu:6.1f} {100 * wait:6.1f} {per_w:7.2f}")
+    return "\n".join(out)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("dir", nargs="*")
@@ -145,8 +227,12 @@ def main(argv=None):
     ap.add_argument("--pmc", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0)
     ap.add_argument("--config", default="")
+    ap.add_argument("--gemv", action="store_true",
+                    help="config-1 GEMV table from <trace dir> <SQ pmc dir> <FETCH dir> <WRITE dir>")
     a = ap.parse_args(argv)
-    if a.pmc:
+    if a.gemv:
+        print(gemv(a.dir[0], a.dir[1], a.dir[2], a.dir[3], a.copy_bytes))
+    elif a.pmc:
         print(pmc(a.dir, a.kernel, a.last))
     elif a.traffic:
         print(traffic(a.dir[0], a.dir[1], a.kernel, a.last, a.copy_bytes, a.config))
