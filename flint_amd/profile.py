@@ -37,7 +37,7 @@ def disable(model):
     _lib.call("fl_state_profile", model._state, None, 0, None)
 
 
-def analyse(buf, grid, slots, n_layer):
+def analyse(buf, grid, slots, n_layer, nh=0, nkv=0):
     t = buf[: grid * slots].view(grid, slots).double().cpu() * TICK_US
     t = t - t[:, :1].min()
     L = n_layer
@@ -90,6 +90,33 @@ def analyse(buf, grid, slots, n_layer):
             "last_consumer_us": float(torch.nan_to_num(rel, nan=-1e30).max(0).values.mean()),
         }
     out["handoffs"] = trans
+    # per workgroup class (no attention unit / attention units by key slice: unit u of slice
+    # (u / NKV) % nsl, nsl = attention workgroups / NH): how far each class's phase ends lag the
+    # median workgroup's, and which class holds the last producer of each phase. A workgroup
+    # ran an attention unit in most layers when its key loop took time (workgroups without a
+    # unit stamp the loop's start and end back to back).
+    att_wg = ((lay[..., 3] - lay[..., 2]) > 0.2).double().mean(1) > 0.5
+    n_att = int(att_wg.sum())
+    cls = torch.full((grid,), -1, dtype=torch.long)
+    if n_att and nh and nkv and n_att % nh == 0:
+        nsl = n_att // nh
+        u = torch.arange(grid)
+        cls = torch.where(att_wg, (u // nkv) % nsl, torch.full_like(u, -1))
+    names = {-1: "no attention"}
+    names.update({c: f"attention slice {c}" for c in range(int(cls.max()) + 1)})
+    lag = {}
+    for pname, k in (("qkv", 1), ("attention", 5), ("o", 7), ("gateup", 9), ("down", 11)):
+        end = lay[..., k]                                   # [grid, L]
+        rel = end - end.median(0).values                    # lag behind the median workgroup
+        last = end.argmax(0)                                # [L] the last workgroup per layer
+        row = {}
+        for c, nm in names.items():
+            sel = cls == c
+            if bool(sel.any()):
+                row[nm] = {"mean_lag_us": float(rel[sel].mean()),
+                           "last_share": float((cls[last] == c).double().mean())}
+        lag[pname] = row
+    out["class_lag"] = lag
     # critical spans: between the last workgroup to finish one phase and the last to finish the
     # next (they add up to the layer's critical path)
     ends = [prev_done.max(0).values] + [lay[..., k].max(0).values for k in (1, 5, 7, 9, 11)]
@@ -124,6 +151,12 @@ def format_report(res, n_layer, label):
     for name, d in res["handoffs"].items():
         out.append(f"{name:20s} {d['producer_spread_us']:16.2f} {d['first_consumer_us']:15.2f} "
                    f"{d['median_consumer_us']:16.2f} {d['last_consumer_us']:14.2f}")
+    if res.get("class_lag"):
+        out += ["", "phase ends by workgroup class: mean lag behind the median workgroup (us) / share of "
+                    "layers in which the class holds the last workgroup"]
+        for pname, row in res["class_lag"].items():
+            out.append(f"  {pname:10s} " + "   ".join(f"{nm}: {d['mean_lag_us']:+.2f} / {d['last_share']:.0%}"
+                                                    for nm, d in row.items()))
     return "\n".join(out)
 
 
@@ -139,6 +172,7 @@ def main(argv=None):
     ap.add_argument("--config", default="flint-3b")
     ap.add_argument("--ctx", type=int, default=512)
     ap.add_argument("--steps", type=int, default=8)
+    ap.add_argument("--save", default=None, help="also save the raw timestamp buffer (torch.save) to this file")
     ap.add_argument("--verify", type=int, default=0,
                     help="profile fl_verify of this many chain tokens (at position ctx) instead of decode")
     a = ap.parse_args(argv)
@@ -163,7 +197,10 @@ def main(argv=None):
         label = f"{a.config} k_decode at ctx {a.ctx + a.steps - 1}, {grid} workgroups"
     model.check()
     disable(model)
-    res = analyse(buf, grid, slots, args.n_layer)
+    if a.save:
+        torch.save({"buf": buf.cpu(), "grid": grid, "slots": slots, "n_layer": args.n_layer,
+                    "n_head": args.n_head, "n_kv": args.n_local_heads}, a.save)
+    res = analyse(buf, grid, slots, args.n_layer, args.n_head, args.n_local_heads)
     print(format_report(res, args.n_layer, label))
     model.close()
 
