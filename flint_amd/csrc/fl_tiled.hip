@@ -171,6 +171,69 @@ __global__ __launch_bounds__(TW_NW * 64) void k_gemv_tiled(const uint4* __restri
   }
 }
 
+// The same GEMV with every unit a wave computes requested up front: one workgroup of NW waves
+// per 16-row block, wave w taking the block's groups w, w + NW, ... (at most UPW of them, all in
+// registers). x is requested first and the weights after it (loads complete in order, so the x
+// staging waits for x alone), then each unit is computed as its bytes arrive. In the loop kernel
+// above a wave requests a unit only after the previous one is done, so every unit pays a full
+// memory latency.
+template <int NW, int UPW>
+__global__ __launch_bounds__(NW * 64) void k_gemv_tiled_pf(const uint4* __restrict__ qt, const uint32_t* __restrict__ sz,
+                                                           const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                           int n, int k) {
+  // x slots: XPT per thread cover K <= NW * UPW * 128 (slots past K hold zeros, never read)
+  constexpr int XPT = UPW * 128 / 8 / 64;
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+  float* part = reinterpret_cast<float*>(smem + (size_t)XPT * NW * 64 * 16);  // [NW][16]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = k >> 7, nb = n >> 4, nx = k >> 3;
+  const auto xr = buf_rsrc(x, (uint32_t)k * 2u);
+  uint4 xv[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int v = tid + i * NW * 64;
+    xv[i] = buf_ld128(xr, v < nx ? (uint32_t)v * 16u : 0xFFFFFFF0u);
+  }
+  const int b = lane >> 4, c = lane & 15, d = c - 4 * b;
+  const uint32_t one = 0x3F80u;
+  const uint32_t ilo = d == 0 ? one : (d == 1 ? one << 16 : 0u), ihi = d == 2 ? one : (d == 3 ? one << 16 : 0u);
+  bool staged = false;
+  for (int rb = blockIdx.x; rb < nb; rb += gridDim.x) {
+    const auto wr = buf_rsrc(qt + (size_t)rb * G * 64, (uint32_t)G * 1024u);
+    const auto sr = buf_rsrc(sz + (size_t)rb * 16 * G, (uint32_t)G * 64u);
+    uint4 w[UPW];
+    uint32_t sw[UPW];
+#pragma unroll
+    for (int i = 0; i < UPW; ++i) {  // units past G: no memory access
+      const int g = wave + NW * i;
+      w[i] = buf_ld128(wr, g < G ? (uint32_t)(g * 64 + lane) * 16u : 0xFFFFFFF0u);
+      sw[i] = buf_ld32(sr, g < G ? (uint32_t)(c * G + g) * 4u : 0xFFFFFFF0u);
+    }
+    if (!staged) {  // every thread stores its slots (no store under a branch that waits for all loads)
+#pragma unroll
+      for (int i = 0; i < XPT; ++i) reinterpret_cast<uint4*>(xs)[tid + i * NW * 64] = xv[i];
+      __syncthreads();
+      staged = true;
+    }
+    fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < UPW; ++i) {
+      const int g = wave + NW * i;
+      if (g < G) unit_dot(w[i], sw[i], xs, g, ilo, ihi, acc);  // wave-uniform
+    }
+    if (lane < 16) part[wave * 16 + lane] = acc[0];
+    __syncthreads();
+    if (tid < 16) {
+      float v = 0.0f;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) v += part[ww * 16 + tid];
+      y[rb * 16 + tid] = (uint16_t)f2bf(v);
+    }
+    __syncthreads();
+  }
+}
+
 // Dequantisation through the same MFMA steps, bf16 [N, K] in row order (for the bit-exactness
 // check against the reference's dequantisation): one wave per 1 KB unit.
 __global__ __launch_bounds__(256) void k_dequant_tiled(const uint4* __restrict__ qt, const uint32_t* __restrict__ sz,
@@ -232,9 +295,20 @@ int fl_gemv_int4_tiled(const uint32_t* qt, const uint32_t* sz, const uint16_t* x
                        int32_t k, void* stream) {
   if (!qt || !sz || !x || !y || n <= 0 || k <= 0 || (n % 16) != 0 || (k % FL_GROUP) != 0 || k > 16384)
     return FL_E_ARG;
-  const size_t shm = (size_t)k * 2 + TW_NW * 16 * 4;
-  hipLaunchKernelGGL(k_gemv_tiled, dim3(n / 16), dim3(TW_NW * 64), shm, as_stream(stream),
-                     reinterpret_cast<const uint4*>(qt), sz, x, y, n, k);
+  const int G = k / FL_GROUP;
+  const uint4* q4 = reinterpret_cast<const uint4*>(qt);
+  // every unit of a wave in registers: 4 waves x 8 units (K <= 4096), 8 x 8 (K <= 8192); LDS: the
+  // x slots (2 per thread) and the waves' partial sums
+  if (G <= 32) {
+    hipLaunchKernelGGL((k_gemv_tiled_pf<4, 8>), dim3(n / 16), dim3(4 * 64), (size_t)2 * 4 * 64 * 16 + 4 * 16 * 4,
+                       as_stream(stream), q4, sz, x, y, n, k);
+  } else if (G <= 64) {
+    hipLaunchKernelGGL((k_gemv_tiled_pf<8, 8>), dim3(n / 16), dim3(8 * 64), (size_t)2 * 8 * 64 * 16 + 8 * 16 * 4,
+                       as_stream(stream), q4, sz, x, y, n, k);
+  } else {
+    hipLaunchKernelGGL(k_gemv_tiled, dim3(n / 16), dim3(TW_NW * 64), (size_t)k * 2 + TW_NW * 16 * 4,
+                       as_stream(stream), q4, sz, x, y, n, k);
+  }
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
 

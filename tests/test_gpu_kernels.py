@@ -184,7 +184,7 @@ def test_scales_and_zeros_gptfast_layout(dev):
         assert got[g, r, 1].view(torch.int16) == zo[r, g].view(torch.int16)
 
 
-TILED_SHAPES = [(3584, 2560), (16384, 2560), (2560, 8192), (16, 128), (48, 384)]
+TILED_SHAPES = [(3584, 2560), (16384, 2560), (2560, 8192), (16, 128), (48, 384), (32, 16384)]
 
 
 def _tiled(q, n, k):
