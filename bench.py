@@ -264,7 +264,7 @@ def spec_loop(model, args, prompt, ref, n, rounds=40):
     return res
 
 
-def gemv_sweep(args, dev, sets=40, rounds=3):
+def gemv_sweep(args, dev, sets=40, rounds=3, steady=True):
     """fl_gemv_int4 at M = 1 over the four per-layer shapes, 40 distinct weight
     sets per shape, called in layer order (QKV, O, gate/up, down of set 0, then set 1, ...) so the
     1.67 GB rotation exceeds the 256 MB Infinity Cache and every call reads its weights from HBM.
@@ -343,8 +343,10 @@ def gemv_sweep(args, dev, sets=40, rounds=3):
         tiled[name] = {"us": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
                        "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     del T
-    return {"sets_per_shape": sets, "rotation_bytes": rot, "shapes": out, "tiled_mfma": tiled,
-            "steady_state": gemv_steady(dev)}
+    res = {"sets_per_shape": sets, "rotation_bytes": rot, "shapes": out, "tiled_mfma": tiled}
+    if steady:
+        res["steady_state"] = gemv_steady(dev)
+    return res
 
 
 def gemv_steady(dev, reps=20):
@@ -493,6 +495,9 @@ def main():
                     help="skip the sampler timings (standalone and fused into the decode launch)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="run only the config-1 GEMV sweep and print its JSON (for profiling)")
+    ap.add_argument("--no-steady", action="store_true",
+                    help="leave the steady-state GEMV leg out of the config-1 sweep (profiling runs: its "
+                         "long calls would share the sweep's kernel names and grids)")
     ap.add_argument("--no-handoff", action="store_true",
                     help="skip the hand-off micro-benchmark (fl_probe_handoff)")
     ap.add_argument("--maps", default=None,
@@ -513,7 +518,7 @@ def main():
     dev = torch.device("cuda:0")
     args = ModelArgs.from_name(a.config)
     if a.gemv_only:
-        gemv = gemv_sweep(args, dev)
+        gemv = gemv_sweep(args, dev, steady=not a.no_steady)
         log(f"config 1 (fl_gemv_int4, {gemv['rotation_bytes'] / 1e9:.2f} GB rotation): {gemv}")
         if a.copy_probe_mb > 0:
             copy_probe(dev, a.copy_probe_mb)
@@ -599,7 +604,7 @@ def main():
 
     gemv = None
     if not a.no_gemv:
-        gemv = gemv_sweep(args, dev)
+        gemv = gemv_sweep(args, dev, steady=not a.no_steady)
         log(f"config 1 (fl_gemv_int4, {gemv['rotation_bytes'] / 1e9:.2f} GB rotation): {gemv['shapes']}")
 
     sampling = None

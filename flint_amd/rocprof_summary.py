@@ -8,7 +8,7 @@
         from `rocprofv3 --pmc ...` runs: every counter's mean per dispatch over the kernel's last N
         dispatches, and the same counters for the last device copy (copyBuffer) if there is one;
     python -m flint_amd.rocprof_summary --gemv <trace dir> <SQ pmc dir> <fetch dir> <write dir> --copy-bytes B
-        the config-1 GEMV sweep (bench.py --gemv-only --copy-probe-mb M): per kernel variant and
+        the config-1 GEMV sweep (bench.py --gemv-only --no-steady --copy-probe-mb M): per kernel variant and
         shape the kernel time, algorithmic and HBM bytes, VALU issue and wait shares;
     python -m flint_amd.rocprof_summary --traffic <fetch dir> <write dir> --copy-bytes B ...
         from two `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of a bench command that
@@ -138,13 +138,18 @@ def traffic(fetch_dir, write_dir, kernel, last, copy_bytes, config, copy_kernel=
 
 
 def _gemv_label(name, grid, seen):
-    """(variant, shape) of a config-1 GEMV dispatch from bench.gemv_sweep: the streamed row-layout
-    kernel (template <4, 5>: K 2560; <6, 4>: K 8192) and the tiled matrix-core kernel, told apart
-    by kernel name and grid (the tiled O and down share a grid and alternate, O first)."""
+    """(variant, shape) of a config-1 GEMV dispatch from bench.gemv_sweep (run with --no-steady):
+    the streamed row-layout kernel (template <4, 5>: K 2560; <6, 4>: K 8192) and the tiled
+    matrix-core kernel (k_gemv_tiled_pf <4, 8>: K 2560; <8, 8>: K 8192; the older k_gemv_tiled:
+    O and down share a grid and alternate, O first), told apart by kernel name and grid."""
     if "k_gemv_stream<4, 5>" in name:
-        return "stream", {57344: "qkv", 40960: "o", 131072: "gate_up"}.get(grid)
+        return "stream", {57344: "qkv", 40960: "o", 131072: "gate_up", 262144: "gate_up"}.get(grid)
     if "k_gemv_stream<6, 4>" in name:
         return "stream", "down"
+    if "k_gemv_tiled_pf<8, 8>" in name:
+        return "tiled", "down"
+    if "k_gemv_tiled_pf<4, 8>" in name:
+        return "tiled", {57344: "qkv", 40960: "o", 262144: "gate_up"}.get(grid)
     if "k_gemv_tiled" in name:
         if grid == 40960:
             seen["t40960"] = seen.get("t40960", 0) + 1
@@ -154,6 +159,7 @@ def _gemv_label(name, grid, seen):
 
 
 GEMV_SHAPES = {"qkv": (3584, 2560), "o": (2560, 2560), "gate_up": (16384, 2560), "down": (2560, 8192)}
+SIMDS, CLOCK_HZ = 256 * 4, 2.4e9  # MI355X: 256 CUs of 4 SIMDs, 2.4 GHz peak engine clock
 
 
 def gemv(trace_dir, pmc_dir, fetch_dir, write_dir, copy_bytes, skip_frac=0.25):
@@ -196,7 +202,7 @@ def gemv(trace_dir, pmc_dir, fetch_dir, write_dir, copy_bytes, skip_frac=0.25):
     out.append(f"FETCH_SIZE reads {fscale:.4f}x and WRITE_SIZE {wscale:.4f}x the bytes of a {copy_bytes}-byte "
                f"device copy (the scale applied below)")
     out.append(f"{'variant':8s} {'shape':8s} {'kernel_us':>9s} {'alg_MB':>8s} {'hbm_MB':>8s} {'GB/s':>7s} {'frac':>6s} "
-               f"{'VALU%':>6s} {'wait%':>6s} {'VALU/wt':>7s}")
+               f"{'VALU%':>6s} {'wait%':>6s} {'VALU/wt':>7s} {'VALU_us':>7s}")
     for (v, shp) in sorted(series, key=lambda t: (t[0], list(GEMV_SHAPES).index(t[1]))):
         n, k = GEMV_SHAPES[shp]
         t = series[(v, shp)]
@@ -210,9 +216,12 @@ def gemv(trace_dir, pmc_dir, fetch_dir, write_dir, copy_bytes, skip_frac=0.25):
         valu = mean(c, "SQ_ACTIVE_INST_VALU") / waves / wave_cyc   # VALU busy share of a wave's life
         wait = mean(c, "SQ_WAIT_INST_ANY") / waves / wave_cyc
         per_w = mean(c, "SQ_INSTS_VALU") * 64.0 / (n * k)          # VALU lane-ops per weight
+        # the VALU floor: every wave64 VALU instruction takes at least 4 cycles of its SIMD (16
+        # lanes), spread over MI355X's 1024 SIMDs at the 2.4 GHz peak clock
+        valu_us = mean(c, "SQ_INSTS_VALU") * 4.0 / (SIMDS * CLOCK_HZ) * 1e6
         gbs = alg / (us * 1e-6) / 1e9
         out.append(f"{v:8s} {shp:8s} {us:9.2f} {alg / 1e6:8.2f} {hbm / 1e6:8.2f} {gbs:7.0f} {gbs / 8000.0:6.3f} "
-                   f"{100 * valu:6.1f} {100 * wait:6.1f} {per_w:7.2f}")
+                   f"{100 * valu:6.1f} {100 * wait:6.1f} {per_w:7.2f} {valu_us:7.2f}")
     return "\n".join(out)
 
 
