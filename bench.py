@@ -160,13 +160,17 @@ def handoff_probe(dev, words=2560, rounds=2000):
     workgroup per CU, `rounds` chained all-to-all hand-offs; median over the workgroups of their
     time per round. Modes: across all workgroups (every XCD) over the decode kernel's uncached
     exchange memory; within each XCD's 32 workgroups over the same memory; within each XCD over
-    ordinary device memory (L2-local coherent loads). Also reports whether every workgroup ran on
-    XCD blockIdx % 8 (the mapping the XCD-local modes assume)."""
+    ordinary device memory (L2-local coherent loads) -- these three poll single words with a sleep
+    between polls; then across all workgroups polled as the decode kernel's waits poll (16-byte
+    groups, the missing ones re-requested together, no sleep), with one round of requests in
+    flight and with two (the second round 512 cycles after the first). Also reports whether every
+    workgroup ran on XCD blockIdx % 8 (the mapping the XCD-local modes assume)."""
     from flint_amd import _lib
     import ctypes
     res = {"words": words, "rounds": rounds}
     grid = ctypes.c_int32()
-    for mode, name in ((0, "all_uncached_us"), (1, "xcd_uncached_us"), (2, "xcd_l2_us")):
+    for mode, name in ((0, "all_uncached_us"), (1, "xcd_uncached_us"), (2, "xcd_l2_us"),
+                       (3 | 1 << 8, "all_groups_us"), (3 | 2 << 8 | 8 << 16, "all_groups_depth2_us")):
         out = torch.zeros(2 * 1024, dtype=torch.int64, device=dev)
         for _ in range(2):      # the first call allocates and warms up
             _lib.call("fl_probe_handoff", mode, words, rounds, _lib.ptr(out), ctypes.byref(grid),
@@ -184,6 +188,37 @@ def handoff_probe(dev, words=2560, rounds=2000):
         if mode == 0:
             xcc = (info & 0xF).tolist()
             res["xcd_is_blockidx_mod_8"] = all(x == i % 8 for i, x in enumerate(xcc))
+    return res
+
+
+def handoff_sweep(dev, rounds=2000):
+    """The group-poll hand-off over its knobs (fl_probe_handoff mode 3): the sleep before each
+    re-request, the number of request rounds in flight and their spacing, at 2560 and 8192 words.
+    Returns {words: {label: median us per hand-off}} (python3 bench.py --handoff-sweep)."""
+    from flint_amd import _lib
+    import ctypes
+    grid = ctypes.c_int32()
+
+    def run(mode, words):
+        out = torch.zeros(2 * 1024, dtype=torch.int64, device=dev)
+        for _ in range(2):
+            _lib.call("fl_probe_handoff", mode, words, rounds, _lib.ptr(out), ctypes.byref(grid),
+                      _lib.stream_ptr())
+            torch.cuda.synchronize()
+        o = out[:2 * grid.value].view(-1, 2).cpu()
+        if int(((o[:, 1] >> 32) & 1).sum()):
+            return None
+        return round(float(o[:, 0].double().median()) * 0.01 / rounds, 3)
+    res = {}
+    for words in (2560, 8192):
+        r = {"single_words_sleep2": run(0, words)}
+        for rs in (0, 1, 2, 4, 8, 16, 32):
+            r[f"depth1_resleep{rs}"] = run(3 | 1 << 8 | rs << 24, words)
+        for gap in (0, 4, 8, 12):
+            r[f"depth2_gap{gap}"] = run(3 | 2 << 8 | gap << 16, words)
+        for gap in (2, 6):
+            r[f"depth3_gap{gap}"] = run(3 | 3 << 8 | gap << 16, words)
+        res[words] = r
     return res
 
 
@@ -264,11 +299,19 @@ def spec_loop(model, args, prompt, ref, n, rounds=40):
     return res
 
 
+def _median_us(pairs):
+    """Median over calls of the HIP-event time around each call, in us. (The mean let one host-side
+    stall between an event and its launch -- once 36 ms in a sweep of 120 calls -- stand for every
+    call.)"""
+    t = sorted(a.elapsed_time(b) for a, b in pairs)
+    return t[len(t) // 2] * 1000.0
+
+
 def gemv_sweep(args, dev, sets=40, rounds=3, steady=True):
     """fl_gemv_int4 at M = 1 over the four per-layer shapes, 40 distinct weight
     sets per shape, called in layer order (QKV, O, gate/up, down of set 0, then set 1, ...) so the
     1.67 GB rotation exceeds the 256 MB Infinity Cache and every call reads its weights from HBM.
-    HIP events around every call; per shape the mean call time and algorithmic GB/s
+    HIP events around every call; per shape the median call time and algorithmic GB/s
     (N*K/2 int4 + N*K/128*4 scale/zero + 2K x + 2N y bytes). Weights are seeded random int4 words
     with bf16 scales 1e-3 and zeros 0 (the time does not depend on the values)."""
     from flint_amd import _lib
@@ -305,7 +348,7 @@ def gemv_sweep(args, dev, sets=40, rounds=3, steady=True):
     torch.cuda.synchronize()
     out = {}
     for name, n, k in shapes:
-        us = sum(a.elapsed_time(b) for a, b in ev[name]) * 1000.0 / len(ev[name])
+        us = _median_us(ev[name])
         nbytes = n * k // 2 + n * (k // 128) * 4 + 2 * k + 2 * n
         out[name] = {"n": n, "k": k, "us": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
                      "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -338,7 +381,7 @@ def gemv_sweep(args, dev, sets=40, rounds=3, steady=True):
     torch.cuda.synchronize()
     tiled = {}
     for name, n, k in shapes:
-        us = sum(a.elapsed_time(b) for a, b in ev[name]) * 1000.0 / len(ev[name])
+        us = _median_us(ev[name])
         nbytes = n * k // 2 + n * (k // 128) * 4 + 2 * k + 2 * n
         tiled[name] = {"us": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
                        "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -498,6 +541,8 @@ def main():
     ap.add_argument("--no-steady", action="store_true",
                     help="leave the steady-state GEMV leg out of the config-1 sweep (profiling runs: its "
                          "long calls would share the sweep's kernel names and grids)")
+    ap.add_argument("--handoff-sweep", action="store_true",
+                    help="only the hand-off probe's group-poll sweep (fl_probe_handoff mode 3), then exit")
     ap.add_argument("--no-handoff", action="store_true",
                     help="skip the hand-off micro-benchmark (fl_probe_handoff)")
     ap.add_argument("--maps", default=None,
@@ -517,6 +562,9 @@ def main():
 
     dev = torch.device("cuda:0")
     args = ModelArgs.from_name(a.config)
+    if a.handoff_sweep:
+        print(json.dumps({"handoff_sweep": handoff_sweep(dev)}), flush=True)
+        return
     if a.gemv_only:
         gemv = gemv_sweep(args, dev, steady=not a.no_steady)
         log(f"config 1 (fl_gemv_int4, {gemv['rotation_bytes'] / 1e9:.2f} GB rotation): {gemv}")

@@ -155,7 +155,9 @@ __device__ __forceinline__ void stamp(const DecodeParams& p, int& slot) {
   ++slot;
 }
 
-// Slow path of a tag wait: sleep-poll with a limit of p.spin_ticks (2 s by default); a timeout (or
+// Slow path of a tag wait: re-read until the tag matches, within a limit of p.spin_ticks (2 s by
+// default; no sleep between reads: each sleep of 64 cycles lengthened a hand-off by ~25 ns in the
+// hand-off probe, fl_probe.hip mode 3); a timeout (or
 // an earlier error) is recorded in p.err and the wait gives up, so a broken producer can never
 // hang the GPU. After an error every later wait of the launch gives up within 64 polls.
 template <typename T, typename Ok, typename Ld>
@@ -163,7 +165,6 @@ __device__ __forceinline__ T spin_until(const DecodeParams& p, T v, Ok ok, Ld ld
   const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
   unsigned it = 0;
   while (!ok(v)) {
-    __builtin_amdgcn_s_sleep(2);
     v = ld();
     if (__builtin_expect((++it & 63u) == 0, 0)) {  // rare: out of the hot code
       if (__hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
@@ -201,7 +202,6 @@ __device__ __forceinline__ void poll_tagged(const DecodeParams& p, unsigned long
       if (valid(i) && !ok(v[i])) done = false;
     if (done) return;
     if (it == 0) t0 = __builtin_amdgcn_s_memrealtime();
-    __builtin_amdgcn_s_sleep(2);
 #pragma unroll
     for (int i = 0; i < B; ++i)
       if (valid(i) && !ok(v[i])) v[i] = ld_coh_u64(addr(i));

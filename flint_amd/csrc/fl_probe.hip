@@ -17,7 +17,11 @@
 //   1: the workgroups of one XCD (blockIdx % 8: the round-robin dispatch over the 8 XCDs of an
 //      MI355X), 8 independent groups; the same memory;
 //   2: the workgroups of one XCD; ordinary device memory, whose coherent loads are served by
-//      that XCD's L2 (the one L2 all the group's CUs share).
+//      that XCD's L2 (the one L2 all the group's CUs share);
+//   3: all workgroups, uncached memory, polled the way the decode kernel's waits poll: 16-byte
+//      groups of 4 words, every missing group re-requested at once, 1 to 3 rounds of requests in
+//      flight (k_probe_groups).
+// Modes 0-2 poll single words with a sleep between polls.
 // Every workgroup also records its XCC_ID hardware register, so the host can check the
 // blockIdx-to-XCD mapping that modes 1 and 2 assume. Every wait is bounded (about 0.5 s): a
 // workgroup that is not resident, or a mapping that is not the assumed one, ends in a reported
@@ -91,6 +95,86 @@ __global__ __launch_bounds__(PR_NT, 1) void k_probe_handoff(uint32_t* __restrict
   }
 }
 
+// Mode 3: all workgroups over the uncached exchange memory, polled in 16-byte groups of 4 words
+// (the decode kernel's poll_issue form) with DEPTH rounds of requests in flight: round r + 1 is
+// requested before round r's answers are checked, `gap` x 64 cycles after it, so a word that
+// lands just after one round passed the coherence point is seen by the next without a full round
+// trip in between. Each round re-requests only the groups not yet seen complete (complete groups
+// get an out-of-range request, which touches no memory and keeps the requests branch-free),
+// `resleep` x 64 cycles after the answers that found them incomplete.
+constexpr int PR_MAXG = PR_MAXW / 4 / PR_NT;  // 16-byte groups polled per thread, at most
+template <int DEPTH>
+__global__ __launch_bounds__(PR_NT, 1) void k_probe_groups(uint32_t* __restrict__ buf, int words,
+                                                           int rounds, int gap, int resleep,
+                                                           unsigned long long* __restrict__ out) {
+  extern __shared__ uint32_t pad[];
+  const int tid = threadIdx.x, wg = blockIdx.x, G = gridDim.x;
+  const int share = (words + G - 1) / G;
+  const int w0 = wg * share, w1 = min(words, w0 + share);
+  const int ng = words >> 2;
+  if (tid == 0) pad[0] = 0;
+  bool timed_out = false;
+  __syncthreads();
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  for (int r = 0; r < rounds && !timed_out; ++r) {
+    uint32_t* v = buf + (size_t)(r & 1) * words;
+    const uint32_t tag = (uint32_t)(r % 65535) + 1u;
+    for (int i = w0 + tid; i < w1; i += PR_NT) st_coh_u32(v + i, (tag << 16) | (uint32_t)(i & 0xFFFF));
+    const auto rs = buf_rsrc(v, (uint32_t)words * 4u);
+    bool seen[PR_MAXG];
+#pragma unroll
+    for (int j = 0; j < PR_MAXG; ++j) seen[j] = tid + j * PR_NT >= ng;
+    uint4 q[DEPTH][PR_MAXG];
+    auto issue = [&](uint4 (&d)[PR_MAXG]) {
+#pragma unroll
+      for (int j = 0; j < PR_MAXG; ++j)
+        d[j] = buf_ld128_coh(rs, seen[j] ? 0xFFFFFFF0u : (uint32_t)(tid + j * PR_NT) * 16u);
+    };
+    auto take = [&](const uint4 (&d)[PR_MAXG]) {
+      bool all = true;
+#pragma unroll
+      for (int j = 0; j < PR_MAXG; ++j) {
+        const uint4 w = d[j];
+        seen[j] = seen[j] || (((w.x >> 16) == tag) & ((w.y >> 16) == tag) & ((w.z >> 16) == tag) &
+                              ((w.w >> 16) == tag));
+        all &= seen[j];
+      }
+      return all;
+    };
+    auto pause = [&] {
+      for (int s = 0; s < gap; ++s) __builtin_amdgcn_s_sleep(1);
+    };
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      if (d) pause();
+      issue(q[d]);
+    }
+    const unsigned long long ts = __builtin_amdgcn_s_memrealtime();
+    for (bool done = false; !done;) {
+#pragma unroll
+      for (int d = 0; d < DEPTH && !done; ++d) {
+        if (take(q[d])) {
+          done = true;
+        } else {
+          for (int t = 0; t < resleep; ++t) __builtin_amdgcn_s_sleep(1);
+          issue(q[d]);
+        }
+      }
+      if (!done && __builtin_amdgcn_s_memrealtime() - ts > PR_SPIN) {
+        timed_out = true;
+        break;
+      }
+    }
+    timed_out = __syncthreads_or(timed_out);
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+  if (tid == 0) {
+    const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // hwreg(HW_REG_XCC_ID)
+    out[2 * wg] = t1 - t0;
+    out[2 * wg + 1] = (unsigned long long)xcc | ((unsigned long long)timed_out << 32);
+  }
+}
+
 // exchange buffers, kept for the process (the uncached one must never be freed once read)
 std::mutex g_probe_mu;
 uint32_t* g_probe_uc[64] = {};
@@ -102,8 +186,13 @@ extern "C" {
 
 int fl_probe_handoff(int32_t mode, int32_t words, int32_t rounds, uint64_t* out, int32_t* grid,
                      void* stream) {
-  if (mode < 0 || mode > 2 || words < 4 || words > PR_MAXW || rounds < 1 || rounds > 100000 || !out ||
-      !grid)
+  // mode: bits 0-7 the kind (0..3); kind 3 also takes the poll depth (bits 8-11, 1..3), the gap
+  // between the first rounds' requests (bits 16-23, x 64 cycles) and the sleep before a re-request
+  // (bits 24-30, x 64 cycles)
+  const int kind = mode & 0xFF, depth = (mode >> 8) & 0xF, gap = (mode >> 16) & 0xFF,
+            resleep = (mode >> 24) & 0x7F;
+  if (mode < 0 || kind > 3 || (kind < 3 && mode != kind) || (kind == 3 && (depth < 1 || depth > 3 || words % 4)) ||
+      words < 4 || words > PR_MAXW || rounds < 1 || rounds > 100000 || !out || !grid)
     return FL_E_ARG;
   int dev = 0, cu = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FL_E_HIP;
@@ -112,28 +201,38 @@ int fl_probe_handoff(int32_t mode, int32_t words, int32_t rounds, uint64_t* out,
   uint32_t* buf;
   {
     std::lock_guard<std::mutex> lk(g_probe_mu);
-    uint32_t** slot = mode == 2 ? &g_probe_rw[dev] : &g_probe_uc[dev];
+    uint32_t** slot = kind == 2 ? &g_probe_rw[dev] : &g_probe_uc[dev];
     if (!*slot) {
       void* p = nullptr;
-      const hipError_t e = mode == 2 ? hipMalloc(&p, bytes) : hipExtMallocWithFlags(&p, bytes, hipDeviceMallocUncached);
+      const hipError_t e = kind == 2 ? hipMalloc(&p, bytes) : hipExtMallocWithFlags(&p, bytes, hipDeviceMallocUncached);
       if (e != hipSuccess) return FL_E_HIP;
       if (hipMemset(p, 0, bytes) != hipSuccess) return FL_E_HIP;
       *slot = reinterpret_cast<uint32_t*>(p);
     }
     buf = *slot;
   }
+  const void* kfn = kind < 3 ? reinterpret_cast<const void*>(k_probe_handoff)
+                  : depth == 1 ? reinterpret_cast<const void*>(k_probe_groups<1>)
+                  : depth == 2 ? reinterpret_cast<const void*>(k_probe_groups<2>)
+                               : reinterpret_cast<const void*>(k_probe_groups<3>);
   // every workgroup must be resident at once (one per CU)
   int occ = 0;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(k_probe_handoff),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, PR_LDS) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(k_probe_handoff),
-                                                   PR_NT, PR_LDS) != hipSuccess || occ < 1)
+  if (hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, PR_LDS) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn, PR_NT, PR_LDS) != hipSuccess || occ < 1)
     return FL_E_LAUNCH;
   // tags restart at 1 each call: clear both buffers of every group first (stream-ordered)
   if (hipMemsetAsync(buf, 0, bytes, reinterpret_cast<hipStream_t>(stream)) != hipSuccess) return FL_E_HIP;
   *grid = cu;
-  hipLaunchKernelGGL(k_probe_handoff, dim3(cu), dim3(PR_NT), PR_LDS, reinterpret_cast<hipStream_t>(stream),
-                     buf, (int)words, (int)rounds, (int)mode, reinterpret_cast<unsigned long long*>(out));
+  auto* o = reinterpret_cast<unsigned long long*>(out);
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (kind < 3)
+    hipLaunchKernelGGL(k_probe_handoff, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, kind, o);
+  else if (depth == 1)
+    hipLaunchKernelGGL(k_probe_groups<1>, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, gap, resleep, o);
+  else if (depth == 2)
+    hipLaunchKernelGGL(k_probe_groups<2>, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, gap, resleep, o);
+  else
+    hipLaunchKernelGGL(k_probe_groups<3>, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, gap, resleep, o);
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
 

@@ -242,7 +242,12 @@ int fl_sample_noalloc(const float* logits, int32_t rows, int32_t vocab, float te
  * workgroup `rounds` times in a chain, the way the decode / verify kernels hand activations
  * between phases. mode 0: all workgroups, over the uncached exchange memory the kernels use;
  * mode 1: the workgroups of each XCD separately (blockIdx % 8), same memory; mode 2: the
- * workgroups of each XCD over ordinary device memory (coherent loads served by that XCD's L2).
+ * workgroups of each XCD over ordinary device memory (coherent loads served by that XCD's L2);
+ * modes 0-2 poll single words with a sleep between polls. mode 3 | depth << 8 | gap << 16 |
+ * resleep << 24: all workgroups, uncached memory, polled as the decode kernel polls (16-byte
+ * groups of 4 words, the missing ones re-requested together) with depth (1..3) rounds of
+ * requests in flight, the first rounds gap x 64 cycles apart, resleep x 64 cycles before a
+ * re-request; words a multiple of 4.
  * out (device, uint64 [2 * grid]): per workgroup the 100 MHz-clock ticks of all rounds, then its
  * XCC_ID register | (1 << 32) if a wait timed out (0.5 s bound). *grid receives the number of
  * workgroups (the CU count). Stream-ordered; allocates its exchange buffers on the first call. */
