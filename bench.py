@@ -191,6 +191,27 @@ def handoff_probe(dev, words=2560, rounds=2000):
     return res
 
 
+def dequant_rate(dev, iters=2000):
+    """Compute rate of the exact dequantisation plus an M = 8 MFMA product with every weight
+    already in registers (fl_probe_dequant): the row layout on the vector ALUs (k_verify's tile
+    product) and the tiled layout on the matrix cores, in weights per second over the slowest
+    workgroup, beside the rate at which HBM delivers int4 weights with their scale/zero words
+    (8 TB/s / 0.53125 B per weight)."""
+    from flint_amd import _lib
+    import ctypes
+    grid = ctypes.c_int32()
+    res = {"hbm_tweights_s": round(HBM_PEAK_GBS * 1e9 / (0.5 + 4 / 128) / 1e12, 2)}
+    for mode, name in ((0, "row_valu_tweights_s"), (1, "tiled_mfma_tweights_s")):
+        out = torch.zeros(2 * 1024, dtype=torch.int64, device=dev)
+        for _ in range(2):      # the first call loads the code object
+            _lib.call("fl_probe_dequant", mode, iters, _lib.ptr(out), ctypes.byref(grid), _lib.stream_ptr())
+            torch.cuda.synchronize()
+        ticks = out[:2 * grid.value].view(-1, 2)[:, 0].double().cpu()
+        weights = grid.value * 8 * 3 * 2048 * iters
+        res[name] = round(weights / (float(ticks.max()) * 1e-8) / 1e12, 2)
+    return res
+
+
 def handoff_sweep(dev, rounds=2000):
     """The group-poll hand-off over its knobs (fl_probe_handoff mode 3): the sleep before each
     re-request, the number of request rounds in flight and their spacing, at 2560 and 8192 words.
@@ -661,10 +682,12 @@ def main():
         sampling.update(fused_sampling(model, args, dev, a.ctx))
         log(f"sampling over {args.vocab_size} logits: {sampling}")
 
-    handoff = None
+    handoff = dq_rate = None
     if not a.no_handoff:
         handoff = handoff_probe(dev)
         log(f"hand-off of a {handoff['words']}-word tagged vector: {handoff}")
+        dq_rate = dequant_rate(dev)
+        log(f"exact dequantisation + M = 8 MFMA product, weights in registers: {dq_rate}")
 
     if a.copy_probe_mb > 0:
         copy_probe(dev, a.copy_probe_mb)
@@ -704,6 +727,7 @@ def main():
         "gemv_sweep": gemv,
         "sampling": sampling,
         "handoff": handoff,
+        "dequant_rate": dq_rate,
     }
     print(json.dumps(out), flush=True)
     # release the decode state (and its device memory) before interpreter shutdown

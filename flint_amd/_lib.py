@@ -30,6 +30,7 @@ EXPORTS = [
     "fl_state_force_timeout",
     "fl_decode_step", "fl_decode_sample", "fl_decode_hidden", "fl_verify", "fl_kv_move", "fl_sample",
     "fl_sample_noalloc", "fl_probe_handoff", "fl_tile_int4", "fl_dequant_int4_tiled", "fl_gemv_int4_tiled",
+    "fl_probe_dequant",
 ]
 
 
@@ -99,6 +100,7 @@ def load(path=LIB_PATH):
         "fl_tile_int4": ([vp, vp, i32, i32, vp], i32),
         "fl_dequant_int4_tiled": ([vp, vp, vp, i32, i32, vp], i32),
         "fl_gemv_int4_tiled": ([vp, vp, vp, vp, i32, i32, vp], i32),
+        "fl_probe_dequant": ([i32, i32, vp, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

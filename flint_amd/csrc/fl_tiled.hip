@@ -264,6 +264,93 @@ __global__ __launch_bounds__(256) void k_dequant_tiled(const uint4* __restrict__
   }
 }
 
+// Diagnostic: the compute rate of the exact dequantisation with an M = 8 matrix-core product and
+// no memory traffic at all. Each wave keeps PDQ_NU units (16 rows x one 128-group: 2048 weights)
+// of seeded pseudo-random words in registers and recomputes them `iters` times against 8 token
+// rows in LDS -- k_verify's tile product at M = 8 with the weights already there. MODE 0: this
+// library's row layout, dequantised on the vector ALUs (dq32, four 16x16x32 MFMAs per 32 weights:
+// k_verify's tile_mma); MODE 1: the tiled layout, both exact fp32 steps on 16x16x16 MFMAs and the
+// dot on a 16x16x32 MFMA per two tiles (unit_dot with token rows in place of the one x row).
+// out[2 wg] = the workgroup's 100 MHz ticks, out[2 wg + 1] = bits of its result (kept so the
+// work is not dropped).
+constexpr int PDQ_NU = 3, PDQ_LD = 392;  // units per wave; token-row pitch (bf16)
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void k_probe_dequant(int iters, unsigned long long* __restrict__ out) {
+  __shared__ __align__(16) uint16_t xs[17 * PDQ_LD];  // token rows 0..7, row 16 zero (rows 8..15)
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int i = tid; i < 17 * PDQ_LD / 2; i += 512)
+    reinterpret_cast<uint32_t*>(xs)[i] = i < 8 * PDQ_LD / 2 ? 0x3F803F80u ^ ((i * 2654435761u) & 0x007F007Fu) : 0u;
+  __syncthreads();
+  uint4 w[PDQ_NU];
+  uint32_t s[PDQ_NU];
+  uint32_t h = (blockIdx.x * 512u + tid) * 2654435761u + 12345u;
+  auto next = [&h]() {
+    h ^= h << 13;
+    h ^= h >> 17;
+    h ^= h << 5;
+    return h;
+  };
+#pragma unroll
+  for (int u = 0; u < PDQ_NU; ++u) {
+    w[u] = make_uint4(next(), next(), next(), next());
+    s[u] = 0x3A833A83u ^ (next() & 0x00070007u);  // scales near 1e-3, zeros near 1e-3
+  }
+  const int r = lane & 15, c = lane >> 4;
+  fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  __syncthreads();
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int u = 0; u < PDQ_NU; ++u) {
+      // the words are opaque to the compiler each pass, so nothing is hoisted out of the loop
+      asm volatile("" : "+v"(w[u].x), "+v"(w[u].y), "+v"(w[u].z), "+v"(w[u].w), "+v"(s[u]));
+      if constexpr (MODE == 0) {
+        const uint16_t* xrow = xs + (r < 8 ? r : 16) * PDQ_LD + c * 32 + u * 128;
+        uint4 xa[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xa[e] = *reinterpret_cast<const uint4*>(xrow + e * 8);
+        uint32_t d[4][4];
+        dq32(w[u], dq_const(s[u]), d);
+        mfma_chunk(d, xa, acc);
+      } else {
+        const int b = lane >> 4, cc = lane & 15;  // tiled lane (b, c): rows 4b..4b+3, column c
+        const GroupK k = group_k(s[u], cc - 4 * b);
+        const AndOrK ao = and_or_k();
+        const uint32_t one = 0x3F80u;
+        const int dd = cc - 4 * b;
+        const uint32_t ilo = dd == 0 ? one : (dd == 1 ? one << 16 : 0u), ihi = dd == 2 ? one : (dd == 3 ? one << 16 : 0u);
+        uint32_t wa = w[u].x, wb = w[u].y, wc = w[u].z, wd = w[u].w;
+        const uint16_t* xrow = xs + (cc < 8 ? cc : 16) * PDQ_LD + u * 128 + 4 * b;
+#pragma unroll
+        for (int tp = 0; tp < 4; ++tp) {
+          uint32_t q0[2], q1[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int t = 2 * tp + hh;
+            uint32_t& lo = t < 4 ? wa : wb;
+            uint32_t& hi = t < 4 ? wc : wd;
+            const uint32_t r0 = and_or(lo, ao), r1 = and_or(hi, ao);
+            lo >>= 4;
+            hi >>= 4;
+            tile_dq(r0, r1, k, ilo, ihi, q0[hh], q1[hh]);
+          }
+          const uint2 xa = *reinterpret_cast<const uint2*>(xrow + 32 * tp);
+          const uint2 xb = *reinterpret_cast<const uint2*>(xrow + 32 * tp + 16);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b8(xa.x, xa.y, xb.x, xb.y), b8(q0[0], q1[0], q0[1], q1[1]),
+                                                        acc, 0, 0, 0);
+        }
+      }
+    }
+  }
+  const float v = acc[0] + acc[1] + acc[2] + acc[3];
+  __syncthreads();  // the workgroup's time is its slowest wave's
+  const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+  if (tid == 0) {
+    out[2 * blockIdx.x] = t1 - t0;
+    out[2 * blockIdx.x + 1] = __float_as_uint(v);
+  }
+}
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 }  // namespace
@@ -309,6 +396,21 @@ int fl_gemv_int4_tiled(const uint32_t* qt, const uint32_t* sz, const uint16_t* x
     hipLaunchKernelGGL(k_gemv_tiled, dim3(n / 16), dim3(TW_NW * 64), (size_t)k * 2 + TW_NW * 16 * 4,
                        as_stream(stream), q4, sz, x, y, n, k);
   }
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+}
+
+int fl_probe_dequant(int32_t mode, int32_t iters, uint64_t* out, int32_t* grid, void* stream) {
+  if (mode < 0 || mode > 1 || iters < 1 || iters > 1000000 || !out || !grid) return FL_E_ARG;
+  int dev = 0, cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu < 1)
+    return FL_E_HIP;
+  *grid = cu;
+  auto* o = reinterpret_cast<unsigned long long*>(out);
+  if (mode == 0)
+    hipLaunchKernelGGL(k_probe_dequant<0>, dim3(cu), dim3(512), 0, as_stream(stream), (int)iters, o);
+  else
+    hipLaunchKernelGGL(k_probe_dequant<1>, dim3(cu), dim3(512), 0, as_stream(stream), (int)iters, o);
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
 

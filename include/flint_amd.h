@@ -253,6 +253,15 @@ int fl_sample_noalloc(const float* logits, int32_t rows, int32_t vocab, float te
  * workgroups (the CU count). Stream-ordered; allocates its exchange buffers on the first call. */
 int fl_probe_handoff(int32_t mode, int32_t words, int32_t rounds, uint64_t* out, int32_t* grid,
                      void* stream);
+/* Compute rate of the exact int4 dequantisation with an M = 8 matrix-core product and no memory
+ * traffic, no counterpart in the reference: one 512-thread workgroup per CU, every wave keeping 3
+ * units (16 rows x one 128-group) of seeded words in registers and recomputing them `iters`
+ * times against 8 token rows in LDS. mode 0: the row layout dequantised on the vector ALUs plus
+ * the MFMA dot (k_verify's tile product); mode 1: the tiled layout, dequantisation and dot on
+ * the matrix cores (fl_gemv_int4_tiled's unit with token rows). out (device, uint64 [2 * grid]):
+ * per workgroup the 100 MHz-clock ticks of its loop, then bits of its result; *grid receives the
+ * number of workgroups. Weights per workgroup: 8 x 3 x 2048 x iters. Stream-ordered. */
+int fl_probe_dequant(int32_t mode, int32_t iters, uint64_t* out, int32_t* grid, void* stream);
 
 #ifdef __cplusplus
 }

@@ -54,6 +54,8 @@ def test_argument_errors_without_gpu():
     assert lib.fl_probe_handoff(3 | 4 << 8, 64, 10, p, ctypes.byref(g), None) == -1   # depth 4
     assert lib.fl_probe_handoff(3 | 1 << 8, 66, 10, p, ctypes.byref(g), None) == -1   # 66 % 4
     assert lib.fl_probe_handoff(1 | 1 << 8, 64, 10, p, ctypes.byref(g), None) == -1   # extra bits
+    assert lib.fl_probe_dequant(2, 10, p, ctypes.byref(g), None) == -1                 # no mode 2
+    assert lib.fl_probe_dequant(0, 0, p, ctypes.byref(g), None) == -1                 # iters >= 1
 
 
 def test_storage_permutations():

@@ -28,3 +28,19 @@ def test_probe_handoff_modes(dev, mode, words):
     us = float(o[:, 0].double().median()) * 0.01 / 50
     log(f"probe mode {mode:#x} words {words}: {us:.3f} us per hand-off, "
         f"xcd = blockIdx % 8: {all(x == i % 8 for i, x in enumerate(xcc))}")
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_probe_dequant_modes(dev, mode):
+    """The dequantisation-rate probe (fl_probe_dequant) runs both forms to completion with a
+    positive time in every workgroup; the rate is logged (and reported by bench.py)."""
+    from flint_amd import _lib
+    grid = ctypes.c_int32()
+    out = torch.zeros(2 * 1024, dtype=torch.int64, device=dev)
+    _lib.call("fl_probe_dequant", mode, 50, _lib.ptr(out), ctypes.byref(grid), _lib.stream_ptr())
+    torch.cuda.synchronize()
+    o = out[:2 * grid.value].view(-1, 2).cpu()
+    assert grid.value >= 8
+    assert bool((o[:, 0] > 0).all())
+    rate = grid.value * 8 * 3 * 2048 * 50 / (float(o[:, 0].max()) * 1e-8) / 1e12
+    log(f"probe dequant mode {mode}: {rate:.2f} Tweights/s (50 passes)")
