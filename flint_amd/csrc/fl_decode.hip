@@ -1067,6 +1067,9 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
 constexpr int GQ_VRK = 288;                      // keys per LDS round (32 slices x 288 keys: one round up to ctx 9216)
 constexpr int GQ_VT_LD = GQ_VRK + 8;             // V^T row pitch (bf16)
 constexpr int GQ_CPT = (GQ_VRK * 8 + NT - 1) / NT;  // 16-byte K (and V) chunks per thread per round
+constexpr int GQ_KT = NT - FL_WAVE;                   // threads of the first round (all waves but the last)
+constexpr int GQ_CPT1 = (GQ_VRK * 8 + GQ_KT - 1) / GQ_KT;  // ... and their chunks each
+static_assert(GQ_CPT1 >= GQ_CPT, "the register arrays hold either kind of round");
 constexpr int GQ_ROWS = 8;                       // query heads per KV group this path takes
 constexpr int GQ_MAXSL = 32;                     // slices per group (4 per wave in the merge)
 constexpr int GQ_KS = 0, GQ_VT = GQ_KS + GQ_VRK * 128, GQ_WP = GQ_VT + 64 * GQ_VT_LD * 2;
@@ -1165,20 +1168,24 @@ __device__ void attention_gqa(const DecodeParams& p, int l, uint32_t qtag, uint3
   uint16_t* const qs = reinterpret_cast<uint16_t*>(ws);  // [16][64] q rows, then new k, new v
   uint16_t* const kn = qs + 16 * 64;
   uint16_t* const vn = kn + 64;
-  // cached keys [k0 + kb, k0 + kb + n) into rows 0 .. n-1 of ks and columns 0 .. n-1 of vt
-  auto load_round = [&](int kb, int n) {
+  // cached keys [k0 + kb, k0 + kb + n): requested into registers by NTH threads, CPT 16-byte
+  // chunks each (request_round), then stored into rows 0 .. n-1 of ks and columns 0 .. n-1 of vt
+  // (store_round)
+  uint4 kv[GQ_CPT1], vv[GQ_CPT1];
+  auto request_round = [&](int kb, int n, auto cpt, int nth) {
     const auto kr = buf_rsrc(p.kc + cbase + (size_t)(k0 + kb) * 64, (uint32_t)n * 128u);
     const auto vr = buf_rsrc(p.vc + cbase + (size_t)(k0 + kb) * 64, (uint32_t)n * 128u);
-    uint4 kv[GQ_CPT], vv[GQ_CPT];
 #pragma unroll
-    for (int i = 0; i < GQ_CPT; ++i) {  // loads past the round's n keys read as 0, touching no memory
-      const int ci = tid + NT * i;
+    for (int i = 0; i < decltype(cpt)::value; ++i) {  // loads past the round's n keys read as 0, touching no memory
+      const int ci = tid + nth * i;
       kv[i] = buf_ld128(kr, (uint32_t)ci * 16u);
       vv[i] = buf_ld128(vr, (uint32_t)ci * 16u);
     }
+  };
+  auto store_round = [&](int n, auto cpt, int nth) {
 #pragma unroll
-    for (int i = 0; i < GQ_CPT; ++i) {
-      const int ci = tid + NT * i, key = ci >> 3, d0 = (ci & 7) * 8;
+    for (int i = 0; i < decltype(cpt)::value; ++i) {
+      const int ci = tid + nth * i, key = ci >> 3, d0 = (ci & 7) * 8;
       if (key >= n) continue;  // a row past the round: the new key may be staged there
       *reinterpret_cast<uint4*>(ks + key * 64 + d0) = kv[i];
       const uint32_t w4[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
@@ -1189,38 +1196,48 @@ __device__ void attention_gqa(const DecodeParams& p, int l, uint32_t qtag, uint3
       }
     }
   };
-  if (nc > 0) load_round(0, min(nc, GQ_VRK));  // cached keys: requested before the q wait
-  {  // q of the group's heads (rows 0 .. QPG-1) and, for the last slice, the new key's k and v
+  using CptAll = std::integral_constant<int, GQ_CPT>;
+  using CptKey = std::integral_constant<int, GQ_CPT1>;
+  auto load_round = [&](int kb, int n) {  // later rounds: every thread
+    request_round(kb, n, CptAll{}, NT);
+    store_round(n, CptAll{}, NT);
+  };
+  // The first round of cached keys is requested by the seven key waves before the q wait and
+  // stored after it; the last wave holds no keys and polls q (and the new k / v) alone. A wave's
+  // loads complete in order, so a poll behind a wave's share of the round (72 KB per workgroup)
+  // returned only after the round had arrived: the q / k / v wait took 4.0-4.4 us per layer at
+  // ctx 8192 against 2.1 us in the per-head units.
+  const bool keyw = wave < NWAVE - 1;
+  if (nc > 0 && keyw) request_round(0, min(nc, GQ_VRK), CptKey{}, GQ_KT);
+  if (!keyw) {  // q of the group's heads (rows 0 .. QPG-1) and, for the last slice, the new key's k and v
     const int nq = QPG * 32, total = nq + (last ? 64 : 0);
-    const int HALFW = (NH + 2 * NKV) * 32;
-    (void)HALFW;
-    constexpr int B = 2;
+    constexpr int B = (GQ_ROWS * 32 + 64 + 63) / 64;
     auto word = [&](int idx) {
       if (idx < nq) return p.qkv + (g * QPG + (idx >> 5)) * 32 + (idx & 31);
       const int i2 = idx - nq;
       return p.qkv + ((i2 >> 5) ? NH + NKV + g : NH + g) * 32 + (i2 & 31);
     };
-    for (int base = 0; base < total; base += B * NT) {
-      unsigned long long v[B];
+    unsigned long long v[B];
 #pragma unroll
-      for (int i = 0; i < B; ++i) {
-        const int idx = base + tid + i * NT;
-        v[i] = idx < total ? ld_coh_u64(word(idx)) : 0ull;
-      }
-      poll_tagged<B>(p, v, qtag, [&](int i) { return word(base + tid + i * NT); },
-                     [&](int i) { return base + tid + i * NT < total; });
+    for (int i = 0; i < B; ++i) {
+      const int idx = lane + i * 64;
+      v[i] = idx < total ? ld_coh_u64(word(idx)) : 0ull;
+    }
+    poll_tagged<B>(p, v, qtag, [&](int i) { return word(lane + i * 64); },
+                   [&](int i) { return lane + i * 64 < total; });
 #pragma unroll
-      for (int i = 0; i < B; ++i) {
-        const int idx = base + tid + i * NT;
-        if (idx < total) {
-          uint16_t* dst = idx < nq ? qs + (idx >> 5) * 64 : ((idx - nq) >> 5 ? vn : kn);
-          const int dp = idx & 31;  // NEOX pair: dims dp and dp + 32
-          dst[dp] = (uint16_t)v[i];
-          dst[dp + 32] = (uint16_t)(v[i] >> 16);
-        }
+    for (int i = 0; i < B; ++i) {
+      const int idx = lane + i * 64;
+      if (idx < total) {
+        uint16_t* dst = idx < nq ? qs + (idx >> 5) * 64 : ((idx - nq) >> 5 ? vn : kn);
+        const int dp = idx & 31;  // NEOX pair: dims dp and dp + 32
+        dst[dp] = (uint16_t)v[i];
+        dst[dp + 32] = (uint16_t)(v[i] >> 16);
       }
     }
-    for (int i = tid; i < (16 - QPG) * 32; i += NT) reinterpret_cast<uint32_t*>(qs + QPG * 64)[i] = 0u;
+    for (int i = lane; i < (16 - QPG) * 32; i += 64) reinterpret_cast<uint32_t*>(qs + QPG * 64)[i] = 0u;
+  } else if (nc > 0) {
+    store_round(min(nc, GQ_VRK), CptKey{}, GQ_KT);
   }
   lds_barrier();
   stamp(p, slot);
@@ -2576,6 +2593,8 @@ __device__ void attention_verify(const DecodeParams& p, int l, uint32_t qtag, ui
         }
       }
     };
+    // (the first round is stored before the q wait: holding it in registers across the wait, as
+    // the decode kernel's by-group attention does, spills in this kernel)
     if (nc > 0) load_round(0, min(nc, VRK));  // cached keys: requested before the q wait
     // q of the head for every token (zero rows up to the tile edge); for the last slice the new
     // keys' K / V rows (after the round's cached keys, if they fit, else in a round of their own)
@@ -3613,7 +3632,9 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
     st->since_clear = 0;
   }
   st->att_spw = 8;
-  st->gq_min = 1 << 30;  // the attention by KV group only on request (FLINT_AMD_GQA_MIN)
+  // the attention by KV group from 5120 cached keys: measured on one box against the per-head
+  // units, +25 / +16 us per step at ctx 3072 / 4096, -13 / -20 / -17 us at 6144 / 8192 / 12288
+  st->gq_min = 5120;
   st->gq_kps = 128;
   st->vkps = 128;
   st->vtok_work = 5120;

@@ -9,6 +9,8 @@ if ROOT not in sys.path:
 
 
 def pytest_configure(config):
+    import tests.helpers
+    tests.helpers.CAPTURE = config.pluginmanager.getplugin("capturemanager")
     config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device)")
     config.addinivalue_line("markers", "slow: 40-layer CPU oracle measurements (minutes, ~15 GB); "
                                        "run only with FLINT_AMD_SLOW=1")

@@ -12,10 +12,25 @@ def log(*a):
     sys.stdout.flush()
 
 
+# pytest's capture manager (set by conftest.py): record() lines go straight to the terminal while
+# a test runs, so a long full-size test (minutes of CPU oracle work) shows its progress as it goes
+CAPTURE = None
+
+
+def say(line):
+    """log() past pytest's output capture: the per-step / per-layer lines of the full-size tests,
+    which spend minutes on the CPU oracle, reach the terminal as they are made."""
+    if CAPTURE is not None:
+        with CAPTURE.global_and_fixture_disabled():
+            log(line)
+    else:
+        log(line)
+
+
 def record(line):
-    """log() a parity figure and, when FLINT_AMD_PARITY_OUT names a file, append it there (the
-    per-step / per-layer parity summaries kept beside the profiles)."""
-    log(line)
+    """say() a parity figure and, when FLINT_AMD_PARITY_OUT names a file, append it there (the
+    parity summaries kept beside the profiles)."""
+    say(line)
     path = os.environ.get("FLINT_AMD_PARITY_OUT")
     if path:
         os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)

@@ -22,7 +22,7 @@ import pytest
 import torch
 
 from flint_amd.synth import ModelArgs, synth_weights
-from tests.helpers import (bf16_ulp, log, logit_bar, logit_stats, near_tie, oracle_pair, record,
+from tests.helpers import (bf16_ulp, log, logit_bar, logit_stats, near_tie, oracle_pair, record, say,
                            row_bars, top2_margin, ulp_stats)
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(600)]
@@ -79,7 +79,7 @@ def _check_step(label, name, eng_logits, ref, alt):
     bar, mbar = row_bars(name, fl)
     am_e, am_o = int(torch.argmax(eng_logits)), int(torch.argmax(ref))
     margin = top2_margin(ref)
-    log(f"{label}: kernel max|d|={st['max']:.4f} mean|d|={st['mean']:.2e} within 2e-2 {st['within']:.2%} | "
+    say(f"{label}: kernel max|d|={st['max']:.4f} mean|d|={st['mean']:.2e} within 2e-2 {st['within']:.2%} | "
         f"oracle 2nd order max|d|={fl['max']:.4f} mean|d|={fl['mean']:.2e} within {fl['within']:.2%} | "
         f"argmax {am_e}/{am_o} margin {margin:.4f}")
     assert st["max"] <= bar and st["mean"] <= mbar, (label, st, bar, mbar)
