@@ -61,7 +61,8 @@ def gemv_int4(q, sz, x, y=None):
 
 
 def gemm_int4(q, sz, x, y=None):
-    """Y[M,N] = bf16(X[M,K] . dq[N,K]^T), M <= 32, weights read once for all M rows."""
+    """Y[M,N] = bf16(X[M,K] . dq[N,K]^T) for any M: blocks of up to 32 rows (FL_MAX_VERIFY), each
+    one fl_gemm_int4 launch that reads the weights once for all of its rows."""
     _check_dev(q, torch.int32, "q")
     _check_dev(sz, torch.int32, "sz")
     _check_dev(x, torch.bfloat16, "x")
@@ -71,8 +72,12 @@ def gemm_int4(q, sz, x, y=None):
         raise ValueError("x inner dimension mismatch")
     if y is None:
         y = torch.empty(m, n, dtype=torch.bfloat16, device=q.device)
-    _lib.call("fl_gemm_int4", _lib.ptr(q), _lib.ptr(sz), _lib.ptr(x), _lib.ptr(y), m, n, k,
-              _lib.stream_ptr())
+    if m > 0 and (y.shape != (m, n) or not y.is_contiguous()):
+        raise ValueError("y must be a contiguous [M, N] tensor")
+    for r0 in range(0, m, _lib.MAX_VERIFY):
+        mb = min(_lib.MAX_VERIFY, m - r0)
+        _lib.call("fl_gemm_int4", _lib.ptr(q), _lib.ptr(sz), _lib.ptr(x[r0:]), _lib.ptr(y[r0:]), mb, n, k,
+                  _lib.stream_ptr())
     return y
 
 

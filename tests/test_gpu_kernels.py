@@ -136,10 +136,11 @@ def test_gemm_rows_match_gemv(dev, m):
         assert float((d > 0).float().mean()) < 2e-3
 
 
-@pytest.mark.parametrize("lead", [(1,), (8,), (2, 16), (32,)])
+@pytest.mark.parametrize("lead", [(1,), (8,), (2, 16), (32,), (3, 25)])
 def test_weight_only_int4_linear(dev, lead):
     """WeightOnlyInt4Linear (the drop-in for reference engine/quantize.py:483-525) at M = 1
-    (the GEMV) and M up to 32 (the GEMM, leading dimensions flattened) against the oracle's
+    (the GEMV), M up to 32 (one GEMM launch, leading dimensions flattened) and M = 75 (three
+    launches of up to 32 rows, as gpt-fast's prefill passes a whole prompt) against the oracle's
     linear on the dequantised weights; its buffers hold the quantised values exactly."""
     from flint_amd.quantize import WeightOnlyInt4Linear, unpack_q, unpack_sz
     from oracle import quant
@@ -161,7 +162,7 @@ def test_weight_only_int4_linear(dev, lead):
     log(f"WeightOnlyInt4Linear lead={lead}: max|diff|={diff:.3e} mismatch={mism:.2e}")
     assert mism < 2e-3 and diff <= 2.0 ** -7 * float(ref.float().abs().max())
     with pytest.raises(Exception):
-        mod(torch.zeros(33, k, dtype=torch.bfloat16, device=dev))
+        mod(torch.zeros(4, k + 128, dtype=torch.bfloat16, device=dev))  # wrong inner dimension
 
 
 def test_scales_and_zeros_gptfast_layout(dev):
