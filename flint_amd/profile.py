@@ -105,7 +105,10 @@ def analyse(buf, grid, slots, n_layer, nh=0, nkv=0):
     names = {-1: "no attention"}
     names.update({c: f"attention slice {c}" for c in range(int(cls.max()) + 1)})
     lag = {}
-    for pname, k in (("qkv", 1), ("attention", 5), ("o", 7), ("gateup", 9), ("down", 11)):
+    # one class (no workgroup's key loop was stamped apart from its merge, as in the verify
+    # kernel's attention by tokens) says nothing: no table then
+    for pname, k in (() if int(cls.min()) == int(cls.max()) else
+                     (("qkv", 1), ("attention", 5), ("o", 7), ("gateup", 9), ("down", 11))):
         end = lay[..., k]                                   # [grid, L]
         rel = end - end.median(0).values                    # lag behind the median workgroup
         last = end.argmax(0)                                # [L] the last workgroup per layer
