@@ -192,16 +192,20 @@ def handoff_probe(dev, words=2560, rounds=2000):
 
 
 def dequant_rate(dev, iters=2000):
-    """Compute rate of the exact dequantisation plus an M = 8 MFMA product with every weight
-    already in registers (fl_probe_dequant): the row layout on the vector ALUs (k_verify's tile
-    product) and the tiled layout on the matrix cores, in weights per second over the slowest
-    workgroup, beside the rate at which HBM delivers int4 weights with their scale/zero words
-    (8 TB/s / 0.53125 B per weight)."""
+    """Compute rate of the exact dequantisation with every weight already in registers
+    (fl_probe_dequant), in weights per second over the slowest workgroup, beside the rate at which
+    HBM delivers int4 weights with their scale/zero words (8 TB/s / 0.53125 B per weight). With an
+    M = 8 MFMA product: the row layout on the vector ALUs (k_verify's tile product), the tiled
+    layout on 16x16x16 MFMAs (fl_gemv_int4_tiled's unit_dot) and the same batched over a unit's
+    tiles; with an M = 1 dot on the vector ALUs (the decode kernel's form): dq32 and the
+    lane-local 4x4x4-MFMA dq32_mx."""
     from flint_amd import _lib
     import ctypes
     grid = ctypes.c_int32()
     res = {"hbm_tweights_s": round(HBM_PEAK_GBS * 1e9 / (0.5 + 4 / 128) / 1e12, 2)}
-    for mode, name in ((0, "row_valu_tweights_s"), (1, "tiled_mfma_tweights_s")):
+    for mode, name in ((0, "row_valu_tweights_s"), (1, "tiled_mfma_tweights_s"),
+                       (2, "tiled_mfma_batched_tweights_s"), (3, "m1_row_valu_tweights_s"),
+                       (4, "m1_row_mfma4_tweights_s")):
         out = torch.zeros(2 * 1024, dtype=torch.int64, device=dev)
         for _ in range(2):      # the first call loads the code object
             _lib.call("fl_probe_dequant", mode, iters, _lib.ptr(out), ctypes.byref(grid), _lib.stream_ptr())

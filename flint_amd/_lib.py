@@ -24,7 +24,7 @@ GROUP = 128
 
 # every symbol include/flint_amd.h declares
 EXPORTS = [
-    "fl_version", "fl_device_info", "fl_quantize_int4", "fl_dequant_int4", "fl_gemv_int4",
+    "fl_version", "fl_device_info", "fl_quantize_int4", "fl_dequant_int4", "fl_dequant_int4_mx", "fl_gemv_int4",
     "fl_gemm_int4", "fl_state_create", "fl_state_destroy", "fl_state_reset", "fl_state_check",
     "fl_state_profile", "fl_state_buffers", "fl_state_set_wait_limit",
     "fl_state_force_timeout",
@@ -78,6 +78,7 @@ def load(path=LIB_PATH):
         "fl_device_info": ([vp, vp], i32),
         "fl_quantize_int4": ([vp, vp, vp, i32, i32, vp], i32),
         "fl_dequant_int4": ([vp, vp, vp, i32, i32, vp], i32),
+        "fl_dequant_int4_mx": ([vp, vp, vp, i32, i32, vp], i32),
         "fl_gemv_int4": ([vp, vp, vp, vp, i32, i32, vp], i32),
         "fl_gemm_int4": ([vp, vp, vp, vp, i32, i32, i32, vp], i32),
         "fl_state_create": ([ctypes.POINTER(ModelDesc), i32, vp, vp, ctypes.POINTER(vp)], i32),

@@ -5,6 +5,7 @@
 #include "../../include/flint_amd.h"
 
 typedef __bf16 fl_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float fl_f32x4 __attribute__((ext_vector_type(4)));
 
 #define FL_WAVE 64
 
@@ -131,12 +132,101 @@ __device__ __forceinline__ void dq32(const uint4 w, const DqConst& k, uint32_t (
   dq_step4<true>(a, b, c, e, k, magic, one_lo, one_hi, d[3]);
 }
 
+// ---- the same dequantisation on 4x4x4 matrix-core steps, lane by lane --------------------------
+// v_mfma_f32_4x4x4_16b_bf16 runs 16 independent 4x4x4 products, block b on lanes 4b..4b+3:
+// row i of A comes from lane 4b + i and column j of B from lane 4b + j (their 4 bf16 along k),
+// and lane 4b + j receives column j of D (its 4 fp32 along i) (checked on the GPU). With B = a
+// lane's own 4 values and A = diag(s) (lane 4b + i puts s at k = i), lane j receives s * B_j[i]
+// in slot i: an elementwise product, exact for bf16 inputs, with C added once. So
+//   D1 = diag(s) . (128 + q) + (-136 s)  = (q - 8) s exactly (one nonzero product, as in dq_step4),
+//   D2 = I . bf16(D1) + z               = fp32(bf16(D1) + z), the reference's fp32 add,
+// each rounded to bf16 by v_cvt_pk_bf16_f32: the same bits as dq32, in 16 matrix-core steps and
+// 28 vector instructions (plus the per-group constants) per 32 weights instead of 124. The
+// diagonal is lane 4b + i's own scale, so the four lanes of every block must hold chunks with the
+// same (scale, zero) word -- 4 consecutive lanes on 4 chunks of one 128-group of one row -- and
+// all 64 lanes must run it together (wave-uniform control flow).
+typedef short fl_s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ fl_s16x4 mx_s4(uint32_t lo, uint32_t hi) {
+  return __builtin_bit_cast(fl_s16x4, make_uint2(lo, hi));
+}
+struct MxLane {      // this lane's diagonal slot (lane & 3) as masks over the 4 bf16 of an operand
+  uint32_t mlo, mhi;
+  uint32_t mask, magic;  // the AND-OR constants, kept in registers (see mx_lane)
+};
+__device__ __forceinline__ MxLane mx_lane() {
+  const int i = (int)(__lane_id() & 3);
+  MxLane m;
+  m.mlo = i == 0 ? 0x0000FFFFu : (i == 1 ? 0xFFFF0000u : 0u);
+  m.mhi = i == 2 ? 0x0000FFFFu : (i == 3 ? 0xFFFF0000u : 0u);
+  // (w & mask) | magic with both constants opaque to constant folding: the compiler emits one
+  // v_and_or_b32 and, seeing the instruction, keeps the wait states the matrix-core results
+  // around it need (an and-or written as inline asm would hide them from it)
+  m.mask = 0x000F000Fu;
+  m.magic = 0x43004300u;
+  asm volatile("" : "+v"(m.mask));
+  asm volatile("" : "+v"(m.magic));
+  return m;
+}
+__device__ __forceinline__ void dq32_mx(const uint4 w, uint32_t szw, const MxLane& m, uint32_t (&d)[4][4]) {
+  const uint32_t sb = szw & 0xFFFFu, sp = sb | (sb << 16);
+  const fl_s16x4 as = mx_s4(sp & m.mlo, sp & m.mhi);
+  const fl_s16x4 ai = mx_s4(0x3F803F80u & m.mlo, 0x3F803F80u & m.mhi);  // bf16 1.0 on the diagonal
+  const float c1v = -136.0f * bf2f(sb), zv = bf2f(szw >> 16);
+  const fl_f32x4 c1 = {c1v, c1v, c1v, c1v}, c2 = {zv, zv, zv, zv};
+  uint32_t v[4] = {w.x, w.y, w.z, w.w};
+  fl_f32x4 t[8];  // t[2j + h]: nibble step j of words 2h, 2h + 1
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t r0 = (v[2 * h] & m.mask) | m.magic, r1 = (v[2 * h + 1] & m.mask) | m.magic;
+      t[2 * j + h] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(as, mx_s4(r0, r1), c1, 0, 0, 0);
+    }
+    if (j < 3) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] >>= 4;
+    }
+  }
+  uint32_t a[8][2];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    a[u][0] = pack_bf16x2(t[u][0], t[u][1]);
+    a[u][1] = pack_bf16x2(t[u][2], t[u][3]);
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) t[u] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(ai, mx_s4(a[u][0], a[u][1]), c2, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      d[j][2 * h] = pack_bf16x2(t[2 * j + h][0], t[2 * j + h][1]);
+      d[j][2 * h + 1] = pack_bf16x2(t[2 * j + h][2], t[2 * j + h][3]);
+    }
+  }
+}
+
 // dot of one 16-byte chunk (32 int4 elements of one 128-group) with 32 bf16 x values
 // (16 packed pairs), accumulated into acc.
 __device__ __forceinline__ float chunk_dot(const uint4 w, uint32_t szw, const uint4* x4, float acc) {
   const uint4 x[4] = {x4[0], x4[1], x4[2], x4[3]};  // requested first: the dequantisation hides them
   uint32_t d[4][4];
   dq32(w, dq_const(szw), d);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc = dot2_bf16(d[0][i], x[i].x, acc);
+    acc = dot2_bf16(d[1][i], x[i].y, acc);
+    acc = dot2_bf16(d[2][i], x[i].z, acc);
+    acc = dot2_bf16(d[3][i], x[i].w, acc);
+  }
+  return acc;
+}
+
+// chunk_dot through dq32_mx (same bits; the four lanes of every 4-lane block on one 128-group
+// of one row, all lanes together)
+__device__ __forceinline__ float chunk_dot_mx(const uint4 w, uint32_t szw, const uint4* x4, float acc) {
+  const uint4 x[4] = {x4[0], x4[1], x4[2], x4[3]};
+  uint32_t d[4][4];
+  dq32_mx(w, szw, mx_lane(), d);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     acc = dot2_bf16(d[0][i], x[i].x, acc);
@@ -155,7 +245,6 @@ __device__ __forceinline__ float chunk_dot(const uint4 w, uint32_t szw, const ui
 // 32 k-values {128u + 32c + 8e + t}, so word e of the chunk is the B fragment and the matching
 // 16 bytes of each activation row the A fragment (a permuted k order; every k appears once).
 typedef __bf16 fl_bf16x8 __attribute__((ext_vector_type(8)));
-typedef float fl_f32x4 __attribute__((ext_vector_type(4)));
 
 // acc += X(rows, the chunk's 32 k) . W(this lane's row, same k)^T; d from dq32, xa[e] = 8 bf16
 // of this lane's activation row at k = 128u + 32c + 8e

@@ -464,6 +464,10 @@ __device__ void stage_tagged(const DecodeParams& p, const uint32_t* src, int n, 
 //  - by row pairs: 2^lg lanes per pair of rows 2p, 2p+1 (rp_lg); lane j's i-th chunk is chunk
 //    j + (i / 2) * 2^lg of row 2p + i % 2, so chunks 2k and 2k+1 of a thread cover the same 32
 //    activations: each read of x from LDS serves both rows (gate and up of one output).
+// Every mapping gives the four lanes of each 4-lane block the four chunks of one 128-group of one
+// row (or all four none), as the matrix-core dequantisation (dq32_mx) needs: cpr is a multiple
+// of 4, the strides are multiples of cpr or of NT, and the host admits the by-rows mappings only
+// with 2^lg >= 4 lanes per row (phase_fits).
 struct ChunkMap {
   bool by_rows;
   int S;    // by stride
@@ -576,7 +580,7 @@ __device__ __forceinline__ void gemv_predq(const uint4 (&wr)[MC], const uint32_t
 #pragma unroll
   for (int i = 0; i < PD; ++i) {  // chunk OFF + i into slot i
     uint32_t d[4][4];
-    dq32(wr[OFF + i], dq_const(sr[OFF + i]), d);
+    dq32_mx(wr[OFF + i], sr[OFF + i], mx_lane(), d);
 #pragma unroll
     for (int k = 0; k < 4; ++k) dql[(4 * i + k) * NT + tid] = make_uint4(d[k][0], d[k][1], d[k][2], d[k][3]);
     __builtin_amdgcn_sched_barrier(0);
@@ -591,7 +595,7 @@ __device__ __forceinline__ void gemv_predq_reg(const uint4 (&wr)[MC], const uint
   static_assert(PR >= 1 && OFF + PR <= MC, "pre-dequantised chunks");
 #pragma unroll
   for (int i = 0; i < PR; ++i) {
-    dq32(wr[OFF + i], dq_const(sr[OFF + i]), d[i]);
+    dq32_mx(wr[OFF + i], sr[OFF + i], mx_lane(), d[i]);
     __builtin_amdgcn_sched_barrier(0);
     between(i);
   }
@@ -683,11 +687,11 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
       const uint4 xr[4] = {x4[0], x4[1], x4[2], x4[3]};  // read once for both rows
       const int i = 2 * k;
       const bool ok = on && c < cpr;
-      const float ya = (i < PD) ? pre_dot(i, xr) : chunk_dot(wr[i], sr[i], xr, 0.0f);
+      const float ya = (i < PD) ? pre_dot(i, xr) : chunk_dot_mx(wr[i], sr[i], xr, 0.0f);
       acc_a += ok ? ya : 0.0f;
       next(i);
       __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time
-      const float yb = (i + 1 < PD) ? pre_dot(i + 1, xr) : chunk_dot(wr[i + 1], sr[i + 1], xr, 0.0f);
+      const float yb = (i + 1 < PD) ? pre_dot(i + 1, xr) : chunk_dot_mx(wr[i + 1], sr[i + 1], xr, 0.0f);
       acc_b += ok ? yb : 0.0f;
       next(i + 1);
       __builtin_amdgcn_sched_barrier(0);
@@ -711,7 +715,7 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
     for (int i = 0; i < MC; ++i) {
       const int c = lj + (i << lg);
       const uint4* x4 = reinterpret_cast<const uint4*>(xs) + xslot(4 * min(c, cpr - 1));
-      const float y = (i < PD) ? pre_dot(i, x4) : chunk_dot(wr[i], sr[i], x4, 0.0f);
+      const float y = (i < PD) ? pre_dot(i, x4) : chunk_dot_mx(wr[i], sr[i], x4, 0.0f);
       acc += (on && c < cpr) ? y : 0.0f;
       next(i);
       __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time; loads spread
@@ -733,7 +737,7 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
     for (int i = 0; i < MC; ++i) {
       const int f = tid + i * S;
       if (active && f < total)
-        part[f] = (i < PD) ? pre_dot(i, xr) : chunk_dot(wr[i], sr[i], xr, 0.0f);
+        part[f] = (i < PD) ? pre_dot(i, xr) : chunk_dot_mx(wr[i], sr[i], xr, 0.0f);
       next(i);
       __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time
     }
@@ -745,7 +749,7 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
       const int f = tid + i * S;
       const uint4* x4 = reinterpret_cast<const uint4*>(xs) + xslot(4 * c);
       if (active && f < total)
-        part[f] = (i < PD) ? pre_dot(i, x4) : chunk_dot(wr[i], sr[i], x4, 0.0f);
+        part[f] = (i < PD) ? pre_dot(i, x4) : chunk_dot_mx(wr[i], sr[i], x4, 0.0f);
       c += step;
       if (c >= cpr) c -= cpr;
       next(i);
@@ -3319,14 +3323,16 @@ int phase_fits(int n, int k, int G, int cap, int mode) {
   R += (R & 1);
   const int cpr = k >> 5;
   if (R > ROWS_MAX || cpr > NT) return 0;
+  // by rows / row pairs: at least 4 lanes per row, so each 4-lane block of the matrix-core
+  // dequantisation stays on one row
   if (mode == GM_ROWS) {
     int lg = 5;  // rs_lg
     while (lg > 0 && ((R << lg) > NT || (1 << (lg - 1)) >= cpr)) --lg;
-    return R <= NT && (cpr + (1 << lg) - 1) >> lg <= cap;
+    return lg >= 2 && R <= NT && (cpr + (1 << lg) - 1) >> lg <= cap;
   }
   if (mode == GM_PAIRS) {
     const int lg = rp_lg(R, cpr);
-    return R <= 2 * NT && 2 * ((cpr + (1 << lg) - 1) >> lg) <= cap;
+    return lg >= 2 && R <= 2 * NT && 2 * ((cpr + (1 << lg) - 1) >> lg) <= cap;
   }
   return mode == GM_COLUMN ? R <= (NT / cpr) * cap : (long)R * cpr <= (long)cap * NT;
 }

@@ -60,14 +60,26 @@ __global__ __launch_bounds__(256) void k_quantize(const uint16_t* __restrict__ w
 }
 
 // One thread per 16-byte chunk (4 packed words, 32 elements of one group): bf16 outputs through
-// the same dequantisation sequence the GEMVs use.
+// the same dequantisation sequence the GEMVs use -- dq32 on the vector ALUs (MX = false: the
+// M <= 32 GEMM of this file and the verify tiles) or dq32_mx on the matrix cores (MX = true: the
+// M = 1 GEMVs of this file and the decode kernel's). Threads 4b..4b+3 hold the four chunks of one group (nchunks is a
+// multiple of 4), as dq32_mx needs; every thread runs it (past the end on the last chunk) so
+// that all lanes of a wave run the matrix-core steps together.
+template <bool MX>
 __global__ __launch_bounds__(256) void k_dequant(const uint32_t* __restrict__ q,
                                                  const uint32_t* __restrict__ sz,
                                                  uint16_t* __restrict__ out, int64_t nchunks) {
   const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= nchunks) return;
+  if constexpr (!MX) {
+    if (c >= nchunks) return;
+  }
+  const int64_t cc = c < nchunks ? c : nchunks - 1;
   uint32_t d[4][4];
-  dq32(reinterpret_cast<const uint4*>(q)[c], dq_const(sz[c >> 2]), d);
+  if constexpr (MX)
+    dq32_mx(reinterpret_cast<const uint4*>(q)[cc], sz[cc >> 2], mx_lane(), d);
+  else
+    dq32(reinterpret_cast<const uint4*>(q)[cc], dq_const(sz[cc >> 2]), d);
+  if (c >= nchunks) return;
   uint4* o = reinterpret_cast<uint4*>(out + c * 32);
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = make_uint4(d[0][i], d[1][i], d[2][i], d[3][i]);
@@ -75,8 +87,9 @@ __global__ __launch_bounds__(256) void k_dequant(const uint32_t* __restrict__ q,
 
 // M=1 GEMV. A workgroup owns `rows_per_wg` consecutive rows, whose packed words form one
 // contiguous block; its 16-byte chunks (32 elements each) are dealt round-robin over the
-// threads so that every thread gets the same number of chunks and every load is coalesced.
-// Per-chunk partial sums go to LDS and each row is summed there in a fixed order.
+// threads so that every thread gets the same number of chunks and every load is coalesced
+// (threads 4b..4b+3 take the four chunks of one group, as the matrix-core dequantisation's lane
+// blocks need). Per-chunk partial sums go to LDS and each row is summed there in a fixed order.
 constexpr int kGemvThreads = 256;
 constexpr int kGemvMaxChunks = 8;  // per thread
 
@@ -117,7 +130,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(const uint32_t* __restric
     const int f = tid + i * kGemvThreads;
     if (f < total) {
       const uint4* x4 = reinterpret_cast<const uint4*>(xs + c * 32);
-      part[f] = chunk_dot(wr[i], sr[i], x4, 0.0f);
+      part[f] = chunk_dot_mx(wr[i], sr[i], x4, 0.0f);
     }
     c += step;
     if (c >= cpr) c -= cpr;
@@ -144,7 +157,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(const uint32_t* __restric
 // vector is staged in LDS once per workgroup (its requests go out first, ahead of the weights,
 // so the first tile does not wait behind them). A row's partial sums meet in a DPP reduction
 // over its lanes (fixed order); its first lane writes y. All loads are range-checked buffer
-// loads (tiles past N read zeros and store nothing), so no load sits under a branch.
+// loads (tiles past N read zeros and store nothing), so no load sits under a branch. With 16 or
+// 64 lanes per row, lanes 4b..4b+3 always hold the four chunks of one group (dq32_mx's blocks).
 constexpr int GV_NW = 8;
 constexpr int GV_NT = GV_NW * 64;
 constexpr int GV_WG = 2;  // workgroups per CU (four waves per SIMD hide more of the HBM latency than
@@ -173,7 +187,7 @@ __device__ __forceinline__ void gv_tile(const uint4* xs, int t, int n, const uin
 #pragma unroll
   for (int i = 0; i < C; ++i) {
     const int c = j + (i << LG);
-    acc = chunk_dot(w[i], s[i], xs + 5 * c, acc);  // chunk c's 4 x slots start at 5c (bank spread)
+    acc = chunk_dot_mx(w[i], s[i], xs + 5 * c, acc);  // chunk c's 4 x slots start at 5c (bank spread)
     __builtin_amdgcn_sched_barrier(0);              // one chunk's temporaries live at a time
   }
   acc = group_sum(acc, 1 << LG);
@@ -307,7 +321,18 @@ int fl_dequant_int4(const uint32_t* q, const uint32_t* sz, uint16_t* out, int32_
   const int64_t nchunks = (int64_t)n * (k / 32);
   const int64_t blocks = (nchunks + 255) / 256;
   if (blocks > 0x7FFFFFFF) return FL_E_ARG;
-  hipLaunchKernelGGL(k_dequant, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), q, sz,
+  hipLaunchKernelGGL(k_dequant<false>, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), q, sz,
+                     out, nchunks);
+  return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
+}
+
+int fl_dequant_int4_mx(const uint32_t* q, const uint32_t* sz, uint16_t* out, int32_t n, int32_t k,
+                       void* stream) {
+  if (!q || !sz || !out || n <= 0 || k <= 0 || (k % FL_GROUP) != 0) return FL_E_ARG;
+  const int64_t nchunks = (int64_t)n * (k / 32);
+  const int64_t blocks = (nchunks + 255) / 256;
+  if (blocks > 0x7FFFFFFF) return FL_E_ARG;
+  hipLaunchKernelGGL(k_dequant<true>, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), q, sz,
                      out, nchunks);
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }

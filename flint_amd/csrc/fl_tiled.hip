@@ -28,8 +28,6 @@
 
 namespace {
 
-typedef short fl_s16x4 __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ fl_s16x4 s4(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(fl_s16x4, make_uint2(lo, hi));
 }
@@ -106,6 +104,42 @@ __device__ __forceinline__ void tile_dq(uint32_t r0, uint32_t r1, const GroupK& 
   const fl_f32x4 d2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(s4(ilo, ihi), s4(a0, a1), k.c2, 0, 0, 0);
   o0 = pack_bf16x2(d2[0], d2[1]);
   o1 = pack_bf16x2(d2[2], d2[3]);
+}
+
+// The 8 tiles of one unit (this lane's 16 bytes w) dequantised with the steps batched across the
+// tiles: the 8 D1 MFMAs, then their roundings, then the 8 D2 MFMAs, then theirs, so no rounding
+// waits on the MFMA issued just before it. o[t] = tile_dq's (o0, o1) of tile t.
+__device__ __forceinline__ void unit_dq_batched(uint4 w, const GroupK& k, uint32_t ilo, uint32_t ihi,
+                                                uint32_t (&o)[8][2]) {
+  auto mm = [](uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, fl_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(s4(a0, a1), s4(b0, b1), c, 0, 0, 0);
+  };
+  const AndOrK ao = and_or_k();
+  uint32_t wa = w.x, wb = w.y, wc = w.z, wd = w.w;
+  fl_f32x4 d[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    uint32_t& lo = t < 4 ? wa : wb;
+    uint32_t& hi = t < 4 ? wc : wd;
+    const uint32_t r0 = and_or(lo, ao), r1 = and_or(hi, ao);
+    lo >>= 4;
+    hi >>= 4;
+    d[t] = mm(r0, r1, k.b1lo, k.b1hi, k.c1);
+  }
+  uint32_t a[8][2];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    a[t][0] = pack_bf16x2(d[t][0], d[t][1]);
+    a[t][1] = pack_bf16x2(d[t][2], d[t][3]);
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+    d[t] = mm(ilo, ihi, a[t][0], a[t][1], k.c2);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    o[t][0] = pack_bf16x2(d[t][0], d[t][1]);
+    o[t][1] = pack_bf16x2(d[t][2], d[t][3]);
+  }
 }
 
 // One 1 KB unit (16 rows x one 128-group) of the tiled matrix, dequantised and dotted with x:
@@ -270,7 +304,10 @@ __global__ __launch_bounds__(256) void k_dequant_tiled(const uint4* __restrict__
 // rows in LDS -- k_verify's tile product at M = 8 with the weights already there. MODE 0: this
 // library's row layout, dequantised on the vector ALUs (dq32, four 16x16x32 MFMAs per 32 weights:
 // k_verify's tile_mma); MODE 1: the tiled layout, both exact fp32 steps on 16x16x16 MFMAs and the
-// dot on a 16x16x32 MFMA per two tiles (unit_dot with token rows in place of the one x row).
+// dot on a 16x16x32 MFMA per two tiles (unit_dot with token rows in place of the one x row);
+// MODE 2: MODE 1's arithmetic with each step batched over the unit's 8 tiles (unit_dq_batched);
+// MODES 3 / 4: M = 1 as the decode kernel computes it, one row-layout chunk per lane dotted with x
+// on the vector ALUs, dequantised by dq32 (3) or by the lane-local matrix-core dq32_mx (4).
 // out[2 wg] = the workgroup's 100 MHz ticks, out[2 wg + 1] = bits of its result (kept so the
 // work is not dropped).
 constexpr int PDQ_NU = 3, PDQ_LD = 392;  // units per wave; token-row pitch (bf16)
@@ -297,6 +334,7 @@ __global__ __launch_bounds__(512, 1) void k_probe_dequant(int iters, unsigned lo
   }
   const int r = lane & 15, c = lane >> 4;
   fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const MxLane mxl = mx_lane();
   __syncthreads();
   const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
   for (int it = 0; it < iters; ++it) {
@@ -312,6 +350,42 @@ __global__ __launch_bounds__(512, 1) void k_probe_dequant(int iters, unsigned lo
         uint32_t d[4][4];
         dq32(w[u], dq_const(s[u]), d);
         mfma_chunk(d, xa, acc);
+      } else if constexpr (MODE == 3 || MODE == 4) {
+        // M = 1, decode's form: one row chunk per lane dotted with x on the vector ALUs
+        const uint16_t* xrow = xs + c * 32 + u * 128;
+        uint4 xa[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xa[e] = *reinterpret_cast<const uint4*>(xrow + e * 8);
+        uint32_t d[4][4];
+        if constexpr (MODE == 3)
+          dq32(w[u], dq_const(s[u]), d);
+        else
+          dq32_mx(w[u], s[u], mxl, d);
+        float a = acc[0];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a = dot2_bf16(d[0][i], xa[i].x, a);
+          a = dot2_bf16(d[1][i], xa[i].y, a);
+          a = dot2_bf16(d[2][i], xa[i].z, a);
+          a = dot2_bf16(d[3][i], xa[i].w, a);
+        }
+        acc[0] = a;
+      } else if constexpr (MODE == 2) {
+        const int b = lane >> 4, cc = lane & 15, dd = cc - 4 * b;
+        const GroupK k = group_k(s[u], dd);
+        const uint32_t one = 0x3F80u;
+        const uint32_t ilo = dd == 0 ? one : (dd == 1 ? one << 16 : 0u), ihi = dd == 2 ? one : (dd == 3 ? one << 16 : 0u);
+        uint32_t o[8][2];
+        unit_dq_batched(w[u], k, ilo, ihi, o);
+        const uint16_t* xrow = xs + (cc < 8 ? cc : 16) * PDQ_LD + u * 128 + 4 * b;
+#pragma unroll
+        for (int tp = 0; tp < 4; ++tp) {
+          const uint2 xa = *reinterpret_cast<const uint2*>(xrow + 32 * tp);
+          const uint2 xb = *reinterpret_cast<const uint2*>(xrow + 32 * tp + 16);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b8(xa.x, xa.y, xb.x, xb.y),
+                                                        b8(o[2 * tp][0], o[2 * tp][1], o[2 * tp + 1][0], o[2 * tp + 1][1]),
+                                                        acc, 0, 0, 0);
+        }
       } else {
         const int b = lane >> 4, cc = lane & 15;  // tiled lane (b, c): rows 4b..4b+3, column c
         const GroupK k = group_k(s[u], cc - 4 * b);
@@ -400,7 +474,7 @@ int fl_gemv_int4_tiled(const uint32_t* qt, const uint32_t* sz, const uint16_t* x
 }
 
 int fl_probe_dequant(int32_t mode, int32_t iters, uint64_t* out, int32_t* grid, void* stream) {
-  if (mode < 0 || mode > 1 || iters < 1 || iters > 1000000 || !out || !grid) return FL_E_ARG;
+  if (mode < 0 || mode > 4 || iters < 1 || iters > 1000000 || !out || !grid) return FL_E_ARG;
   int dev = 0, cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu < 1)
@@ -409,8 +483,14 @@ int fl_probe_dequant(int32_t mode, int32_t iters, uint64_t* out, int32_t* grid, 
   auto* o = reinterpret_cast<unsigned long long*>(out);
   if (mode == 0)
     hipLaunchKernelGGL(k_probe_dequant<0>, dim3(cu), dim3(512), 0, as_stream(stream), (int)iters, o);
-  else
+  else if (mode == 1)
     hipLaunchKernelGGL(k_probe_dequant<1>, dim3(cu), dim3(512), 0, as_stream(stream), (int)iters, o);
+  else if (mode == 2)
+    hipLaunchKernelGGL(k_probe_dequant<2>, dim3(cu), dim3(512), 0, as_stream(stream), (int)iters, o);
+  else if (mode == 3)
+    hipLaunchKernelGGL(k_probe_dequant<3>, dim3(cu), dim3(512), 0, as_stream(stream), (int)iters, o);
+  else
+    hipLaunchKernelGGL(k_probe_dequant<4>, dim3(cu), dim3(512), 0, as_stream(stream), (int)iters, o);
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
 

@@ -35,13 +35,15 @@ def quantize_int4(w, q=None, sz=None):
     return q, sz
 
 
-def dequantize_int4(q, sz):
-    """Bit-exact bf16 [N, K] dequantisation (the GEMVs' own device routine)."""
+def dequantize_int4(q, sz, matrix_cores=False):
+    """Bit-exact bf16 [N, K] dequantisation through the kernels' own device routine: the vector-ALU
+    form (M = 1 GEMV kernels, verify tiles) or, with matrix_cores, the decode GEMVs' MFMA form."""
     _check_dev(q, torch.int32, "q")
     _check_dev(sz, torch.int32, "sz")
     n, k = q.shape[0], q.shape[1] * 8
     out = torch.empty(n, k, dtype=torch.bfloat16, device=q.device)
-    _lib.call("fl_dequant_int4", _lib.ptr(q), _lib.ptr(sz), _lib.ptr(out), n, k, _lib.stream_ptr())
+    _lib.call("fl_dequant_int4_mx" if matrix_cores else "fl_dequant_int4", _lib.ptr(q), _lib.ptr(sz),
+              _lib.ptr(out), n, k, _lib.stream_ptr())
     return out
 
 

@@ -37,6 +37,7 @@ def test_argument_errors_without_gpu():
     lib = _lib.load()
     assert lib.fl_quantize_int4(None, None, None, 16, 128, None) == -1
     assert lib.fl_dequant_int4(None, None, None, 16, 128, None) == -1
+    assert lib.fl_dequant_int4_mx(None, None, None, 16, 128, None) == -1
     p = ctypes.c_void_p(16)
     assert lib.fl_gemv_int4(p, p, p, p, 16, 100, None) == -1       # K not a multiple of 128
     assert lib.fl_gemv_int4(p, p, p, p, 0, 128, None) == -1
@@ -54,7 +55,7 @@ def test_argument_errors_without_gpu():
     assert lib.fl_probe_handoff(3 | 4 << 8, 64, 10, p, ctypes.byref(g), None) == -1   # depth 4
     assert lib.fl_probe_handoff(3 | 1 << 8, 66, 10, p, ctypes.byref(g), None) == -1   # 66 % 4
     assert lib.fl_probe_handoff(1 | 1 << 8, 64, 10, p, ctypes.byref(g), None) == -1   # extra bits
-    assert lib.fl_probe_dequant(2, 10, p, ctypes.byref(g), None) == -1                 # no mode 2
+    assert lib.fl_probe_dequant(5, 10, p, ctypes.byref(g), None) == -1                 # no mode 5
     assert lib.fl_probe_dequant(0, 0, p, ctypes.byref(g), None) == -1                 # iters >= 1
 
 

@@ -41,16 +41,41 @@ def test_quantize_bit_exact(dev, n, k):
         assert torch.equal(z.cpu().view(torch.int16), zo.view(torch.int16))
 
 
+@pytest.mark.parametrize("matrix_cores", [False, True])
 @pytest.mark.parametrize("n,k", SHAPES)
-def test_dequant_bit_exact(dev, n, k):
+def test_dequant_bit_exact(dev, n, k, matrix_cores):
+    """Both device forms of the dequantisation (vector ALUs; 4x4x4 MFMAs lane by lane, the decode
+    GEMVs') give the oracle's bits, edge groups (scale clamp, outlier, two values) included."""
     from flint_amd.quantize import quantize_int4, dequantize_int4
     from oracle import quant
     w = _weights(n, k, 2, "edge")
-    log(f"dequant n={n} k={k}")
+    log(f"dequant n={n} k={k} matrix_cores={matrix_cores}")
     q, sz = quantize_int4(w.to(dev))
-    dq = dequantize_int4(q, sz).cpu()
+    dq = dequantize_int4(q, sz, matrix_cores).cpu()
     ref = quant.dq_linear_weight(w)
     assert torch.equal(dq.view(torch.int16), ref.view(torch.int16))
+
+
+def test_dequant_mx_extreme_scales(dev):
+    """The matrix-core form on hand-set (scale, zero) words across the bf16 range -- tiny and huge
+    scales, zeros of both signs and magnitudes that make the fp32 add round -- against the vector
+    form, every nibble value in every position."""
+    from flint_amd.quantize import dequantize_int4
+    g = torch.Generator().manual_seed(11)
+    n, k = 64, 512
+    q = torch.randint(-2**31, 2**31 - 1, (n, k // 8), generator=g, dtype=torch.int64).to(torch.int32)
+    q[0] = 0x76543210
+    q[1] = -0x789abcdf   # 0x87654321 as int32
+    s = torch.tensor([1e-30, 3e-8, 1e-6, 2.5e-3, 0.02, 1.0, 7.5, 3e4, 1e30], dtype=torch.float32)
+    z = torch.tensor([0.0, -0.0, 1e-30, -2.5e-3, 0.6, -1.0, 200.0, -3e4, 1e30], dtype=torch.float32)
+    si = torch.randint(0, len(s), (n, k // 128), generator=g)
+    zi = torch.randint(0, len(z), (n, k // 128), generator=g)
+    sb = s[si].to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
+    zb = z[zi].to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
+    sz = (sb | (zb << 16)).to(torch.int32)
+    a = dequantize_int4(q.to(dev), sz.to(dev), False).cpu()
+    b = dequantize_int4(q.to(dev), sz.to(dev), True).cpu()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
 @pytest.mark.parametrize("n,k", SHAPES)

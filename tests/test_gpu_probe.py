@@ -30,9 +30,9 @@ def test_probe_handoff_modes(dev, mode, words):
         f"xcd = blockIdx % 8: {all(x == i % 8 for i, x in enumerate(xcc))}")
 
 
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
 def test_probe_dequant_modes(dev, mode):
-    """The dequantisation-rate probe (fl_probe_dequant) runs both forms to completion with a
+    """The dequantisation-rate probe (fl_probe_dequant) runs every form to completion with a
     positive time in every workgroup; the rate is logged (and reported by bench.py)."""
     from flint_amd import _lib
     grid = ctypes.c_int32()
