@@ -58,6 +58,8 @@ class Weights(ctypes.Structure):
         ("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p),
         ("final_norm", ctypes.c_void_p), ("embed", ctypes.c_void_p), ("rope", ctypes.c_void_p),
         ("rope_len", ctypes.c_int32),
+        ("wqkv_t", ctypes.c_void_p), ("wo_t", ctypes.c_void_p),
+        ("wgu_t", ctypes.c_void_p), ("wd_t", ctypes.c_void_p),
     ]
 
 

@@ -6,6 +6,7 @@
 
 typedef __bf16 fl_bf16x2 __attribute__((ext_vector_type(2)));
 typedef float fl_f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 fl_bf16x8 __attribute__((ext_vector_type(8)));
 
 #define FL_WAVE 64
 
@@ -221,6 +222,70 @@ __device__ __forceinline__ float chunk_dot(const uint4 w, uint32_t szw, const ui
   return acc;
 }
 
+// ---- the same on the tiled layout (fl_tile_int4): four rows of one column per lane ----------
+// Lane L's 16 bytes of a 1 KB unit (16 rows x one 128-group) hold rows 4p..4p+3, p = (L / 4) % 4,
+// at columns c + 16t, c = 4 (L / 16) + L % 4, t = 0..7 (tile t: words 0 / 1 rows 4p, 4p+1 at bits
+// 4(t%4), 16 + 4(t%4) for t < 4 / t >= 4; words 2 / 3 rows 4p+2, 4p+3). Per tile, the 4x4x4 block
+// of lanes 4b..4b+3 is a transpose: D1 = A . diag(s) + C1 with A = the lane's (128 + q) of four
+// rows and B = diag(s of row L % 16 in slot L % 4), so lane L receives row L % 16 at columns
+// 4 (L / 16) + 0..3 times its own row's scale; D2 = I . t + z as in dq32_mx. o[t] = the bf16 pairs
+// (columns 4 (L / 16) + 0,1 / + 2,3 of tile t) of row L % 16, the B fragment of a 16x16x32 dot
+// over tiles t, t + 1. The steps run NB tiles at a time (NB = 8: every rounding waits on an MFMA
+// issued 8 instructions earlier).
+template <int NB>
+__device__ __forceinline__ void unit_dq_t(const uint4 w, uint32_t szw, const MxLane& m, uint32_t (&o)[8][2]) {
+  static_assert(NB == 2 || NB == 4 || NB == 8, "tiles per batch");
+  const uint32_t sb = szw & 0xFFFFu, sp = sb | (sb << 16);
+  const fl_s16x4 bs = mx_s4(sp & m.mlo, sp & m.mhi);
+  const fl_s16x4 ai = mx_s4(0x3F803F80u & m.mlo, 0x3F803F80u & m.mhi);
+  const float c1v = -136.0f * bf2f(sb), zv = bf2f(szw >> 16);
+  const fl_f32x4 c1 = {c1v, c1v, c1v, c1v}, c2 = {zv, zv, zv, zv};
+  uint32_t v[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int t0 = 0; t0 < 8; t0 += NB) {
+    fl_f32x4 d[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int t = t0 + u;
+      const uint32_t lo = v[t >> 2] >> (4 * (t & 3)), hi = v[2 + (t >> 2)] >> (4 * (t & 3));
+      d[u] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(mx_s4((lo & m.mask) | m.magic, (hi & m.mask) | m.magic),
+                                                    bs, c1, 0, 0, 0);
+    }
+    uint32_t a[NB][2];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      a[u][0] = pack_bf16x2(d[u][0], d[u][1]);
+      a[u][1] = pack_bf16x2(d[u][2], d[u][3]);
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) d[u] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(ai, mx_s4(a[u][0], a[u][1]), c2, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      o[t0 + u][0] = pack_bf16x2(d[u][0], d[u][1]);
+      o[t0 + u][1] = pack_bf16x2(d[u][2], d[u][3]);
+    }
+  }
+}
+// acc += X . dq^T over one tiled unit: xr = this lane's activation row (token L % 16, or a zero
+// row) at the unit's group, plus 4 (L / 16); the 16x16x32 dot of tiles 2tp, 2tp + 1 takes x at
+// columns 32tp + 4 (L / 16) + 0..3 and 32tp + 16 + 4 (L / 16) + 0..3 (its k = 8 (L / 16) + e).
+// acc: lane L holds row L % 16 for tokens 4 (L / 16) + 0..3.
+template <int NB>
+__device__ __forceinline__ void unit_mma_t(const uint4 w, uint32_t szw, const MxLane& m, const uint16_t* xr,
+                                           fl_f32x4& acc) {
+  uint32_t o[8][2];
+  unit_dq_t<NB>(w, szw, m, o);
+#pragma unroll
+  for (int tp = 0; tp < 4; ++tp) {
+    const uint2 xa = *reinterpret_cast<const uint2*>(xr + 32 * tp);
+    const uint2 xb = *reinterpret_cast<const uint2*>(xr + 32 * tp + 16);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        __builtin_bit_cast(fl_bf16x8, make_uint4(xa.x, xa.y, xb.x, xb.y)),
+        __builtin_bit_cast(fl_bf16x8, make_uint4(o[2 * tp][0], o[2 * tp][1], o[2 * tp + 1][0], o[2 * tp + 1][1])),
+        acc, 0, 0, 0);
+  }
+}
+
 // chunk_dot through dq32_mx (same bits; the four lanes of every 4-lane block on one 128-group
 // of one row, all lanes together)
 __device__ __forceinline__ float chunk_dot_mx(const uint4 w, uint32_t szw, const uint4* x4, float acc) {
@@ -244,7 +309,6 @@ __device__ __forceinline__ float chunk_dot_mx(const uint4 w, uint32_t szw, const
 // (r = l%16, c = l/16) holds chunk c of group u of weight row r, and MFMA step e contracts the
 // 32 k-values {128u + 32c + 8e + t}, so word e of the chunk is the B fragment and the matching
 // 16 bytes of each activation row the A fragment (a permuted k order; every k appears once).
-typedef __bf16 fl_bf16x8 __attribute__((ext_vector_type(8)));
 
 // acc += X(rows, the chunk's 32 k) . W(this lane's row, same k)^T; d from dq32, xa[e] = 8 bf16
 // of this lane's activation row at k = 128u + 32c + 8e
@@ -315,6 +379,9 @@ __device__ __forceinline__ uint2 buf_ld64(__amdgpu_buffer_rsrc_t r, uint32_t off
 // relaxed atomic load); each aligned dword of the result is read atomically
 __device__ __forceinline__ uint4 buf_ld128_coh(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
+}
+__device__ __forceinline__ uint2 buf_ld64_coh(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 16));
 }
 
 // Workgroup barrier that orders LDS accesses only. __syncthreads also waits for every global

@@ -1903,6 +1903,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(DecodeParams pv) {
 // stay tagged words. Each workgroup keeps its own 16 rows of the residual in LDS for the whole
 // launch, as k_decode keeps them in registers.
 constexpr int VH = 16;  // token rows per pass through a GEMM phase (one MFMA row block)
+constexpr int VT_NB = 8;  // tiles per batch of the tile dequantisation steps (unit_mma_t)
 
 // Verify attention (see attention_verify): keys per load round VRK; LDS regions of a unit, in
 // bytes from the region's start.
@@ -2190,51 +2191,49 @@ __device__ __forceinline__ void stage_norm_rows(const uint16_t* src, int m0, int
   lds_barrier();
 }
 
-// The weights of one 16-row tile of an [N, K] int4 matrix over the K groups g0 .. g0+ng-1
-// (ng <= NWAVE * TW_G): this wave's groups g0 + wave + 8i, one 16-byte quarter-group per lane. Loading
-// does not depend on the token rows, so QKV and gate/up request tiles before they wait for their
-// inputs, and every phase requests the next tile before it computes the current one. Loads
-// complete in order: rows staged after a tile's request arrive only after that tile (measured
-// faster all the same in every phase: the tiles arrive during the wait).
+// The weights of one 16-row tile of an [N, K] int4 matrix in the tiled layout (fl_tile_int4:
+// 1 KB per 16 rows x 128-group unit, 16 bytes per lane) over the K groups g0 .. g0+ng-1
+// (ng <= NWAVE * TW_G): this wave's groups g0 + wave + 8i, one unit each. rows = 16, or 0 to
+// request nothing (every load past the range reads zeros). Loading does not depend on the token
+// rows, so QKV and gate/up request tiles before they wait for their inputs, and every phase
+// requests the next tile before it computes the current one. Loads complete in order: rows
+// staged after a tile's request arrive only after that tile (measured faster all the same in
+// every phase: the tiles arrive during the wait).
 constexpr int TW_G = 3;  // K groups per wave of a tile: D <= 3072 is at most 24 groups, 3 per wave
 static_assert(TW_G * NWAVE * 128 >= 64 * 8 * LM_MAXC, "a tile's K groups fit TW_G per wave at the largest D");
 struct TileW {
   uint4 w[TW_G];
   uint32_t s[TW_G];
 };
-__device__ __forceinline__ void tile_load(const uint32_t* __restrict__ q, const uint32_t* __restrict__ sz,
+__device__ __forceinline__ void tile_load(const uint32_t* __restrict__ qt, const uint32_t* __restrict__ sz,
                                           int n0, int rows, int K, int g0, int ng, TileW& tw) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
-  const int r = lane & 15, c = lane >> 4;
+  const int r = lane & 15;
   const int groups = K >> 7;
-  const auto wr = buf_rsrc(q + (size_t)n0 * (K >> 3), (uint32_t)rows * (uint32_t)(K >> 1));
+  const auto wr = buf_rsrc(qt + (size_t)n0 * (K >> 3), (uint32_t)rows * (uint32_t)(K >> 1));
   const auto sr = buf_rsrc(sz + (size_t)n0 * groups, (uint32_t)rows * (uint32_t)groups * 4u);
 #pragma unroll
   for (int i = 0; i < TW_G; ++i) {
     const int u = wave + NWAVE * i;
     const uint32_t gg = (uint32_t)(g0 + u);
     const bool in = u < ng;
-    tw.w[i] = buf_ld128(wr, in ? (uint32_t)r * (uint32_t)(K >> 1) + gg * 64u + (uint32_t)c * 16u : 0xFFFFFFF0u);
+    tw.w[i] = buf_ld128(wr, in ? (gg * 64u + (uint32_t)lane) * 16u : 0xFFFFFFF0u);
     tw.s[i] = buf_ld32(sr, in ? ((uint32_t)r * (uint32_t)groups + gg) * 4u : 0xFFFFFFF0u);
   }
 }
-// acc += X(token rows 0 .. mh-1 of xs) . dq(tile)^T; xs column 0 = group g0 of the tile's K range
+// acc += X(token rows 0 .. mh-1 of xs) . dq(tile)^T; xs column 0 = group g0 of the tile's K range.
+// Both exact dequantisation steps on 4x4x4 MFMAs, the dot on 16x16x32 MFMAs (unit_mma_t): lane L
+// reads token row L % 16 (or the zero row VH) at columns 32tp + 4 (L / 16) (+ 16) of each group.
 __device__ __forceinline__ void tile_mma(const TileW& tw, int ng, const uint16_t* xs, int ld, int mh,
                                          fl_f32x4& acc) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
   const int r = lane & 15, c = lane >> 4;
-  const uint16_t* xrow = xs + (r < mh ? r : VH) * ld + c * 32;
+  const uint16_t* xrow = xs + (r < mh ? r : VH) * ld + 4 * c;
+  const MxLane m = mx_lane();
 #pragma unroll
   for (int i = 0; i < TW_G; ++i) {
     const int u = wave + NWAVE * i;
-    if (u < ng) {  // wave-uniform
-      uint4 xa[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) xa[e] = *reinterpret_cast<const uint4*>(xrow + u * 128 + e * 8);
-      uint32_t d[4][4];
-      dq32(tw.w[i], dq_const(tw.s[i]), d);
-      mfma_chunk(d, xa, acc);
-    }
+    if (u < ng) unit_mma_t<VT_NB>(tw.w[i], tw.s[i], m, xrow + u * 128, acc);  // wave-uniform
   }
 }
 
@@ -2252,48 +2251,42 @@ struct TileW1 {
   uint4 w;
   uint32_t s;
 };
-__device__ __forceinline__ void tile_load1(const uint32_t* __restrict__ q, const uint32_t* __restrict__ sz,
+__device__ __forceinline__ void tile_load1(const uint32_t* __restrict__ qt, const uint32_t* __restrict__ sz,
                                            int n0, int K, int g0, int ng, TileW1& tw) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
-  const int r = lane & 15, c = lane >> 4, groups = K >> 7;
-  const auto wr = buf_rsrc(q + (size_t)n0 * (K >> 3), 16u * (uint32_t)(K >> 1));
+  const int r = lane & 15, groups = K >> 7;
+  const auto wr = buf_rsrc(qt + (size_t)n0 * (K >> 3), 16u * (uint32_t)(K >> 1));
   const auto sr = buf_rsrc(sz + (size_t)n0 * groups, 16u * (uint32_t)groups * 4u);
   const bool in = wave < ng;
   const uint32_t gg = (uint32_t)(g0 + wave);
-  tw.w = buf_ld128(wr, in ? (uint32_t)r * (uint32_t)(K >> 1) + gg * 64u + (uint32_t)c * 16u : 0xFFFFFFF0u);
+  tw.w = buf_ld128(wr, in ? (gg * 64u + (uint32_t)lane) * 16u : 0xFFFFFFF0u);
   tw.s = buf_ld32(sr, in ? ((uint32_t)r * (uint32_t)groups + gg) * 4u : 0xFFFFFFF0u);
 }
 __device__ __forceinline__ void tile_mma1(const TileW1& tw, int ng, const uint16_t* xs, int ld, int mh,
                                           fl_f32x4& acc) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
   const int r = lane & 15, c = lane >> 4;
-  if (wave < ng) {  // wave-uniform
-    const uint16_t* xrow = xs + (r < mh ? r : VH) * ld + c * 32 + wave * 128;
-    uint4 xa[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) xa[e] = *reinterpret_cast<const uint4*>(xrow + e * 8);
-    uint32_t d[4][4];
-    dq32(tw.w, dq_const(tw.s), d);
-    mfma_chunk(d, xa, acc);
-  }
+  if (wave < ng)  // wave-uniform
+    unit_mma_t<VT_NB>(tw.w, tw.s, mx_lane(), xs + (r < mh ? r : VH) * ld + wave * 128 + 4 * c, acc);
 }
 
 // The activation fragment tile_mma1 reads, from the bf16 [*, stride] rows src (device-coherent
 // loads) into the same place of xs: lane (r, c) of wave w copies row m0 + r (r < mh, w < ng),
-// columns k0 + 128 w + 32 c .. + 31, to xs row r, column 128 w + 32 c. Each lane later reads
-// back only its own fragment, so the copy needs no barrier.
+// columns k0 + 128 w + 32 tp + 4 c + 0..3 and + 16 + 0..3 (tp = 0..3), to xs row r at the same
+// columns less k0. Each lane later reads back only its own fragment, so the copy needs no barrier.
 __device__ __forceinline__ void stage_frag(const uint16_t* src, int stride, int m0, int mh, int k0, int ng,
                                            uint16_t* xs, int ld) {
   const int lane = tid_here() & 63, wave = tid_here() >> 6;
   const int r = lane & 15, c = lane >> 4;
   if (r >= mh || wave >= ng) return;  // rows past mh read xs row VH (zero)
   const auto rs = buf_rsrc(src + (size_t)m0 * stride, (uint32_t)mh * (uint32_t)stride * 2u);
-  uint4 v[4];
+  uint2 v[8];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = buf_ld128_coh(rs, (uint32_t)(r * stride + k0 + wave * 128 + c * 32 + e * 8) * 2u);
-  uint4* const dst = reinterpret_cast<uint4*>(xs + r * ld + wave * 128 + c * 32);
+  for (int e = 0; e < 8; ++e)
+    v[e] = buf_ld64_coh(rs, (uint32_t)(r * stride + k0 + wave * 128 + 32 * (e >> 1) + 16 * (e & 1) + 4 * c) * 2u);
+  uint16_t* const dst = xs + r * ld + wave * 128 + 4 * c;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) dst[e] = v[e];
+  for (int e = 0; e < 8; ++e) *reinterpret_cast<uint2*>(dst + 32 * (e >> 1) + 16 * (e & 1)) = v[e];
 }
 
 // four tiles' partials at once: tile i's go to part + i * NWAVE * 256; ends with a barrier
@@ -2941,7 +2934,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
                    t_h1 = tag_of(e0 + 2), t_act = tag_of(e0 + 3), t_h2 = tag_of(e0 + 4);
     uint32_t* const vf = p.vflag;
     // ---------------- P1: RMSNorm + QKV + RoPE + KV append ----------------
-    const uint32_t* const qkv_q = p.w.wqkv_q + (size_t)l * NQKV * (D >> 3);
+    const uint32_t* const qkv_q = p.w.wqkv_t + (size_t)l * NQKV * (D >> 3);  // tiled layout
     const uint32_t* const qkv_sz = p.w.wqkv_sz + (size_t)l * NQKV * (D >> 7);
     if (wg < NQKV / 16) {
       stage_norm_w(p.w.attn_norm + (size_t)l * D, D, nws);
@@ -3010,7 +3003,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     for (int i = tid; i < (ld >> 3); i += NT) reinterpret_cast<uint4*>(xs + VH * ld)[i] = make_uint4(0u, 0u, 0u, 0u);
     // ---------------- P3: O projection + residual ----------------
     if (owner) {
-      const uint32_t* const o_q = p.w.wo_q + (size_t)l * D * (D >> 3);
+      const uint32_t* const o_q = p.w.wo_t + (size_t)l * D * (D >> 3);  // tiled layout
       const uint32_t* const o_sz = p.w.wo_sz + (size_t)l * D * (D >> 7);
       for (int h0 = 0; h0 < M; h0 += VH) {
         const int mh = min(VH, M - h0);
@@ -3044,7 +3037,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     if (!owner) stamp(p, slot);
     stamp(p, slot);
     if (wg < (2 * F) / 16) {
-      const uint32_t* const gu_q = p.w.wgu_q + (size_t)l * 2 * F * (D >> 3);
+      const uint32_t* const gu_q = p.w.wgu_t + (size_t)l * 2 * F * (D >> 3);  // tiled layout
       const uint32_t* const gu_sz = p.w.wgu_sz + (size_t)l * 2 * F * (D >> 7);
       // this workgroup's tiles wg, wg+G, ... in rounds of up to 4: the round's MFMAs run back to
       // back into 4 accumulators, one publish and one epilogue per round. The first round's
@@ -3104,7 +3097,7 @@ __global__ __launch_bounds__(NT, 1) void k_verify(DecodeParams pv) {
     int p5slot = slot;
     slot += 2;
     {
-      const uint32_t* const d_q = p.w.wd_q + (size_t)l * D * (F >> 3);
+      const uint32_t* const d_q = p.w.wd_t + (size_t)l * D * (F >> 3);  // tiled layout
       const uint32_t* const d_sz = p.w.wd_sz + (size_t)l * D * (F >> 7);
       const int ntile = D / 16, ng = F >> 7, GPP = min(NWAVE, D >> 7), KP = (ng + GPP - 1) / GPP, GK = G / KP;
       const int k = wg % KP, kg0 = k * GPP, kgn = min(GPP, ng - kg0);
@@ -3817,6 +3810,7 @@ int fl_verify(const fl_weights* w, fl_state* st, const int32_t* tokens, int32_t 
               const int32_t* depth, const uint8_t* amask, int32_t pos, int32_t* tokens_out,
               float* logits, uint16_t* feat, void* stream) {
   if (!st || !tokens || !depth || !amask || !tokens_out || !weights_ok(w)) return FL_E_ARG;
+  if (!w->wqkv_t || !w->wo_t || !w->wgu_t || !w->wd_t) return FL_E_ARG;  // verify reads the tiled copies
   if (m < 1 || m > FL_MAX_VERIFY) return FL_E_M;
   if (pos < 0 || pos + m > st->max_seq) return FL_E_POS;
   if (!st->verify_ok) return FL_E_ARG;

@@ -2,52 +2,34 @@
 //
 // The dequantisation contract is the same as everywhere in this library, gpt-fast's
 // bf16(bf16((q - 8) * s) + z) (reference engine/quantize.py:138-155), and y = bf16(sum x * dq) with
-// fp32 accumulation (quantize.py:517-525). On the vector ALUs that takes about 4.4 operations per
-// weight (fl_common.h dq32 + the dot), which bounds an HBM-streaming GEMV at about half of the
-// bandwidth. Here the two exact fp32 steps and the dot run as MFMAs instead:
+// fp32 accumulation (quantize.py:517-525). Here the two exact fp32 steps and the dot run as MFMAs:
 //   D1 = A1 . diag(s) + C1:  A1 = (128 + q) as bf16 (one AND-OR per two weights puts the nibble in
 //        the mantissa of 128.0), C1 = -136 s, so D1 = (q - 8) s exactly (one nonzero product);
 //        v_cvt_pk_bf16_f32 rounds it to bf16 (RNE), the reference's first rounding;
 //   D2 = I . a + C2:  C2 = z, so D2 = fp32(a + z), the reference's fp32 add; cvt rounds it again;
-//   D3 += x . dq  (16x16x32 MFMA over two 16-position tiles; every output row holds the same sum).
-// Both dequantisation MFMAs have one nonzero product per output plus the accumulator, so their
-// fp32 results are exactly the reference's (D1 is exactly representable; D2 is one fp32 addition,
-// and where that addition rounds, |a| is below 2^-16 |z| and the bf16 rounding gives z either way).
-// The vector ALUs keep the nibble extraction and the four roundings: about 2.4 operations per
-// weight instead of 4.4.
+//   D3 += x . dq  (16x16x32 MFMA over two 16-position tiles; for M = 1 every output row holds the
+//        same sum, for M <= 16 token rows one row each).
+// Both dequantisation steps are v_mfma_f32_4x4x4_16b_bf16: 16 independent 4x4x4 products, block
+// b on lanes 4b..4b+3 (row i of A from lane 4b + i, column j of B from lane 4b + j, column j of D
+// to lane 4b + j). With A1 = four rows at one column per lane and B1 = diag(s) (lane 4b + j puts
+// the scale of its own row in slot j), lane 4b + j receives, in slot i, lane 4b + i's value of row
+// j times row j's scale: the block transposes, so every lane ends with four columns of one row.
+// Both have one nonzero product per output plus the accumulator, so their fp32 results are
+// exactly the reference's (D1 is exactly representable; D2 is one fp32 addition, and where that
+// addition rounds, |a| is below 2^-16 |z| and the bf16 rounding gives z either way).
 //
 // Tiled layout (fl_tile_int4 converts this library's row layout into it): for each block of 16 rows
-// and each 128-column group, 1 KB; lane l = 16 b + c of a wave reads the 16 bytes at l * 16:
-// 4 words holding rows 4b..4b+3 at the 8 columns c + 16 t (t = 0..7):
-//   word 0: bits 4t..4t+3 = q[4b][c + 16t], bits 16+4t.. = q[4b+1][c + 16t]   (t = 0..3)
-//   word 1: the same for t = 4..7;  words 2 / 3: rows 4b+2 / 4b+3.
-// That is the A operand of a 16x16x16 MFMA (lane: 4 consecutive k = rows, at i = column c) for each
-// of the 8 tiles, after one AND-OR per register. Scale / zero words stay [N, K/128].
+// and each 128-column group, 1 KB; lane L of a wave reads the 16 bytes at L * 16: rows
+// 4 p .. 4 p + 3 with p = (L / 4) % 4, at the 8 columns c + 16 t (t = 0..7), c = 4 (L / 16) + L % 4:
+//   word 0: bits 4t..4t+3 = q[4p][c + 16t], bits 16+4t.. = q[4p+1][c + 16t]   (t = 0..3)
+//   word 1: the same for t = 4..7;  words 2 / 3: rows 4p+2 / 4p+3.
+// After D1 and D2, lane L holds row L % 16 at columns 4 (L / 16) .. + 3 of each tile: the B
+// fragment of the 16x16x32 dot for two tiles. Scale / zero words stay [N, K/128]. The unit
+// routines (unit_dq_t, unit_mma_t) live in fl_common.h: the verify kernel runs them too.
 #include "fl_common.h"
 #include <algorithm>
 
 namespace {
-
-__device__ __forceinline__ fl_s16x4 s4(uint32_t lo, uint32_t hi) {
-  return __builtin_bit_cast(fl_s16x4, make_uint2(lo, hi));
-}
-__device__ __forceinline__ fl_bf16x8 b8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  return __builtin_bit_cast(fl_bf16x8, make_uint4(a, b, c, d));
-}
-// (w & mask) | magic: with both constants in registers (hidden from constant folding: gfx950's
-// three-operand encoding takes no literal) the compiler emits one v_and_or_b32 and still sees the
-// instruction, so it keeps the wait states that matrix-core results around it need (inline asm
-// hides those from it: an and-or written as asm here read registers an MFMA was still writing)
-struct AndOrK {
-  uint32_t mask, magic;
-};
-__device__ __forceinline__ AndOrK and_or_k() {
-  uint32_t mask = 0x000F000Fu, magic = 0x43004300u;
-  asm volatile("" : "+s"(mask));
-  asm volatile("" : "+v"(magic));
-  return {mask, magic};
-}
-__device__ __forceinline__ uint32_t and_or(uint32_t w, const AndOrK& k) { return (w & k.mask) | k.magic; }
 
 // row layout -> tiled layout: one thread per 16-byte tiled chunk
 __global__ __launch_bounds__(256) void k_tile_int4(const uint32_t* __restrict__ q, uint4* __restrict__ qt,
@@ -56,7 +38,7 @@ __global__ __launch_bounds__(256) void k_tile_int4(const uint32_t* __restrict__ 
   const int G = k >> 7;
   const int64_t chunks = (int64_t)(n >> 4) * G * 64;
   if (idx >= chunks) return;
-  const int l = (int)(idx & 63), b = l >> 4, c = l & 15;
+  const int l = (int)(idx & 63), p = (l >> 2) & 3, c = 4 * (l >> 4) + (l & 3);
   const int64_t blk = idx >> 6;
   const int g = (int)(blk % G), rb = (int)(blk / G);
   const int kw = k >> 3;  // words per row
@@ -66,11 +48,11 @@ __global__ __launch_bounds__(256) void k_tile_int4(const uint32_t* __restrict__ 
   };
   uint32_t wd[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {      // rows 4b + 2h, 4b + 2h + 1 -> words 2h, 2h + 1
+  for (int h = 0; h < 2; ++h) {      // rows 4p + 2h, 4p + 2h + 1 -> words 2h, 2h + 1
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int col = g * 128 + c + 16 * t;
-      const int r = rb * 16 + 4 * b + 2 * h;
+      const int r = rb * 16 + 4 * p + 2 * h;
       const uint32_t v = nib(r, col) | (nib(r + 1, col) << 16);
       wd[2 * h + (t >> 2)] |= v << (4 * (t & 3));
     }
@@ -78,97 +60,13 @@ __global__ __launch_bounds__(256) void k_tile_int4(const uint32_t* __restrict__ 
   qt[idx] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
 }
 
-// This lane's per-group constants: B1 = diag(s) (k = 4b + e, column c), C1 = -136 s_c,
-// C2 = z_c, from the (scale, zero) word of row c of the block
-struct GroupK {
-  uint32_t b1lo, b1hi;
-  fl_f32x4 c1, c2;
-};
-__device__ __forceinline__ GroupK group_k(uint32_t szw, int d) {  // d = c - 4b
-  const uint32_t sb = szw & 0xFFFFu;
-  GroupK k;
-  k.b1lo = d == 0 ? sb : (d == 1 ? sb << 16 : 0u);
-  k.b1hi = d == 2 ? sb : (d == 3 ? sb << 16 : 0u);
-  const float c1 = -136.0f * bf2f(sb), z = bf2f(szw >> 16);
-  k.c1 = fl_f32x4{c1, c1, c1, c1};
-  k.c2 = fl_f32x4{z, z, z, z};
-  return k;
-}
-
-// Dequantise one 16x16 tile (registers r0 / r1 from the tiled chunk: (128 + q) pairs of rows
-// 4b, 4b+1 and 4b+2, 4b+3 at column c) into this lane's bf16 pairs of columns 4b .. 4b+3 of row c.
-__device__ __forceinline__ void tile_dq(uint32_t r0, uint32_t r1, const GroupK& k, uint32_t ilo, uint32_t ihi,
-                                        uint32_t& o0, uint32_t& o1) {
-  const fl_f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(s4(r0, r1), s4(k.b1lo, k.b1hi), k.c1, 0, 0, 0);
-  const uint32_t a0 = pack_bf16x2(d1[0], d1[1]), a1 = pack_bf16x2(d1[2], d1[3]);
-  const fl_f32x4 d2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(s4(ilo, ihi), s4(a0, a1), k.c2, 0, 0, 0);
-  o0 = pack_bf16x2(d2[0], d2[1]);
-  o1 = pack_bf16x2(d2[2], d2[3]);
-}
-
-// The 8 tiles of one unit (this lane's 16 bytes w) dequantised with the steps batched across the
-// tiles: the 8 D1 MFMAs, then their roundings, then the 8 D2 MFMAs, then theirs, so no rounding
-// waits on the MFMA issued just before it. o[t] = tile_dq's (o0, o1) of tile t.
-__device__ __forceinline__ void unit_dq_batched(uint4 w, const GroupK& k, uint32_t ilo, uint32_t ihi,
-                                                uint32_t (&o)[8][2]) {
-  auto mm = [](uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, fl_f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(s4(a0, a1), s4(b0, b1), c, 0, 0, 0);
-  };
-  const AndOrK ao = and_or_k();
-  uint32_t wa = w.x, wb = w.y, wc = w.z, wd = w.w;
-  fl_f32x4 d[8];
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    uint32_t& lo = t < 4 ? wa : wb;
-    uint32_t& hi = t < 4 ? wc : wd;
-    const uint32_t r0 = and_or(lo, ao), r1 = and_or(hi, ao);
-    lo >>= 4;
-    hi >>= 4;
-    d[t] = mm(r0, r1, k.b1lo, k.b1hi, k.c1);
-  }
-  uint32_t a[8][2];
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    a[t][0] = pack_bf16x2(d[t][0], d[t][1]);
-    a[t][1] = pack_bf16x2(d[t][2], d[t][3]);
-  }
-#pragma unroll
-  for (int t = 0; t < 8; ++t)
-    d[t] = mm(ilo, ihi, a[t][0], a[t][1], k.c2);
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    o[t][0] = pack_bf16x2(d[t][0], d[t][1]);
-    o[t][1] = pack_bf16x2(d[t][2], d[t][3]);
-  }
-}
-
 // One 1 KB unit (16 rows x one 128-group) of the tiled matrix, dequantised and dotted with x:
-// acc += x[group] . dq^T. w: this lane's 16 bytes; xs: x in LDS (bf16, plain order).
-__device__ __forceinline__ void unit_dot(uint4 w, uint32_t szw, const uint16_t* xs, int g, uint32_t ilo,
-                                         uint32_t ihi, fl_f32x4& acc) {
-  const int lane = threadIdx.x & 63, b = lane >> 4, c = lane & 15;
-  const GroupK k = group_k(szw, c - 4 * b);
-  const AndOrK ao = and_or_k();
-  uint32_t wa = w.x, wb = w.y, wc = w.z, wd = w.w;
-#pragma unroll
-  for (int tp = 0; tp < 4; ++tp) {  // tiles 2tp, 2tp + 1: one 16x16x32 dot MFMA per pair
-    uint32_t q0[2], q1[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int t = 2 * tp + h;
-      uint32_t& lo = t < 4 ? wa : wb;
-      uint32_t& hi = t < 4 ? wc : wd;
-      const uint32_t r0 = and_or(lo, ao), r1 = and_or(hi, ao);
-      lo >>= 4;
-      hi >>= 4;
-      tile_dq(r0, r1, k, ilo, ihi, q0[h], q1[h]);
-    }
-    // x at columns 4b .. 4b+3 of tiles 2tp and 2tp + 1 (k = 8b + e of the MFMA)
-    const uint2 xa = *reinterpret_cast<const uint2*>(xs + g * 128 + 32 * tp + 4 * b);
-    const uint2 xb = *reinterpret_cast<const uint2*>(xs + g * 128 + 32 * tp + 16 + 4 * b);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b8(xa.x, xa.y, xb.x, xb.y), b8(q0[0], q1[0], q0[1], q1[1]),
-                                                  acc, 0, 0, 0);
-  }
+// acc += x[group] . dq^T (every output row of the MFMA holds the same sum). w: this lane's 16
+// bytes; xs: x in LDS (bf16, plain order).
+__device__ __forceinline__ void unit_dot(uint4 w, uint32_t szw, const uint16_t* xs, int g, const MxLane& m,
+                                         fl_f32x4& acc) {
+  const int b = (threadIdx.x & 63) >> 4;
+  unit_mma_t<8>(w, szw, m, xs + g * 128 + 4 * b, acc);
 }
 
 // y = bf16(W x): one workgroup of TW_NW waves per 16-row block (blocks strided over the grid); the
@@ -185,14 +83,13 @@ __global__ __launch_bounds__(TW_NW * 64) void k_gemv_tiled(const uint4* __restri
   for (int i = tid; i < (k >> 3); i += TW_NW * 64)
     reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(x)[i];
   __syncthreads();
-  const int b = lane >> 4, c = lane & 15, d = c - 4 * b;
-  const uint32_t one = 0x3F80u;  // bf16 1.0: the identity's A fragment (k = 4b + e, row c)
-  const uint32_t ilo = d == 0 ? one : (d == 1 ? one << 16 : 0u), ihi = d == 2 ? one : (d == 3 ? one << 16 : 0u);
+  const int c = lane & 15;
+  const MxLane m = mx_lane();
   for (int rb = blockIdx.x; rb < nb; rb += gridDim.x) {
     fl_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     const uint4* blk = qt + (size_t)rb * G * 64;
     const uint32_t* srow = sz + (size_t)(rb * 16 + c) * G;
-    for (int g = wave; g < G; g += TW_NW) unit_dot(blk[(size_t)g * 64 + lane], srow[g], xs, g, ilo, ihi, acc);
+    for (int g = wave; g < G; g += TW_NW) unit_dot(blk[(size_t)g * 64 + lane], srow[g], xs, g, m, acc);
     if (lane < 16) part[wave * 16 + lane] = acc[0];
     __syncthreads();
     if (tid < 16) {
@@ -229,9 +126,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiled_pf(const uint4* __restri
     const int v = tid + i * NW * 64;
     xv[i] = buf_ld128(xr, v < nx ? (uint32_t)v * 16u : 0xFFFFFFF0u);
   }
-  const int b = lane >> 4, c = lane & 15, d = c - 4 * b;
-  const uint32_t one = 0x3F80u;
-  const uint32_t ilo = d == 0 ? one : (d == 1 ? one << 16 : 0u), ihi = d == 2 ? one : (d == 3 ? one << 16 : 0u);
+  const int c = lane & 15;
+  const MxLane m = mx_lane();
   bool staged = false;
   for (int rb = blockIdx.x; rb < nb; rb += gridDim.x) {
     const auto wr = buf_rsrc(qt + (size_t)rb * G * 64, (uint32_t)G * 1024u);
@@ -254,7 +150,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiled_pf(const uint4* __restri
 #pragma unroll
     for (int i = 0; i < UPW; ++i) {
       const int g = wave + NW * i;
-      if (g < G) unit_dot(w[i], sw[i], xs, g, ilo, ihi, acc);  // wave-uniform
+      if (g < G) unit_dot(w[i], sw[i], xs, g, m, acc);  // wave-uniform
     }
     if (lane < 16) part[wave * 16 + lane] = acc[0];
     __syncthreads();
@@ -277,25 +173,12 @@ __global__ __launch_bounds__(256) void k_dequant_tiled(const uint4* __restrict__
   const int G = k >> 7;
   if (unit >= (int64_t)(n >> 4) * G) return;
   const int g = (int)(unit % G), rb = (int)(unit / G);
-  const int b = lane >> 4, c = lane & 15, d = c - 4 * b;
-  const uint32_t one = 0x3F80u;
-  const uint32_t ilo = d == 0 ? one : (d == 1 ? one << 16 : 0u), ihi = d == 2 ? one : (d == 3 ? one << 16 : 0u);
-  const uint4 w = qt[unit * 64 + lane];
-  const GroupK kk = group_k(sz[(size_t)(rb * 16 + c) * G + g], d);
-  const AndOrK ao = and_or_k();
-  uint32_t wa = w.x, wb = w.y, wc = w.z, wd = w.w;
+  const int b = lane >> 4, c = lane & 15;
+  uint32_t o[8][2];
+  unit_dq_t<8>(qt[unit * 64 + lane], sz[(size_t)(rb * 16 + c) * G + g], mx_lane(), o);
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    uint32_t& lo = t < 4 ? wa : wb;
-    uint32_t& hi = t < 4 ? wc : wd;
-    const uint32_t r0 = and_or(lo, ao), r1 = and_or(hi, ao);
-    lo >>= 4;
-    hi >>= 4;
-    uint32_t o0, o1;
-    tile_dq(r0, r1, kk, ilo, ihi, o0, o1);
-    // row c of the block, columns 16t + 4b .. +3 of group g
-    *reinterpret_cast<uint2*>(out + (size_t)(rb * 16 + c) * k + g * 128 + 16 * t + 4 * b) = make_uint2(o0, o1);
-  }
+  for (int t = 0; t < 8; ++t)  // row c of the block, columns 16t + 4b .. +3 of group g
+    *reinterpret_cast<uint2*>(out + (size_t)(rb * 16 + c) * k + g * 128 + 16 * t + 4 * b) = make_uint2(o[t][0], o[t][1]);
 }
 
 // Diagnostic: the compute rate of the exact dequantisation with an M = 8 matrix-core product and
@@ -303,9 +186,9 @@ __global__ __launch_bounds__(256) void k_dequant_tiled(const uint4* __restrict__
 // of seeded pseudo-random words in registers and recomputes them `iters` times against 8 token
 // rows in LDS -- k_verify's tile product at M = 8 with the weights already there. MODE 0: this
 // library's row layout, dequantised on the vector ALUs (dq32, four 16x16x32 MFMAs per 32 weights:
-// k_verify's tile_mma); MODE 1: the tiled layout, both exact fp32 steps on 16x16x16 MFMAs and the
-// dot on a 16x16x32 MFMA per two tiles (unit_dot with token rows in place of the one x row);
-// MODE 2: MODE 1's arithmetic with each step batched over the unit's 8 tiles (unit_dq_batched);
+// k_verify's tile_mma); MODE 1: the tiled layout, both exact fp32 steps on 4x4x4 MFMAs and the
+// dot on a 16x16x32 MFMA per two tiles (unit_mma_t over two tiles at a time); MODE 2: the same
+// with each step batched over the unit's 8 tiles (unit_mma_t<8>, the kernels' form);
 // MODES 3 / 4: M = 1 as the decode kernel computes it, one row-layout chunk per lane dotted with x
 // on the vector ALUs, dequantised by dq32 (3) or by the lane-local matrix-core dq32_mx (4).
 // out[2 wg] = the workgroup's 100 MHz ticks, out[2 wg + 1] = bits of its result (kept so the
@@ -371,48 +254,11 @@ __global__ __launch_bounds__(512, 1) void k_probe_dequant(int iters, unsigned lo
         }
         acc[0] = a;
       } else if constexpr (MODE == 2) {
-        const int b = lane >> 4, cc = lane & 15, dd = cc - 4 * b;
-        const GroupK k = group_k(s[u], dd);
-        const uint32_t one = 0x3F80u;
-        const uint32_t ilo = dd == 0 ? one : (dd == 1 ? one << 16 : 0u), ihi = dd == 2 ? one : (dd == 3 ? one << 16 : 0u);
-        uint32_t o[8][2];
-        unit_dq_batched(w[u], k, ilo, ihi, o);
-        const uint16_t* xrow = xs + (cc < 8 ? cc : 16) * PDQ_LD + u * 128 + 4 * b;
-#pragma unroll
-        for (int tp = 0; tp < 4; ++tp) {
-          const uint2 xa = *reinterpret_cast<const uint2*>(xrow + 32 * tp);
-          const uint2 xb = *reinterpret_cast<const uint2*>(xrow + 32 * tp + 16);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b8(xa.x, xa.y, xb.x, xb.y),
-                                                        b8(o[2 * tp][0], o[2 * tp][1], o[2 * tp + 1][0], o[2 * tp + 1][1]),
-                                                        acc, 0, 0, 0);
-        }
+        const uint16_t* xrow = xs + (r < 8 ? r : 16) * PDQ_LD + u * 128 + 4 * c;
+        unit_mma_t<8>(w[u], s[u], mxl, xrow, acc);
       } else {
-        const int b = lane >> 4, cc = lane & 15;  // tiled lane (b, c): rows 4b..4b+3, column c
-        const GroupK k = group_k(s[u], cc - 4 * b);
-        const AndOrK ao = and_or_k();
-        const uint32_t one = 0x3F80u;
-        const int dd = cc - 4 * b;
-        const uint32_t ilo = dd == 0 ? one : (dd == 1 ? one << 16 : 0u), ihi = dd == 2 ? one : (dd == 3 ? one << 16 : 0u);
-        uint32_t wa = w[u].x, wb = w[u].y, wc = w[u].z, wd = w[u].w;
-        const uint16_t* xrow = xs + (cc < 8 ? cc : 16) * PDQ_LD + u * 128 + 4 * b;
-#pragma unroll
-        for (int tp = 0; tp < 4; ++tp) {
-          uint32_t q0[2], q1[2];
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const int t = 2 * tp + hh;
-            uint32_t& lo = t < 4 ? wa : wb;
-            uint32_t& hi = t < 4 ? wc : wd;
-            const uint32_t r0 = and_or(lo, ao), r1 = and_or(hi, ao);
-            lo >>= 4;
-            hi >>= 4;
-            tile_dq(r0, r1, k, ilo, ihi, q0[hh], q1[hh]);
-          }
-          const uint2 xa = *reinterpret_cast<const uint2*>(xrow + 32 * tp);
-          const uint2 xb = *reinterpret_cast<const uint2*>(xrow + 32 * tp + 16);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b8(xa.x, xa.y, xb.x, xb.y), b8(q0[0], q1[0], q0[1], q1[1]),
-                                                        acc, 0, 0, 0);
-        }
+        const uint16_t* xrow = xs + (r < 8 ? r : 16) * PDQ_LD + u * 128 + 4 * c;
+        unit_mma_t<2>(w[u], s[u], mxl, xrow, acc);
       }
     }
   }

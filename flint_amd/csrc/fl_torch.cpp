@@ -76,6 +76,20 @@ class Engine {
     w_.embed = reinterpret_cast<const uint16_t*>(embed.data_ptr());
     w_.rope = reinterpret_cast<const uint16_t*>(rope.data_ptr());
     w_.rope_len = (int32_t)rope.size(0);
+    // the tiled copies the verify kernel reads (fl_tile_int4), made once here on the default
+    // stream and kept with the other tensors
+    auto tile = [&](const torch::Tensor& q) {
+      torch::Tensor t = torch::empty_like(q);
+      check_rc(fl_tile_int4(reinterpret_cast<const uint32_t*>(q.data_ptr()), reinterpret_cast<uint32_t*>(t.data_ptr()),
+                            (int32_t)(q.numel() / q.size(-1)), (int32_t)(q.size(-1) * 8), nullptr),
+               "fl_tile_int4");
+      keep_.push_back(t);
+      return reinterpret_cast<const uint32_t*>(t.data_ptr());
+    };
+    w_.wqkv_t = tile(wqkv_q);
+    w_.wo_t = tile(wo_q);
+    w_.wgu_t = tile(wgu_q);
+    w_.wd_t = tile(wd_q);
     check_rc(fl_state_create(&d_, (int32_t)k_cache.size(2), reinterpret_cast<uint16_t*>(k_cache.data_ptr()),
                              reinterpret_cast<uint16_t*>(v_cache.data_ptr()), &st_),
              "fl_state_create");

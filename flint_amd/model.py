@@ -8,7 +8,7 @@ bf16 tensor, and one decode step is ONE cooperative kernel launch (fl_decode_ste
 import torch
 
 from . import _lib
-from .quantize import quantize_int4
+from .quantize import quantize_int4, tile_int4
 from .synth import ModelArgs, freqs_cis_table
 
 
@@ -64,6 +64,13 @@ class PackedModel:
         self.final_norm = sd["norm"].to(**bf).contiguous()
         self.embed = sd["embed"].to(**bf).contiguous()
         self.rope = freqs_cis_table(args.block_size, args.head_dim, args.rope_base).to(self.device).contiguous()
+        self._tile()
+
+    def _tile(self):
+        """The four int4 matrices again in the tiled layout (fl_tile_int4), which the verify
+        kernel's matrix-core tiles read; decode reads the row layout."""
+        for name in ("wqkv", "wo", "wgu", "wd"):
+            setattr(self, name + "_t", tile_int4(getattr(self, name + "_q")))
 
     @classmethod
     def from_tensors(cls, args: ModelArgs, t, device="cuda"):
@@ -86,16 +93,20 @@ class PackedModel:
                 raise ValueError(f"{name}: dtype {x.dtype}, expected {dt}")
             setattr(self, name, x.to(self.device).contiguous())
         self.rope = freqs_cis_table(args.block_size, args.head_dim, args.rope_base).to(self.device).contiguous()
+        self._tile()
         return self
 
     def nbytes_int4(self):
+        """Bytes of one copy of the int4 weights with their scale/zero words (what one decode
+        step reads; the tiled copies are verify's)."""
         return sum(t.numel() * 4 for t in (self.wqkv_q, self.wo_q, self.wgu_q, self.wd_q,
                                            self.wqkv_sz, self.wo_sz, self.wgu_sz, self.wd_sz))
 
     def c_weights(self):
         w = _lib.Weights()
         for name in ("wqkv_q", "wqkv_sz", "wo_q", "wo_sz", "wgu_q", "wgu_sz", "wd_q", "wd_sz",
-                     "attn_norm", "ffn_norm", "final_norm", "embed", "rope"):
+                     "attn_norm", "ffn_norm", "final_norm", "embed", "rope",
+                     "wqkv_t", "wo_t", "wgu_t", "wd_t"):
             setattr(w, name, getattr(self, name).data_ptr())
         w.rope_len = self.rope.shape[0]
         return w

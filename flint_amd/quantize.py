@@ -47,6 +47,22 @@ def dequantize_int4(q, sz, matrix_cores=False):
     return out
 
 
+def tile_int4(q, qt=None):
+    """The tiled layout (fl_tile_int4) of a row-layout int4 matrix q [..., N, K/8] (N % 16 == 0;
+    leading dims are stacked rows): same shape and dtype, 1 KB per 16 rows x 128-group unit."""
+    _check_dev(q, torch.int32, "q")
+    k = q.shape[-1] * 8
+    n = q.numel() // q.shape[-1]
+    if n % 16:
+        raise ValueError("tile_int4: the stacked row count must be a multiple of 16")
+    if qt is None:
+        qt = torch.empty_like(q)
+    elif qt.shape != q.shape or qt.dtype != torch.int32 or not qt.is_contiguous():
+        raise ValueError("tile_int4: qt must be a contiguous int32 tensor shaped like q")
+    _lib.call("fl_tile_int4", _lib.ptr(q), _lib.ptr(qt), n, k, _lib.stream_ptr())
+    return qt
+
+
 def gemv_int4(q, sz, x, y=None):
     """y[N] = bf16(x[K] . dq[N,K]^T) with fp32 accumulation (M = 1)."""
     _check_dev(q, torch.int32, "q")

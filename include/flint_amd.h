@@ -62,6 +62,10 @@ typedef struct fl_weights {
   const uint16_t *embed;              /* [V, D] bf16, tied LM head               */
   const uint16_t *rope;               /* [rope_len, 32, 2] bf16 (cos, sin)       */
   int32_t rope_len;
+  /* The same four int4 matrices in the tiled layout (fl_tile_int4 of each layer-stacked matrix,
+   * same sizes as wqkv_q .. wd_q): fl_verify's matrix-core tiles read these, the decode entry
+   * points the row layout above. Required by fl_verify only. */
+  const uint32_t *wqkv_t, *wo_t, *wgu_t, *wd_t;
 } fl_weights;
 
 typedef struct fl_state fl_state;
@@ -101,10 +105,11 @@ int fl_gemm_int4(const uint32_t* q, const uint32_t* sz, const uint16_t* x, uint1
 
 /* ---- tiled layout: the exact dequantisation on the matrix cores ------------------------- */
 
-/* The same int4 values in the tiled layout the matrix-core GEMV reads (N % 16 == 0): per block
- * of 16 rows and 128-column group, 1 KB; 16 bytes per lane l = 16b + c of a wave: words 0 / 1 hold
- * rows 4b, 4b+1 at columns c + 16t (t = 0..3 / 4..7: row 4b at bits 4(t%4), row 4b+1 at 16 + 4(t%4)),
- * words 2 / 3 the same for rows 4b+2, 4b+3. qt: uint32 [N/16, K/128, 64, 4]; sz is unchanged.
+/* The same int4 values in the tiled layout the matrix-core kernels read (N % 16 == 0): per block
+ * of 16 rows and 128-column group, 1 KB; 16 bytes per lane l of a wave, with p = (l / 4) % 4 and
+ * c = 4 (l / 16) + l % 4: words 0 / 1 hold rows 4p, 4p+1 at columns c + 16t (t = 0..3 / 4..7: row
+ * 4p at bits 4(t%4), row 4p+1 at 16 + 4(t%4)), words 2 / 3 the same for rows 4p+2, 4p+3.
+ * qt: uint32 [N/16, K/128, 64, 4]; sz is unchanged.
  * No counterpart in the reference (its tinygemm tile layout, quantize.py:359-364, serves the
  * same purpose for its CUDA kernel). */
 int fl_tile_int4(const uint32_t* q, uint32_t* qt, int32_t n, int32_t k, void* stream);
