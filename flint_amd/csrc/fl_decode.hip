@@ -786,12 +786,21 @@ __device__ __forceinline__ void gemv_compute(const uint4 (&wr)[MC], const uint32
 // Key slices of one query head over the cached keys 0..pos-1. Keys are processed in 8-key steps
 // (8 keys x 64 dims: one 16-byte K load and one 16-byte V load per lane); a slice is one
 // workgroup, whose 8 waves take interleaved steps so that each group of 8 steps covers 64
-// consecutive keys. `spw` is the target number of steps per wave: slices = ceil(steps /
-// (8 * spw)), at most G / NH, at least 1 (the new key at pos always has a slice).
+// consecutive keys. One slice while no wave takes more than `spw` steps; beyond that, 4/5 of the
+// workgroups take a slice each (NH x nsl <= 0.8 G), at most G / NH and MAX_SLICES, at least 1 (the
+// new key at pos always has a slice). Measured at flint-3b (40 heads, 256 workgroups; tok/s by
+// slice count, the merge left to the O phase from 2 slices): ctx 128 / 256: 1 slice 1165 / 1141
+// against 1128-1133 / 1124-1130 with 3-5; ctx 512 / 1024 / 2048 / 4096: 5 slices 1121 / 1109 /
+// 1069 / 981 against 2 slices 1095 / 1035 (merged in the attention phase), 6 slices 1093 / 1081 /
+// 1055 / 971, 4 slices 1116 / 1100 / 1027 / 943. spw < 0 fixes the count at -spw (tuning knob).
 __host__ __device__ inline void attn_slices(int pos, int NH, int G, int spw, int& nsl, int& sps) {
   const int ns = (pos + 7) >> 3;
-  const int per = NWAVE * spw;
-  nsl = (ns + per - 1) / per;
+  if (spw < 0)
+    nsl = -spw;
+  else if (ns <= NWAVE * spw)
+    nsl = 1;
+  else
+    nsl = (4 * G) / (5 * NH);
   if (nsl < 1) nsl = 1;
   int cap = G / NH < MAX_SLICES ? G / NH : MAX_SLICES;
   if (cap < 1) cap = 1;
@@ -816,12 +825,13 @@ __host__ __device__ inline void attn_slices(int pos, int NH, int G, int spw, int
 // round of steps with an online rescale between rounds and for the new key. Waves merge through
 // LDS; slices > 0 publish (m, l, o) as tagged 64-bit words and slice 0 merges them in order (with
 // DEFER_MERGE_SLICES or more slices it returns its own (m, l, o) in mg and merges in the O phase).
-// With this many key slices or more, slice 0 leaves its merge to the O phase, after its own O
-// chunks are dequantised (it waits longest for the other slices, and its workgroup would otherwise
-// start that work last and be the last O producer). Measured against merging in the attention
-// phase: ctx 2048 / 3072 / 4096 / 8192 (4, 6, 6, 6 slices): -24, -66, -40, -48 us per step; with 2
-// or 3 slices the merge itself then waits behind the O phase's requests: +30 us (2), +5 us (3).
-constexpr int DEFER_MERGE_SLICES = 4;
+// With this many key slices or more (the host's default; FLINT_AMD_DEFER_SLICES to tune), slice 0
+// leaves its merge to the O phase, after its own O chunks are dequantised (it waits longest for the
+// other slices, and its workgroup would otherwise start that work last and be the last O
+// producer). Measured against merging in the attention phase: ctx 2048 / 3072 / 4096 / 8192 (4, 6,
+// 6, 6 slices): -24, -66, -40, -48 us per step; at ctx 512 with 2 slices +10 tok/s (1105 against
+// 1095) once the GEMVs dequantised on the matrix cores (before that, +30 us per step).
+constexpr int DEFER_MERGE_SLICES = 2;
 // A key-slice merge left to the caller: slice 0's (max, sum, o) after its own keys (wave 0, lane d)
 struct SliceMerge {
   bool pend = false;  // workgroup-uniform
@@ -1043,10 +1053,10 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
       mg.O = O;
       mg.hq = hq;
       mg.nsl = nsl;
-      if (!DEFER || nsl < DEFER_MERGE_SLICES) slice_merge(p, mg, otag, ptag);
+      if (!DEFER || nsl < 2) slice_merge(p, mg, otag, ptag);
     }
   }
-  mg.pend = DEFER && sl == 0 && nsl >= DEFER_MERGE_SLICES;
+  mg.pend = DEFER && sl == 0 && nsl >= 2;
   __builtin_amdgcn_s_setprio(0);
   stamp(p, slot);
 }
@@ -3347,6 +3357,7 @@ struct fl_state {
   uint32_t* shist;              // fused sampling exchange: per-workgroup histograms
   unsigned long long* sword;    // ... bin totals, maxima, partial sums
   int att_spw, gq_min, gq_kps;
+  int defer_min;  // key slices from which the per-head attention leaves its merge to the O phase
   int vkps, vtok_work;
   int coop;       // launch with hipLaunchCooperativeKernel (else a plain launch, the default)
   // the k_decode instantiations of the chunk budget that fits the model, by attention: per-head
@@ -3550,7 +3561,7 @@ int decode_launch(const fl_weights* w, fl_state* st, const int32_t* token_in, ui
   } else {
     int nsl, sps;
     attn_slices(pos, st->d.n_head, st->grid, st->att_spw, nsl, sps);
-    if (nsl >= DEFER_MERGE_SLICES) kd = st->kdec[1];
+    if (nsl >= st->defer_min) kd = st->kdec[1];
   }
   const hipError_t e =
       st->coop ? hipLaunchCooperativeKernel(kd, dim3(st->grid), dim3(NT), args, 0, as_stream(stream))
@@ -3630,7 +3641,9 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
     st->clear_period = (uint32_t)std::max(1L, P);
     st->since_clear = 0;
   }
-  st->att_spw = 8;
+  st->att_spw = 7;  // one key slice up to 448 cached keys (tok/s at ctx 320 / 384 / 448: one slice
+                    // 1136 / 1124 / 1112, five 1121 / 1119 / 1120)
+  st->defer_min = DEFER_MERGE_SLICES;
   // the attention by KV group from 5120 cached keys: measured on one box against the per-head
   // units, +25 / +16 us per step at ctx 3072 / 4096, -13 / -20 / -17 us at 6144 / 8192 / 12288
   st->gq_min = 5120;
@@ -3648,6 +3661,14 @@ int fl_state_create(const fl_model_desc* d, int32_t max_seq, uint16_t* k_cache, 
   if (const char* e = getenv("FLINT_AMD_ATT_STEPS")) {  // tuning knob: steps per wave per slice
     const int v = atoi(e);
     if (v >= 1 && v <= 64) st->att_spw = v;
+  }
+  if (const char* e = getenv("FLINT_AMD_ATT_SLICES")) {  // tuning knob: a fixed key-slice count
+    const int v = atoi(e);
+    if (v >= 1 && v <= MAX_SLICES) st->att_spw = -v;
+  }
+  if (const char* e = getenv("FLINT_AMD_DEFER_SLICES")) {  // tuning knob: slices from which slice 0
+    const int v = atoi(e);                                  // merges in the O phase
+    if (v >= 2) st->defer_min = v;
   }
   if (const char* e = getenv("FLINT_AMD_GQA_MIN")) st->gq_min = std::max(0, atoi(e));  // tuning knob
   if (const char* e = getenv("FLINT_AMD_GQA_KEYS")) {  // tuning knob: keys per GQA slice

@@ -117,12 +117,14 @@ def test_greedy_decode_parity(dev, name, prompt_len, steps):
     assert ties <= 4
 
 
-@pytest.mark.parametrize("steps_per_wave", [1, 3])
-def test_decode_multi_slice_attention(dev, monkeypatch, steps_per_wave):
+@pytest.mark.parametrize("slices,defer", [(2, 2), (5, 2), (16, 2), (3, 64)])
+def test_decode_multi_slice_attention(dev, monkeypatch, slices, defer):
     """Attention split over several key slices per head (slices > 0 publish tagged partials,
-    slice 0 merges them): forced by a small steps-per-wave target, at contexts that give 2 to 16
-    slices, including a partly filled last step."""
-    monkeypatch.setenv("FLINT_AMD_ATT_STEPS", str(steps_per_wave))
+    slice 0 merges them, in the O phase from `defer` slices on, else in the attention phase):
+    the slice count forced (fewer where the context has fewer 8-key steps), including a partly
+    filled last step."""
+    monkeypatch.setenv("FLINT_AMD_ATT_SLICES", str(slices))
+    monkeypatch.setenv("FLINT_AMD_DEFER_SLICES", str(defer))
     name = "tiny"
     args, sd, eng, orc = make_pair(name, seed=5)
     bar = logit_bar(name)
@@ -132,7 +134,7 @@ def test_decode_multi_slice_attention(dev, monkeypatch, steps_per_wave):
         fill_kv_random(eng, orc, pos, seed=pos)
         tok = (13 * pos + 1) % args.vocab_size
         am_e, am_o, (ok, d, within, same), lg, lo, fe, fo = _step_compare(eng, orc, tok, pos, name)
-        log(f"spw={steps_per_wave} pos={pos}: max|dlogit|={d:.3e} ({within:.1%} within 2e-2) "
+        log(f"slices={slices} defer={defer} pos={pos}: max|dlogit|={d:.3e} ({within:.1%} within 2e-2) "
             f"argmax eng={am_e} oracle={am_o}")
         assert ok
         assert am_e == am_o or near_tie(lo, bar)
