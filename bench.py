@@ -163,14 +163,16 @@ def handoff_probe(dev, words=2560, rounds=2000):
     ordinary device memory (L2-local coherent loads) -- these three poll single words with a sleep
     between polls; then across all workgroups polled as the decode kernel's waits poll (16-byte
     groups, the missing ones re-requested together, no sleep), with one round of requests in
-    flight and with two (the second round 512 cycles after the first). Also reports whether every
-    workgroup ran on XCD blockIdx % 8 (the mapping the XCD-local modes assume)."""
+    flight and with two (the second round 512 cycles after the first), and within each XCD polled
+    that way. Also reports whether every workgroup ran on XCD blockIdx % 8 (the mapping the
+    XCD-local modes assume)."""
     from flint_amd import _lib
     import ctypes
     res = {"words": words, "rounds": rounds}
     grid = ctypes.c_int32()
     for mode, name in ((0, "all_uncached_us"), (1, "xcd_uncached_us"), (2, "xcd_l2_us"),
-                       (3 | 1 << 8, "all_groups_us"), (3 | 2 << 8 | 8 << 16, "all_groups_depth2_us")):
+                       (3 | 1 << 8, "all_groups_us"), (3 | 2 << 8 | 8 << 16, "all_groups_depth2_us"),
+                       (4, "xcd_groups_us")):
         out = torch.zeros(2 * 1024, dtype=torch.int64, device=dev)
         for _ in range(2):      # the first call allocates and warms up
             _lib.call("fl_probe_handoff", mode, words, rounds, _lib.ptr(out), ctypes.byref(grid),
@@ -195,10 +197,10 @@ def dequant_rate(dev, iters=2000):
     """Compute rate of the exact dequantisation with every weight already in registers
     (fl_probe_dequant), in weights per second over the slowest workgroup, beside the rate at which
     HBM delivers int4 weights with their scale/zero words (8 TB/s / 0.53125 B per weight). With an
-    M = 8 MFMA product: the row layout on the vector ALUs (k_verify's tile product), the tiled
-    layout on 16x16x16 MFMAs (fl_gemv_int4_tiled's unit_dot) and the same batched over a unit's
-    tiles; with an M = 1 dot on the vector ALUs (the decode kernel's form): dq32 and the
-    lane-local 4x4x4-MFMA dq32_mx."""
+    M = 8 MFMA product: the row layout on the vector ALUs (the verify tiles' former product), the
+    tiled layout on 4x4x4 MFMAs two tiles at a time and batched over a unit's 8 tiles (the verify
+    tiles' and fl_gemv_int4_tiled's unit_mma_t); with an M = 1 dot on the vector ALUs (the decode
+    kernel's form): dq32 and the lane-local 4x4x4-MFMA dq32_mx."""
     from flint_amd import _lib
     import ctypes
     grid = ctypes.c_int32()

@@ -20,7 +20,8 @@
 //      that XCD's L2 (the one L2 all the group's CUs share);
 //   3: all workgroups, uncached memory, polled the way the decode kernel's waits poll: 16-byte
 //      groups of 4 words, every missing group re-requested at once, 1 to 3 rounds of requests in
-//      flight (k_probe_groups).
+//      flight (k_probe_groups);
+//   4: the workgroups of one XCD (as mode 1), polled as mode 3 with one round in flight.
 // Modes 0-2 poll single words with a sleep between polls.
 // Every workgroup also records its XCC_ID hardware register, so the host can check the
 // blockIdx-to-XCD mapping that modes 1 and 2 assume. Every wait is bounded (about 0.5 s): a
@@ -101,23 +102,28 @@ __global__ __launch_bounds__(PR_NT, 1) void k_probe_handoff(uint32_t* __restrict
 // lands just after one round passed the coherence point is seen by the next without a full round
 // trip in between. Each round re-requests only the groups not yet seen complete (complete groups
 // get an out-of-range request, which touches no memory and keeps the requests branch-free),
-// `resleep` x 64 cycles after the answers that found them incomplete.
+// `resleep` x 64 cycles after the answers that found them incomplete. local: the groups of mode 4
+// (each XCD's workgroups exchange a vector of their own, in buffers of their own).
 constexpr int PR_MAXG = PR_MAXW / 4 / PR_NT;  // 16-byte groups polled per thread, at most
 template <int DEPTH>
 __global__ __launch_bounds__(PR_NT, 1) void k_probe_groups(uint32_t* __restrict__ buf, int words,
-                                                           int rounds, int gap, int resleep,
+                                                           int rounds, int gap, int resleep, int local,
                                                            unsigned long long* __restrict__ out) {
   extern __shared__ uint32_t pad[];
   const int tid = threadIdx.x, wg = blockIdx.x, G = gridDim.x;
-  const int share = (words + G - 1) / G;
-  const int w0 = wg * share, w1 = min(words, w0 + share);
+  const int group = local ? wg % PR_GROUPS : 0;
+  const int gsize = local ? (G - group + PR_GROUPS - 1) / PR_GROUPS : G;  // workgroups in the group
+  const int gi = local ? wg / PR_GROUPS : wg;                            // index within it
+  uint32_t* const vec = buf + (size_t)group * 2 * words;                 // the group's two buffers
+  const int share = (words + gsize - 1) / gsize;
+  const int w0 = gi * share, w1 = min(words, w0 + share);
   const int ng = words >> 2;
   if (tid == 0) pad[0] = 0;
   bool timed_out = false;
   __syncthreads();
   const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
   for (int r = 0; r < rounds && !timed_out; ++r) {
-    uint32_t* v = buf + (size_t)(r & 1) * words;
+    uint32_t* v = vec + (size_t)(r & 1) * words;
     const uint32_t tag = (uint32_t)(r % 65535) + 1u;
     for (int i = w0 + tid; i < w1; i += PR_NT) st_coh_u32(v + i, (tag << 16) | (uint32_t)(i & 0xFFFF));
     const auto rs = buf_rsrc(v, (uint32_t)words * 4u);
@@ -186,14 +192,15 @@ extern "C" {
 
 int fl_probe_handoff(int32_t mode, int32_t words, int32_t rounds, uint64_t* out, int32_t* grid,
                      void* stream) {
-  // mode: bits 0-7 the kind (0..3); kind 3 also takes the poll depth (bits 8-11, 1..3), the gap
+  // mode: bits 0-7 the kind (0..4); kind 3 also takes the poll depth (bits 8-11, 1..3), the gap
   // between the first rounds' requests (bits 16-23, x 64 cycles) and the sleep before a re-request
-  // (bits 24-30, x 64 cycles)
-  const int kind = mode & 0xFF, depth = (mode >> 8) & 0xF, gap = (mode >> 16) & 0xFF,
-            resleep = (mode >> 24) & 0x7F;
-  if (mode < 0 || kind > 3 || (kind < 3 && mode != kind) || (kind == 3 && (depth < 1 || depth > 3 || words % 4)) ||
+  // (bits 24-30, x 64 cycles); kind 4 takes none (one round in flight)
+  const int kind = mode & 0xFF, gap = (mode >> 16) & 0xFF, resleep = (mode >> 24) & 0x7F;
+  const int depth = kind == 4 ? 1 : (mode >> 8) & 0xF;
+  if (mode < 0 || kind > 4 || (kind != 3 && mode != kind) || (kind >= 3 && (depth < 1 || depth > 3 || words % 4)) ||
       words < 4 || words > PR_MAXW || rounds < 1 || rounds > 100000 || !out || !grid)
     return FL_E_ARG;
+  const int local = kind == 4;
   int dev = 0, cu = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FL_E_HIP;
   if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return FL_E_HIP;
@@ -228,11 +235,14 @@ int fl_probe_handoff(int32_t mode, int32_t words, int32_t rounds, uint64_t* out,
   if (kind < 3)
     hipLaunchKernelGGL(k_probe_handoff, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, kind, o);
   else if (depth == 1)
-    hipLaunchKernelGGL(k_probe_groups<1>, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, gap, resleep, o);
+    hipLaunchKernelGGL(k_probe_groups<1>, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, gap, resleep,
+                       local, o);
   else if (depth == 2)
-    hipLaunchKernelGGL(k_probe_groups<2>, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, gap, resleep, o);
+    hipLaunchKernelGGL(k_probe_groups<2>, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, gap, resleep,
+                       local, o);
   else
-    hipLaunchKernelGGL(k_probe_groups<3>, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, gap, resleep, o);
+    hipLaunchKernelGGL(k_probe_groups<3>, dim3(cu), dim3(PR_NT), PR_LDS, s, buf, (int)words, (int)rounds, gap, resleep,
+                       local, o);
   return hipGetLastError() == hipSuccess ? FL_OK : FL_E_LAUNCH;
 }
 

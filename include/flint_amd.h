@@ -258,7 +258,8 @@ int fl_sample_noalloc(const float* logits, int32_t rows, int32_t vocab, float te
  * resleep << 24: all workgroups, uncached memory, polled as the decode kernel polls (16-byte
  * groups of 4 words, the missing ones re-requested together) with depth (1..3) rounds of
  * requests in flight, the first rounds gap x 64 cycles apart, resleep x 64 cycles before a
- * re-request; words a multiple of 4.
+ * re-request; words a multiple of 4. mode 4: the workgroups of each XCD separately, polled as
+ * mode 3 with one round in flight.
  * out (device, uint64 [2 * grid]): per workgroup the 100 MHz-clock ticks of all rounds, then its
  * XCC_ID register | (1 << 32) if a wait timed out (0.5 s bound). *grid receives the number of
  * workgroups (the CU count). Stream-ordered; allocates its exchange buffers on the first call. */

@@ -50,7 +50,9 @@ def test_argument_errors_without_gpu():
     assert lib.fl_decode_step(None, None, None, 0, None, None, None, None) == -1
     # hand-off probe modes: kind 3 takes a depth of 1..3 and a word count divisible by 4
     g = ctypes.c_int32()
-    assert lib.fl_probe_handoff(4, 64, 10, p, ctypes.byref(g), None) == -1            # no kind 4
+    assert lib.fl_probe_handoff(5, 64, 10, p, ctypes.byref(g), None) == -1            # no kind 5
+    assert lib.fl_probe_handoff(4 | 1 << 8, 64, 10, p, ctypes.byref(g), None) == -1   # kind 4: no knobs
+    assert lib.fl_probe_handoff(4, 66, 10, p, ctypes.byref(g), None) == -1            # kind 4: 66 % 4
     assert lib.fl_probe_handoff(3, 64, 10, p, ctypes.byref(g), None) == -1            # depth 0
     assert lib.fl_probe_handoff(3 | 4 << 8, 64, 10, p, ctypes.byref(g), None) == -1   # depth 4
     assert lib.fl_probe_handoff(3 | 1 << 8, 66, 10, p, ctypes.byref(g), None) == -1   # 66 % 4

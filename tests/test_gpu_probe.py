@@ -12,7 +12,7 @@ from tests.helpers import log
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("mode", [0, 1, 2, 3 | 1 << 8, 3 | 2 << 8 | 8 << 16, 3 | 3 << 8 | 4 << 16 | 2 << 24])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3 | 1 << 8, 3 | 2 << 8 | 8 << 16, 3 | 3 << 8 | 4 << 16 | 2 << 24, 4])
 @pytest.mark.parametrize("words", [256, 2560])
 def test_probe_handoff_modes(dev, mode, words):
     from flint_amd import _lib
