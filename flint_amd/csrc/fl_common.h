@@ -206,22 +206,6 @@ __device__ __forceinline__ void dq32_mx(const uint4 w, uint32_t szw, const MxLan
   }
 }
 
-// dot of one 16-byte chunk (32 int4 elements of one 128-group) with 32 bf16 x values
-// (16 packed pairs), accumulated into acc.
-__device__ __forceinline__ float chunk_dot(const uint4 w, uint32_t szw, const uint4* x4, float acc) {
-  const uint4 x[4] = {x4[0], x4[1], x4[2], x4[3]};  // requested first: the dequantisation hides them
-  uint32_t d[4][4];
-  dq32(w, dq_const(szw), d);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    acc = dot2_bf16(d[0][i], x[i].x, acc);
-    acc = dot2_bf16(d[1][i], x[i].y, acc);
-    acc = dot2_bf16(d[2][i], x[i].z, acc);
-    acc = dot2_bf16(d[3][i], x[i].w, acc);
-  }
-  return acc;
-}
-
 // ---- the same on the tiled layout (fl_tile_int4): four rows of one column per lane ----------
 // Lane L's 16 bytes of a 1 KB unit (16 rows x one 128-group) hold rows 4p..4p+3, p = (L / 4) % 4,
 // at columns c + 16t, c = 4 (L / 16) + L % 4, t = 0..7 (tile t: words 0 / 1 rows 4p, 4p+1 at bits
@@ -286,8 +270,9 @@ __device__ __forceinline__ void unit_mma_t(const uint4 w, uint32_t szw, const Mx
   }
 }
 
-// chunk_dot through dq32_mx (same bits; the four lanes of every 4-lane block on one 128-group
-// of one row, all lanes together)
+// dot of one 16-byte chunk (32 int4 elements of one 128-group) with 32 bf16 x values (16 packed
+// pairs), accumulated into acc; the chunk dequantised by dq32_mx (the four lanes of every 4-lane
+// block on one 128-group of one row, all lanes together)
 __device__ __forceinline__ float chunk_dot_mx(const uint4 w, uint32_t szw, const uint4* x4, float acc) {
   const uint4 x[4] = {x4[0], x4[1], x4[2], x4[3]};
   uint32_t d[4][4];

@@ -61,8 +61,8 @@ __global__ __launch_bounds__(256) void k_quantize(const uint16_t* __restrict__ w
 
 // One thread per 16-byte chunk (4 packed words, 32 elements of one group): bf16 outputs through
 // the same dequantisation sequence the GEMVs use -- dq32 on the vector ALUs (MX = false: the
-// M <= 32 GEMM of this file and the verify tiles) or dq32_mx on the matrix cores (MX = true: the
-// M = 1 GEMVs of this file and the decode kernel's). Threads 4b..4b+3 hold the four chunks of one group (nchunks is a
+// M <= 32 GEMM of this file) or dq32_mx on the matrix cores (MX = true: the M = 1 GEMVs of this
+// file and the decode kernel's; the verify tiles run the tiled form, fl_dequant_int4_tiled's). Threads 4b..4b+3 hold the four chunks of one group (nchunks is a
 // multiple of 4), as dq32_mx needs; every thread runs it (past the end on the last chunk) so
 // that all lanes of a wave run the matrix-core steps together.
 template <bool MX>

@@ -186,7 +186,7 @@ __global__ __launch_bounds__(256) void k_dequant_tiled(const uint4* __restrict__
 // of seeded pseudo-random words in registers and recomputes them `iters` times against 8 token
 // rows in LDS -- k_verify's tile product at M = 8 with the weights already there. MODE 0: this
 // library's row layout, dequantised on the vector ALUs (dq32, four 16x16x32 MFMAs per 32 weights:
-// k_verify's tile_mma); MODE 1: the tiled layout, both exact fp32 steps on 4x4x4 MFMAs and the
+// the verify tiles' former product, and fl_gemm_int4's); MODE 1: the tiled layout, both exact fp32 steps on 4x4x4 MFMAs and the
 // dot on a 16x16x32 MFMA per two tiles (unit_mma_t over two tiles at a time); MODE 2: the same
 // with each step batched over the unit's 8 tiles (unit_mma_t<8>, the kernels' form);
 // MODES 3 / 4: M = 1 as the decode kernel computes it, one row-layout chunk per lane dotted with x

@@ -37,7 +37,8 @@ def quantize_int4(w, q=None, sz=None):
 
 def dequantize_int4(q, sz, matrix_cores=False):
     """Bit-exact bf16 [N, K] dequantisation through the kernels' own device routine: the vector-ALU
-    form (M = 1 GEMV kernels, verify tiles) or, with matrix_cores, the decode GEMVs' MFMA form."""
+    form (fl_gemm_int4's) or, with matrix_cores, the lane-by-lane MFMA form of the decode GEMVs and
+    fl_gemv_int4."""
     _check_dev(q, torch.int32, "q")
     _check_dev(sz, torch.int32, "sz")
     n, k = q.shape[0], q.shape[1] * 8

@@ -81,13 +81,13 @@ int fl_device_info(int32_t* num_cu, int32_t* decode_grid);
 int fl_quantize_int4(const uint16_t* w, uint32_t* q, uint32_t* sz,
                      int32_t n, int32_t k, void* stream);
 
-/* Bit-exact dequantisation to bf16 [N,K] on the vector ALUs, the device routine of the M = 1
- * GEMV kernels and the verify tiles.
+/* Bit-exact dequantisation to bf16 [N,K] on the vector ALUs, the device routine of
+ * fl_gemm_int4.
  * Replaces reference engine/quantize.py:138-162 group_dequantize_tensor(_from_qparams). */
 int fl_dequant_int4(const uint32_t* q, const uint32_t* sz, uint16_t* out,
                     int32_t n, int32_t k, void* stream);
 /* The same bits through the matrix-core form of the dequantisation that the decode kernel's
- * GEMVs run (both rounding steps as 4x4x4 MFMAs, lane by lane). Replaces reference
+ * GEMVs and fl_gemv_int4 run (both rounding steps as 4x4x4 MFMAs, lane by lane). Replaces reference
  * engine/quantize.py:138-162 as fl_dequant_int4 does; kept apart so that each form is checked. */
 int fl_dequant_int4_mx(const uint32_t* q, const uint32_t* sz, uint16_t* out,
                        int32_t n, int32_t k, void* stream);
