@@ -124,6 +124,15 @@ def test_verify_rejects_bad_arguments(dev):
     with pytest.raises(_lib.FlError) as e:
         eng.verify(toks[:4], 62)
     assert e.value.code == -2
+    # the verify tiles read the tiled copies: without them fl_verify refuses (FL_E_ARG), and the
+    # decode entry points, which read the row layout, still run
+    eng._cw.wgu_t = None
+    with pytest.raises(_lib.FlError) as e:
+        eng.verify(toks[:4], 0)
+    assert e.value.code == -1
+    out = torch.empty(1, dtype=torch.int32, device=dev)
+    eng.decode_step(toks[:1], 0, token_out=out)
+    eng.check()
 
 
 @pytest.mark.parametrize("name,pos", [("small", 40), ("small", 300), ("flint-3b-l1", 700)])
