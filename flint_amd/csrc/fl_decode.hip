@@ -1029,13 +1029,23 @@ __device__ void attention_phase(const DecodeParams& p, int l, uint32_t qtag, uin
   if (tid < 64) __builtin_amdgcn_s_setprio(1);
   if (tid < 64) {  // thread d: output dim d, waves merged in a fixed order
     const int d = tid;
+    // every wave's values are read before any is used: one LDS round trip instead of one per
+    // wave's output value (+0.7% tok/s at ctx 512, measured on one box)
     float M = -INFINITY, Ls = 0.0f, O = 0.0f;
-    for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, wpart[w * 66]);
+    float wmx[NWAVE], wls[NWAVE], wov[NWAVE];
+#pragma unroll
     for (int w = 0; w < NWAVE; ++w) {
-      const float* wp = wpart + w * 66;
-      const float e = (wp[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wp[0] - M);
-      Ls += wp[1] * e;
-      O += wp[2 + d] * e;
+      wmx[w] = wpart[w * 66];
+      wls[w] = wpart[w * 66 + 1];
+      wov[w] = wpart[w * 66 + 2 + d];
+    }
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, wmx[w]);
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) {
+      const float e = (wmx[w] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wmx[w] - M);
+      Ls += wls[w] * e;
+      O += wov[w] * e;
     }
     unsigned long long* hpart = p.part + (size_t)hq * MAX_SLICES * 66;
     if (sl > 0) {
@@ -1380,14 +1390,21 @@ __device__ void attention_gqa(const DecodeParams& p, int l, uint32_t qtag, uint3
   }
   lds_barrier();
   auto unit_word = [&](int j, int wd) {  // the unit's word wd of head row j, waves in order
+    float xm[NWAVE], xv[NWAVE];  // every wave's pair read before any is used
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) {
+      xm[w] = wp[(w * GQ_ROWS + j) * 66];
+      xv[w] = wp[(w * GQ_ROWS + j) * 66 + wd];
+    }
     float mm = -INFINITY;
-    for (int w = 0; w < NWAVE; ++w) mm = fmaxf(mm, wp[(w * GQ_ROWS + j) * 66]);
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) mm = fmaxf(mm, xm[w]);
     if (wd == 0) return mm;
     float val = 0.0f;
+#pragma unroll
     for (int w = 0; w < NWAVE; ++w) {
-      const float* x = wp + (w * GQ_ROWS + j) * 66;
-      const float e = (x[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(x[0] - mm);
-      val += x[wd] * e;
+      const float e = (xm[w] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(xm[w] - mm);
+      val += xv[w] * e;
     }
     return val;
   };
@@ -2461,12 +2478,20 @@ __device__ __forceinline__ void attn_tokens_pass(const DecodeParams& p, int pos,
     const int t = tid >> 6, d = tid & 63;
     const float* wt = wpart + t * NWAVE * 66;
     float M_ = -INFINITY, Ls = 0.0f, O = 0.0f;
-    for (int w = 0; w < NWAVE; ++w) M_ = fmaxf(M_, wt[w * 66]);
+    float wmx[NWAVE], wls[NWAVE], wov[NWAVE];  // all read before any is used, as in decode
+#pragma unroll
     for (int w = 0; w < NWAVE; ++w) {
-      const float* wp = wt + w * 66;
-      const float e = (wp[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wp[0] - M_);
-      Ls += wp[1] * e;
-      O += wp[2 + d] * e;
+      wmx[w] = wt[w * 66];
+      wls[w] = wt[w * 66 + 1];
+      wov[w] = wt[w * 66 + 2 + d];
+    }
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) M_ = fmaxf(M_, wmx[w]);
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) {
+      const float e = (wmx[w] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wmx[w] - M_);
+      Ls += wls[w] * e;
+      O += wov[w] * e;
     }
     st_coh_u16(p.vattn + (size_t)(m0 + mi0 + t) * p.D + hq * 64 + d, f2bf(O / Ls));
   }
