@@ -253,3 +253,40 @@ def test_exchange_clearing_keeps_results(dev, monkeypatch):
     _, lg2, _ = eng.verify(ref[40:45].to(dev), 45)
     assert torch.equal(lg2.cpu(), lg_ref)
     eng.check()
+
+
+def test_tags_over_a_full_period(dev):
+    """Every exchange word carries a 16-bit tag of its launch's epoch (5 per layer and launch,
+    kept mod 65535), and the exchange buffers are zeroed once per window of launches whose tags
+    are all distinct (fl_state_create). One decode step repeated (same token, same position, same
+    cache: the same inputs, so the same bits) for more launches than a tag period spans the
+    epoch's wrap and the periodic clears; verify launches in between (they advance the same epoch)
+    must repeat their first result too, and no wait may time out."""
+    args, _, eng, orc = make_pair("tiny", seed=8)
+    eng.setup_caches(1, 256)
+    orc.setup_caches(eng.max_seq_length)
+    pos = 100
+    fill_kv_random(eng, orc, pos, seed=9)
+    per = 5 * args.n_layer
+    n = 65535 // per + 150  # decode launches: past one full tag period
+    log(f"tag period: {65535 / per:.0f} launches of {per} epochs; {n} decode launches, verify every 64th")
+    V = args.vocab_size
+    lg = torch.empty(n, V, dtype=torch.float32, device=dev)
+    tok = torch.tensor([17], dtype=torch.int32, device=dev)
+    vtok = torch.tensor([17, 29], dtype=torch.int32, device=dev)
+    vl = []
+    for i in range(n):
+        eng.decode_step(tok, pos, logits=lg[i])
+        if i % 64 == 0:
+            vl.append(eng.verify(vtok, pos)[1])
+    eng.check()
+    same = (lg == lg[0]).all(dim=1)
+    bad = (~same).nonzero().flatten().tolist()
+    assert not bad, f"decode launches {bad[:8]} differ from the first"
+    for j, v in enumerate(vl):
+        assert torch.equal(v, vl[0]), f"verify launch {j} differs from the first"
+    # and the repeated step is still the oracle's step
+    lo, _ = orc.forward(torch.tensor([17]), pos)
+    ok, d, *_ = compare_logits(lg[0].cpu(), lo[0], "tiny")
+    log(f"  {n} decode + {len(vl)} verify launches repeat bit for bit; max|dlogit| vs oracle {d:.3e}")
+    assert ok
