@@ -12,7 +12,8 @@ oracle's own top-2 margin is within that bar (logged and counted).
 import pytest
 import torch
 
-from tests.helpers import compare_logits, fill_kv_random, log, logit_bar, make_pair, near_tie, top2_margin
+from tests.helpers import (check_rows, compare_logits, fill_kv_random, log, logit_bar, make_pair, near_tie,
+                           oracle_pair, top2_margin)
 
 pytestmark = pytest.mark.gpu
 
@@ -290,3 +291,32 @@ def test_tags_over_a_full_period(dev):
     ok, d, *_ = compare_logits(lg[0].cpu(), lo[0], "tiny")
     log(f"  {n} decode + {len(vl)} verify launches repeat bit for bit; max|dlogit| vs oracle {d:.3e}")
     assert ok
+
+
+def test_last_cache_slot(dev):
+    """The last slot of the cache: a decode step at pos = max_seq - 1 and a verify whose tokens end
+    exactly at max_seq match the oracle; one slot past either is refused (FL_E_POS) before any
+    launch."""
+    from flint_amd import _lib
+    args, _, eng, orc = make_pair("tiny", seed=12)
+    eng.setup_caches(1, 200)
+    S = eng.max_seq_length
+    orc.setup_caches(S)
+    fill_kv_random(eng, orc, S - 1, seed=13)
+    am_e, am_o, (ok, d, *_), lg, lo, *_ = _step_compare(eng, orc, 5, S - 1, "tiny")
+    log(f"decode at the last slot {S - 1}: max|dlogit| {d:.3e}, argmax {am_e} / oracle {am_o}")
+    assert ok and (am_e == am_o or near_tie(lo, logit_bar("tiny")))
+    with pytest.raises(_lib.FlError) as e:
+        eng.decode_step(torch.tensor([5], dtype=torch.int32, device=dev), S)
+    assert e.value.code == -2
+    m = 6
+    fill_kv_random(eng, orc, S - m, seed=14)
+    toks = torch.tensor([3, 9, 27, 81, 243, 729], dtype=torch.int32) % args.vocab_size
+    tout, lgv, _ = eng.verify(toks.to(dev), S - m)
+    eng.check()
+    (alt, _), (lov, _) = oracle_pair(orc, lambda: orc.forward(toks, S - m))
+    ties = check_rows(lgv.cpu(), lov.float(), alt.float(), "tiny", f"tiny verify at slots {S - m}..{S - 1}")
+    assert ties <= 1
+    with pytest.raises(_lib.FlError) as e:
+        eng.verify(toks.to(dev), S - m + 1)
+    assert e.value.code == -2
